@@ -1,0 +1,347 @@
+"""Float64 torch-CPU restatement of the reference MoE block -- TEST INFRASTRUCTURE ONLY.
+
+Follows ``resihp/runtime/moe.py`` (reference) function by function; each
+function cites the lines it restates.  The extensions the MI355X build adds
+are marked as such: SwiGLU experts, sigmoid scoring, always-on shared experts,
+a seeded (non-zero) initial expert bias, Gaussian weight init with a fixed std,
+and FP8 delayed scaling.  None of them changes the reference defaults.
+
+Every function takes a config object by duck typing (the attributes of
+``OracleConfig``), so tests can pass either ``OracleConfig`` or the product's
+``MoEConfig``.
+
+Parity status (what pins each function) is documented in DESIGN.md and
+checked in ``tests/test_oracle_moe.py``.
+"""
+
+from __future__ import annotations
+
+import math
+import zlib
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+_MASK64 = (1 << 64) - 1
+
+
+# --------------------------------------------------------------------------- seeds
+
+
+def splitmix64(x: int) -> int:
+    """SplitMix64 finaliser of ``x + golden gamma`` (resihp/state/rng_data.py:21-25)."""
+    x = (x + 0x9E3779B97F4A7C15) & _MASK64
+    x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & _MASK64
+    x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & _MASK64
+    return x ^ (x >> 31)
+
+
+def derive_seed(*parts: int) -> int:
+    """Fold the parts through splitmix64, keep 63 bits (resihp/state/rng_data.py:28-32)."""
+    h = 0
+    for p in parts:
+        h = splitmix64(h ^ (int(p) & _MASK64))
+    return h & ((1 << 63) - 1)
+
+
+def generator(*parts: int) -> torch.Generator:
+    """CPU generator seeded with ``derive_seed(*parts)`` (resihp/state/rng_data.py:35-38)."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(derive_seed(*parts))
+    return g
+
+
+# --------------------------------------------------------------------------- config
+
+
+@dataclass(frozen=True)
+class OracleConfig:
+    """Fields of ``MoEConfig`` (resihp/runtime/moe.py:28-39) plus the build's extensions."""
+
+    hidden: int = 8
+    ffn: int = 12
+    num_experts: int = 6
+    top_k: int = 2
+    tokens: int = 48
+    seed: int = 4321
+    dtype: torch.dtype = torch.float64
+    bias_update_rate: float = 0.0
+    act: str = "gelu"             # extension: "gelu" (reference) or "swiglu"
+    score: str = "softmax"        # extension: "softmax" (reference) or "sigmoid"
+    normalize: bool = True        # sigmoid gates divided by their sum over the selected k
+    gate_scale: float = 1.0
+    num_shared: int = 0           # extension: always-on shared experts (gate 1)
+    shared_ffn: int = 0
+    expert_bias: bool = False     # extension: keep a selection bias even when bias_update_rate == 0
+    bias_init_std: float = 0.0    # extension: seeded N(0, std) initial expert bias
+    init_std: float = 0.0         # extension: N(0, std) weights instead of N(0, 1/fan_in)
+    router_dtype: torch.dtype | None = None   # dtype of router weight / logits; None = dtype
+
+
+def router_dtype(cfg) -> torch.dtype:
+    rd = getattr(cfg, "router_dtype", None)
+    if rd is not None:
+        return rd
+    return torch.float64 if cfg.dtype == torch.float64 else torch.float32
+
+
+def has_bias(cfg) -> bool:
+    return bool(cfg.bias_update_rate) or bool(getattr(cfg, "expert_bias", False))
+
+
+def fc1_rows(cfg, ffn: int | None = None) -> int:
+    f = cfg.ffn if ffn is None else ffn
+    return 2 * f if cfg.act == "swiglu" else f
+
+
+def param_shapes(cfg) -> dict[str, tuple[tuple[int, ...], bool]]:
+    """Key -> (shape, trainable); the key set of resihp/runtime/moe.py:42-50.
+
+    SwiGLU experts keep the key ``experts.{e}.fc1.weight`` with ``2*ffn`` rows,
+    gate rows first, then up rows.  Shared experts use ``shared_experts.{s}.*``
+    keys, which ``expert_of`` (moe.py:53-54) maps to None, so they are replicated
+    like the router.
+    """
+    h, f, E = cfg.hidden, cfg.ffn, cfg.num_experts
+    out = {"router.weight": ((E, h), True)}
+    if has_bias(cfg):
+        out["router.expert_bias"] = ((E,), False)
+    for e in range(E):
+        out[f"experts.{e}.fc1.weight"] = ((fc1_rows(cfg), h), True)
+        out[f"experts.{e}.fc2.weight"] = ((h, f), True)
+    for s in range(getattr(cfg, "num_shared", 0)):
+        fs = cfg.shared_ffn or f
+        out[f"shared_experts.{s}.fc1.weight"] = ((fc1_rows(cfg, fs), h), True)
+        out[f"shared_experts.{s}.fc2.weight"] = ((h, fs), True)
+    return out
+
+
+def param_dtype(cfg, key: str) -> torch.dtype:
+    return router_dtype(cfg) if key.startswith("router.") else cfg.dtype
+
+
+def init_param(cfg, key: str, shape: tuple[int, ...], trainable: bool) -> torch.Tensor:
+    """resihp/runtime/moe.py:57-61: randn(gen(seed, crc32(key))) / sqrt(fan_in); buffers zero.
+
+    Values are drawn on the CPU in float64 when the parameter dtype is float64,
+    else in float32, and cast once.
+    """
+    dt = param_dtype(cfg, key)
+    gen_dt = torch.float64 if dt == torch.float64 else torch.float32
+    if not trainable:
+        std = getattr(cfg, "bias_init_std", 0.0)
+        if not std:
+            return torch.zeros(shape, dtype=dt)
+        g = generator(cfg.seed, zlib.crc32(key.encode()))
+        return (torch.randn(shape, generator=g, dtype=gen_dt) * std).to(dt)
+    g = generator(cfg.seed, zlib.crc32(key.encode()))
+    w = torch.randn(shape, generator=g, dtype=gen_dt)
+    std = getattr(cfg, "init_std", 0.0)
+    w = w * std if std else w / shape[-1] ** 0.5
+    return w.to(dt)
+
+
+def init_params(cfg) -> dict[str, torch.Tensor]:
+    return {k: init_param(cfg, k, s, tr) for k, (s, tr) in param_shapes(cfg).items()}
+
+
+def batch(cfg, iteration: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """resihp/runtime/moe.py:69-72: x ~ N(0,1) from gen(seed, it, 5); y = tanh(x @ teacher)."""
+    gen_dt = torch.float64 if cfg.dtype == torch.float64 else torch.float32
+    x = torch.randn(cfg.tokens, cfg.hidden, generator=generator(cfg.seed, iteration, 5), dtype=gen_dt)
+    teacher = torch.randn(cfg.hidden, cfg.hidden, generator=generator(cfg.seed, 3), dtype=gen_dt)
+    return x.to(cfg.dtype), torch.tanh(x @ teacher).to(cfg.dtype)
+
+
+# --------------------------------------------------------------------------- routing
+
+
+def select(keys: torch.Tensor, k: int) -> torch.Tensor:
+    """Top-k indices by descending key, ties to the lowest id, NaN ranked as -inf.
+
+    Replaces torch.topk's unspecified tie order (resihp/runtime/moe.py:77) with a
+    stable descending sort.
+    """
+    keys = torch.where(torch.isnan(keys), torch.full_like(keys, -math.inf), keys)
+    return torch.sort(keys, dim=-1, descending=True, stable=True).indices[..., :k]
+
+
+def gates_from_logits(cfg, logits: torch.Tensor, topi: torch.Tensor) -> torch.Tensor:
+    """Gates of the selected experts (resihp/runtime/moe.py:79 for softmax)."""
+    sel = logits.gather(-1, topi)
+    if cfg.score == "softmax":
+        g = torch.softmax(sel, dim=-1)
+    else:
+        s = torch.sigmoid(sel)
+        g = s / s.sum(-1, keepdim=True) if cfg.normalize else s
+    return g * cfg.gate_scale if cfg.gate_scale != 1.0 else g
+
+
+def route(cfg, x: torch.Tensor, router: torch.Tensor, bias: torch.Tensor | None = None,
+          topi: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """resihp/runtime/moe.py:75-79.  ``topi`` may be supplied to follow a given selection."""
+    logits = x.to(router.dtype) @ router.t()
+    if topi is None:
+        key = logits if cfg.score == "softmax" else torch.sigmoid(logits)
+        if bias is not None:
+            key = key + bias
+        topi = select(key.detach(), cfg.top_k)
+    return topi, gates_from_logits(cfg, logits, topi)
+
+
+def dispatch(topi: np.ndarray, E: int, e0: int = 0, e1: int | None = None, n_src: int = 1) -> dict[str, np.ndarray]:
+    """Counts and the stable expert-major permutation (resihp/runtime/moe.py:94,97,192,199-205).
+
+    On one device the reference order -- per expert, pairs ``(token, slot)`` in
+    ascending order -- is a stable argsort of the flat expert ids.
+    """
+    e1 = E if e1 is None else e1
+    flat = np.asarray(topi, np.int64).reshape(-1)
+    T = np.asarray(topi).shape[0]
+    valid = (flat >= 0) & (flat < E)
+    counts = np.zeros(E + 1, np.int64)
+    counts[:E] = np.bincount(flat[valid], minlength=E)
+    counts[E] = int((~valid).sum())
+    local = valid & (flat >= e0) & (flat < e1)
+    order = np.argsort(np.where(local, flat, E + 1), kind="stable")[: int(local.sum())]
+    pair_row = np.full(flat.shape, -1, np.int64)
+    pair_row[order] = np.arange(order.size)
+    offsets = np.concatenate([[0], np.cumsum(counts[e0:e1])])
+    base, rem = divmod(T, n_src)
+    bounds = [0]
+    for s in range(n_src):
+        bounds.append(bounds[-1] + base + (1 if s < rem else 0))
+    src_of_tok = np.searchsorted(np.asarray(bounds[1:]), np.arange(T), side="right")
+    src_counts = np.zeros((n_src, e1 - e0), np.int64)
+    tok = np.arange(flat.size) // np.asarray(topi).shape[1]
+    np.add.at(src_counts, (src_of_tok[tok[local]], flat[local] - e0), 1)
+    return {"counts": counts, "offsets": offsets, "src_counts": src_counts, "perm": order, "pair_row": pair_row}
+
+
+# --------------------------------------------------------------------------- experts
+
+
+def expert_ffn(x: torch.Tensor, fc1: torch.Tensor, fc2: torch.Tensor, act: str = "gelu") -> torch.Tensor:
+    """resihp/runtime/moe.py:82-83 (exact-erf GELU); SwiGLU extension: fc2(silu(x Wg^T) * (x Wu^T))."""
+    hpre = F.linear(x, fc1)
+    if act == "gelu":
+        return F.linear(F.gelu(hpre), fc2)
+    f = fc1.shape[0] // 2
+    return F.linear(F.silu(hpre[:, :f]) * hpre[:, f:], fc2)
+
+
+def token_loss(out: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """resihp/runtime/moe.py:86-87."""
+    return ((out - y) ** 2).mean(dim=-1).sum()
+
+
+def update_expert_bias(cfg, bias: torch.Tensor, loads: torch.Tensor) -> None:
+    """resihp/runtime/moe.py:64-66: bias += rate * sign(mean(load) - load)."""
+    with torch.no_grad():
+        bias.add_(cfg.bias_update_rate * torch.sign(loads.mean() - loads))
+
+
+def layer_forward(cfg, params: dict[str, torch.Tensor], x: torch.Tensor, topi: torch.Tensor | None = None,
+                  update_bias: bool = True) -> torch.Tensor:
+    """resihp/runtime/moe.py:90-101 (+ shared experts).
+
+    Combine order follows the reference: per expert in ascending id,
+    ``combined.index_add(rows, g * y)``, then ``x + combined``.  Shared experts
+    (extension) are added after the routed sum with gate 1.
+    """
+    bias = params.get("router.expert_bias")
+    topi, gates = route(cfg, x, params["router.weight"], bias, topi=topi)
+    gates = gates.to(x.dtype)
+    if bias is not None and update_bias and cfg.bias_update_rate:
+        update_expert_bias(cfg, bias, torch.bincount(topi.reshape(-1), minlength=cfg.num_experts).to(bias.dtype))
+    combined = torch.zeros_like(x)
+    for e in range(cfg.num_experts):
+        rows, slot = (topi == e).nonzero(as_tuple=True)
+        if rows.numel():
+            y = expert_ffn(x[rows], params[f"experts.{e}.fc1.weight"], params[f"experts.{e}.fc2.weight"], cfg.act)
+            combined = combined.index_add(0, rows, gates[rows, slot].unsqueeze(1) * y)
+    out = x + combined
+    for s in range(getattr(cfg, "num_shared", 0)):
+        out = out + expert_ffn(x, params[f"shared_experts.{s}.fc1.weight"], params[f"shared_experts.{s}.fc2.weight"],
+                               cfg.act)
+    return out
+
+
+# --------------------------------------------------------------------------- training
+
+
+class Adam:
+    """Name-keyed Adam, the update of torch.optim.Adam(foreach=False) (resihp/runtime/optim.py:15-46)."""
+
+    def __init__(self, params: dict[str, torch.nn.Parameter], lr: float = 1e-3, betas=(0.9, 0.999),
+                 eps: float = 1e-8, weight_decay: float = 0.0):
+        self.params = dict(params)
+        self.lr, self.betas, self.eps, self.weight_decay = lr, betas, eps, weight_decay
+        self.step_count = 0
+        self.state = {n: {"exp_avg": torch.zeros_like(p), "exp_avg_sq": torch.zeros_like(p)}
+                      for n, p in self.params.items()}
+
+    def zero_grad(self) -> None:
+        for p in self.params.values():
+            p.grad = None
+
+    @torch.no_grad()
+    def step(self) -> None:
+        self.step_count += 1
+        b1, b2 = self.betas
+        bc1 = 1 - b1 ** self.step_count
+        bc2_sqrt = math.sqrt(1 - b2 ** self.step_count)
+        for n, p in self.params.items():
+            g = p.grad if p.grad is not None else torch.zeros_like(p)
+            if self.weight_decay:
+                g = g.add(p, alpha=self.weight_decay)
+            s = self.state[n]
+            s["exp_avg"].lerp_(g, 1 - b1)
+            s["exp_avg_sq"].mul_(b2).addcmul_(g, g.conj(), value=1 - b2)
+            denom = (s["exp_avg_sq"].sqrt() / bc2_sqrt).add_(self.eps)
+            p.addcdiv_(s["exp_avg"], denom, value=-self.lr / bc1)
+
+
+def reference_train(cfg, iterations: int, lr: float = 1e-2):
+    """resihp/runtime/moe.py:104-119: Adam on token_loss / tokens, bias updated in-forward."""
+    shapes = param_shapes(cfg)
+    params = {k: torch.nn.Parameter(init_param(cfg, k, s, tr)) for k, (s, tr) in shapes.items() if tr}
+    buffers = {k: init_param(cfg, k, s, tr) for k, (s, tr) in shapes.items() if not tr}
+    opt = Adam(params, lr=lr)
+    losses = []
+    for it in range(iterations):
+        opt.zero_grad()
+        x, y = batch(cfg, it)
+        loss = token_loss(layer_forward(cfg, {**params, **buffers}, x), y)
+        (loss / cfg.tokens).backward()
+        opt.step()
+        losses.append(loss.item() / cfg.tokens)
+    return losses, {**{k: v.detach().clone() for k, v in params.items()}, **{k: v.clone() for k, v in buffers.items()}}
+
+
+# --------------------------------------------------------------------------- FP8 delayed scaling
+
+FP8_MAX = {"e4m3": 448.0, "e5m2": 57344.0}
+FP8_DTYPE = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+
+
+def amax_roll(history: torch.Tensor, amax: torch.Tensor) -> torch.Tensor:
+    """Newest-first history update (resihp/runtime/reference_model.py:215)."""
+    return torch.cat([amax.reshape(1).to(history.dtype), history[:-1]])
+
+
+def fp8_scale(history: torch.Tensor, fmt: str, margin: int = 0) -> float:
+    """Delayed scaling: scale = fp8_max / max(history) / 2**margin (1 when the history is all zero)."""
+    amax = float(history.max())
+    if not amax > 0.0 or not math.isfinite(amax):
+        return 1.0
+    return FP8_MAX[fmt] / amax / (2.0 ** margin)
+
+
+def quantize(x: torch.Tensor, scale: float, fmt: str) -> torch.Tensor:
+    """Saturating round-to-nearest-even cast of ``x * scale`` to OCP fp8, returned as float64 codes' values."""
+    m = FP8_MAX[fmt]
+    y = (x.to(torch.float32) * torch.tensor(scale, dtype=torch.float32)).clamp(-m, m)
+    return y.to(FP8_DTYPE[fmt]).to(torch.float64)
