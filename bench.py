@@ -1,0 +1,225 @@
+"""MoE-layer throughput benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload mixtral|...] [--no-cpu-baseline]
+
+One step is one forward + backward of the MoE layer over one batch of
+synthetic tokens at the Mixtral-8x7B layer shape (hidden 4096, 8 experts,
+ffn 14336 SwiGLU, top-2 softmax router in float32, 8192 tokens, bfloat16),
+with inputs and weights already resident in HBM.  Weights are random
+N(0, 0.02) of that architecture, drawn on the device; tokens are N(0, 1).
+
+Prints one JSON line: whole-job tokens/s, the grouped-GEMM roofline fraction
+(algorithmic FLOPs / the GEMM kernels' HIP-event time / dense bf16 peak),
+the permute/combine HBM fraction, a per-entry-point time breakdown, and the
+CPU baseline: the float64/float32 torch restatement of the reference layer
+(oracle/moe_ref.py) timed on this host's cores on a bounded token sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import pathlib
+import sys
+import time
+
+import torch
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0        # MI355X HBM3E
+
+WORKLOADS = {
+    # name: (tokens, hidden, ffn, experts, top_k, score, num_shared)
+    "mixtral": (8192, 4096, 14336, 8, 2, "softmax", 0),
+    "dsv2lite": (16384, 2048, 1408, 64, 6, "sigmoid", 2),
+}
+
+GEMM_CALLS = ("rhp_expert_fc1_fwd", "rhp_expert_fc2_fwd", "rhp_expert_fc2_bwd", "rhp_expert_fc1_bwd")
+
+
+def _package():
+    name = "resihp_megatron_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    pkg_dir = ROOT / "resihp-megatron_amd"
+    spec = importlib.util.spec_from_file_location(name, pkg_dir / "__init__.py",
+                                                  submodule_search_locations=[str(pkg_dir)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+class EventTimer:
+    """HIP events around every C-ABI call, on the stream the call enqueues on."""
+
+    def __init__(self):
+        self.pending: dict[str, list] = {}
+        self.pairs: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
+
+    def start(self, name, stream):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(stream)
+        self.pending.setdefault(name, []).append(ev)
+
+    def stop(self, name, stream):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(stream)
+        self.pairs.append((name, self.pending[name].pop(), ev))
+
+    def totals_ms(self) -> dict[str, tuple[float, int]]:
+        out: dict[str, tuple[float, int]] = {}
+        for name, a, b in self.pairs:
+            t, n = out.get(name, (0.0, 0))
+            out[name] = (t + a.elapsed_time(b), n + 1)
+        return out
+
+
+def build_workload(name: str, dev: torch.device):
+    T, h, f, E, k, score, S = WORKLOADS[name]
+    g = torch.Generator(device=dev).manual_seed(1234)
+
+    def randn(*shape, std=1.0, dtype=torch.bfloat16):
+        return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * std).to(dtype)
+
+    router = randn(E, h, std=0.02, dtype=torch.float32).requires_grad_(True)
+    fc1 = [randn(2 * f, h, std=0.02).requires_grad_(True) for _ in range(E)]
+    fc2 = [randn(h, f, std=0.02).requires_grad_(True) for _ in range(E)]
+    s1 = [randn(2 * f, h, std=0.02).requires_grad_(True) for _ in range(S)]
+    s2 = [randn(h, f, std=0.02).requires_grad_(True) for _ in range(S)]
+    bias = randn(E, std=0.1, dtype=torch.float32) if score == "sigmoid" else None
+    x = randn(T, h).requires_grad_(True)
+    dout = randn(T, h)
+    return dict(T=T, h=h, f=f, E=E, k=k, score=score, S=S, router=router, fc1=fc1, fc2=fc2, s1=s1, s2=s2,
+                bias=bias, x=x, dout=dout)
+
+
+def gpu_step(pkg, w, meta):
+    for p in (w["x"], w["router"], *w["fc1"], *w["fc2"], *w["s1"], *w["s2"]):
+        p.grad = None
+    out, _ = pkg.layer.moe_layer(meta, w["x"], w["router"], w["bias"], w["fc1"], w["fc2"], w["s1"], w["s2"])
+    out.backward(w["dout"])
+
+
+def cpu_baseline(name: str, sample_tokens: int, reps: int = 3) -> dict:
+    """The float32 CPU restatement of the reference layer (oracle), fwd + bwd on a token sample."""
+    if str(ROOT) not in sys.path:
+        sys.path.insert(0, str(ROOT))
+    from oracle import moe_ref as M
+
+    T, h, f, E, k, score, S = WORKLOADS[name]
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cfg = M.OracleConfig(hidden=h, ffn=f, num_experts=E, top_k=k, tokens=sample_tokens, act="swiglu", score=score,
+                         num_shared=S, shared_ffn=f if S else 0, dtype=torch.float32)
+    g = torch.Generator().manual_seed(5)
+    params = {}
+    for key, (shape, _) in M.param_shapes(cfg).items():
+        params[key] = torch.empty(shape, dtype=torch.float32).normal_(0.0, 0.02, generator=g).requires_grad_(True)
+    x = torch.randn(sample_tokens, h, generator=g).requires_grad_(True)
+    dout = torch.randn(sample_tokens, h, generator=g)
+    times = []
+    for i in range(reps + 1):
+        for p in (x, *params.values()):
+            p.grad = None
+        t0 = time.perf_counter()
+        M.layer_forward(cfg, params, x).backward(dout)
+        dt = time.perf_counter() - t0
+        if i:
+            times.append(dt)
+    med = sorted(times)[len(times) // 2]
+    return {"value": sample_tokens / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{sample_tokens} of {T} tokens, float32 torch CPU restatement of the reference layer, "
+                      f"fwd+bwd, median of {reps} after 1 warm-up; torch {torch.__version__}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="mixtral", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-sample", type=int, default=256)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs the MoE layer on one GPU; multi-GPU expert parallelism "
+                                   "(the all-to-all dispatch) is not part of it", "n_gpus": args.gpus}))
+        return 2
+    pkg = _package()
+    import importlib
+
+    importlib.import_module(f"{pkg.__name__}.layer")
+    kernels = importlib.import_module(f"{pkg.__name__}.kernels")
+    dev = torch.device("cuda:0")
+    w = build_workload(args.workload, dev)
+    T, h, f, E, k = w["T"], w["h"], w["f"], w["E"], w["k"]
+    meta = pkg.layer.LayerMeta(num_experts=E, top_k=k, ffn=f, act="swiglu", score=w["score"],
+                               num_shared=w["S"], shared_ffn=f if w["S"] else 0)
+    for _ in range(args.warmup):
+        gpu_step(pkg, w, meta)
+    torch.cuda.synchronize()
+
+    timer = EventTimer()
+    kernels.set_timer(timer)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        gpu_step(pkg, w, meta)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kernels.set_timer(None)
+
+    per = {name: (ms / args.steps, n // args.steps) for name, (ms, n) in timer.totals_ms().items()}
+    P = T * k
+    S = w["S"]
+    gemm_flops = 18.0 * (P + S * T) * h * f          # SwiGLU: fwd 6 P h f + bwd 12 P h f
+    gemm_ms = sum(per.get(n, (0.0, 0))[0] for n in GEMM_CALLS)
+    gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
+    s = 2  # bf16 bytes
+    row_bytes = {  # algorithmic HBM bytes per step of the row kernels (token-major permute)
+        "rhp_permute": T * h * s + P * h * s + 4 * P,
+        "rhp_combine": P * h * s + 2 * T * h * s + 8 * P + S * T * h * s,
+        "rhp_combine_bwd": T * h * s + 2 * P * h * s + 8 * P,
+        "rhp_token_bwd": 2 * T * h * s + P * h * s + 12 * P + S * T * h * s,
+    }
+    row_ms = sum(per.get(n, (0.0, 0))[0] for n in row_bytes)
+    row_gbps = sum(row_bytes.values()) / (row_ms * 1e-3) / 1e9 if row_ms else None
+    ms_step = elapsed * 1e3 / args.steps
+    result = {
+        "metric": "MoE-layer tokens/s fwd+bwd (Mixtral shape, 1 GPU)" if args.workload == "mixtral"
+        else f"MoE-layer tokens/s fwd+bwd ({args.workload}, 1 GPU)",
+        "value": T * args.steps / elapsed,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) tokens, random N(0,0.02) weights of the layer shape, drawn on device)",
+        "config": {"workload": f"{args.workload} MoE layer: tokens={T}, hidden={h}, ffn={f} SwiGLU, experts={E}, "
+                               f"top_k={k} {w['score']} router (fp32), shared experts={S}, bf16, fwd+bwd",
+                   "tokens": T, "hidden": h, "ffn": f, "experts": E, "top_k": k, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": gemm_tflops / PEAK_BF16_TFLOPS, "traffic": None,
+                     "kernel": "grouped expert GEMMs (fc1/fc2 fwd, dgrad, wgrad)",
+                     "algorithmic": f"18*P*h*f = {gemm_flops:.4g} FLOP per step, P = {P} routed pairs"},
+        "rows_roofline": {"bound": "hbm", "achieved": row_gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                          "frac": (row_gbps / PEAK_HBM_GBPS) if row_gbps else None,
+                          "kernel": "permute + combine + combine_bwd + token_bwd"},
+        "breakdown_ms": {n: round(v[0], 4) for n, v in sorted(per.items())},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.workload, args.cpu_sample)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,220 @@
+/*
+ * resihp_moe.h -- C ABI of the MI355X (gfx950) MoE expert-parallel layer hot path.
+ *
+ * Every entry point takes raw device pointers, element counts, dtype codes and
+ * a HIP stream, enqueues its kernels on that stream and returns 0 on success.
+ * On failure it returns a nonzero status, enqueues nothing, and
+ * rhp_last_error() returns a message for the calling thread.  The library
+ * never allocates or frees device memory: callers pass outputs and workspace.
+ * It keeps no state between calls, so calls are re-entrant; calls that write
+ * the same buffers must be ordered by the caller's stream.
+ *
+ * Reference interfaces replaced (Sullivan-24/ResiHP-Megatron):
+ *   route                  resihp/runtime/moe.py:75-79
+ *   bincount / dispatch    resihp/runtime/moe.py:94, 97, 192-207
+ *   gather                 resihp/runtime/moe.py:99, 212  (x[rows], x.index_select)
+ *   expert FFN             resihp/runtime/moe.py:82-83, 96-100, 213-223
+ *   combine + residual     resihp/runtime/moe.py:100-101, 225-226
+ *   backward               torch autograd of the above (moe.py:116; _AllToAll.backward :164-167)
+ *   expert-bias update     resihp/runtime/moe.py:64-66, 236-240
+ *
+ * Row layout: tokens are rows of a [T, h] row-major matrix.  Routed pairs are
+ * (token t, slot j) with flat index p = t*k + j.  A dispatch plan assigns every
+ * local pair a row r of the expert-contiguous ("permuted") buffers; the rows
+ * of local expert i are [offsets[i], offsets[i+1]).
+ */
+#ifndef RESIHP_MOE_H
+#define RESIHP_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RHP_ABI_VERSION 1
+#define RHP_MAX_GROUPS_PER_LAUNCH 64
+
+/* Element types. */
+enum { RHP_F64 = 0, RHP_F32 = 1, RHP_BF16 = 2, RHP_E4M3 = 3, RHP_E5M2 = 4 };
+/* Router scoring. */
+enum { RHP_SCORE_SOFTMAX = 0, RHP_SCORE_SIGMOID = 1 };
+/* Expert activation. */
+enum { RHP_ACT_GELU = 0, RHP_ACT_SWIGLU = 1 };
+
+int rhp_abi_version(void);
+
+/* Message of the last failing call on the calling thread ("" if none). */
+const char* rhp_last_error(void);
+
+/* ------------------------------------------------------------------ routing */
+
+/*
+ * Router logits, top-k selection and gates for T tokens.
+ * Replaces route() (resihp/runtime/moe.py:75-79):
+ *   logits = x @ router_w^T          x: [T,h] x_dtype (F64/F32/BF16)
+ *                                   router_w: [E,h] r_dtype (F64 iff x is F64, else F32)
+ *   topi   = top-k of (score(logits) + bias), descending, ties to the lowest id
+ *   gates  = softmax over the selected unbiased logits (score = SOFTMAX), or the
+ *            selected sigmoid scores, divided by their sum if normalize (SIGMOID),
+ *            times scale
+ * bias ([E], r_dtype) may be NULL.  Outputs: logits [T,E] r_dtype, topi [T,k]
+ * int32, gates [T,k] r_dtype.  The logits follow a fixed evaluation order
+ * (segments of min(256,h) elements, each one fused-multiply-add chain, summed
+ * left to right) so that results are reproducible bit for bit.
+ * Requires h % 8 == 0, h % min(256,h) == 0, 1 <= k <= min(E, 16), E <= 1024.
+ */
+int rhp_route(const void* x, int x_dtype, const void* router_w, int r_dtype, const void* bias, int64_t T,
+              int h, int E, int k, int score, int normalize, double scale, void* logits, int32_t* topi,
+              void* gates, hipStream_t stream);
+
+/* Workspace bytes rhp_dispatch needs for these sizes. */
+size_t rhp_dispatch_workspace_bytes(int64_t T, int k, int E, int n_src);
+
+/*
+ * Dispatch plan of the local experts [e0, e1).
+ * Replaces bincount (moe.py:94, 192) and the dispatch ordering (moe.py:97,
+ * 193-207 with one device: pairs sorted stably by expert, then by p).
+ *   counts[E+1]        pairs per expert for all E experts; counts[E] = ids outside [0,E)
+ *   offsets[L+1]       exclusive prefix of counts[e0..e1), L = e1 - e0
+ *   src_counts[n_src*L] local pairs per (source, local expert); the T tokens are
+ *                      split into n_src contiguous sources by even_split
+ *                      (resihp/utils/intervals.py:17-30)
+ *   perm[T*k]          perm[r] = p for local rows r < offsets[L]; the rest is untouched
+ *   pair_row[T*k]      row of pair p, or -1 if its expert is not local
+ * Bit-exact with any stable counting sort.  Requires 1 <= L <= 1024, E <= 1024.
+ */
+int rhp_dispatch(const int32_t* topi, int64_t T, int k, int E, int e0, int e1, int n_src, int32_t* counts,
+                 int32_t* offsets, int32_t* src_counts, int32_t* perm, int32_t* pair_row, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Aux-loss-free bias update: bias[e] += rate * sign(mean(counts) - counts[e]).
+ * Replaces update_expert_bias (moe.py:64-66).  bias: [E] r_dtype; counts: int32 [E].
+ */
+int rhp_update_expert_bias(void* bias, int r_dtype, const int32_t* counts, int E, double rate,
+                           hipStream_t stream);
+
+/* ---------------------------------------------------------- permute/combine */
+
+/*
+ * Permute tokens into expert-contiguous rows: xp[pair_row[t*k+j]] = x[t] for
+ * every local pair.  Replaces x.index_select(0, idx_i) (moe.py:212) / x[rows]
+ * (moe.py:99).  Each token row is read once and written to its k rows.
+ * dtype: F64 / F32 / BF16.
+ */
+int rhp_permute(const void* x, int dtype, int64_t T, int h, int k, const int32_t* pair_row, void* xp,
+                hipStream_t stream);
+
+/*
+ * Weighted unpermute + residual:
+ *   out[t] = x[t] + sum over local slots j, in ascending expert id, of gates[t,j] * y[pair_row[t*k+j]]
+ *            + sum_s shared_y[s][t]
+ * Replaces zeros.index_add(0, idx_i, gates[idx_i,idx_j] * back) and x + combined
+ * (moe.py:225-226; moe.py:100-101).  topi gives the ascending-id order.
+ * y, x, out, shared_y: dtype (F64/F32/BF16); gates: g_dtype (F64/F32).
+ * shared_y is a host array of n_shared (<= 8) device pointers; may be NULL if 0.
+ */
+int rhp_combine(const void* y, const void* x, const void* gates, int g_dtype, const int32_t* topi,
+                const int32_t* pair_row, const void* const* shared_y, int n_shared, int dtype, int64_t T, int h,
+                int k, void* out, hipStream_t stream);
+
+/*
+ * Backward of the weighted unpermute:
+ *   dy[pair_row[t*k+j]] = gates[t,j] * dout[t]
+ *   dgates[t,j]         = <dout[t], y[pair_row[t*k+j]]>   (0 for non-local slots)
+ * dgates has g_dtype.
+ */
+int rhp_combine_bwd(const void* dout, const void* y, const void* gates, int g_dtype, const int32_t* pair_row,
+                    int dtype, int64_t T, int h, int k, void* dy, void* dgates, hipStream_t stream);
+
+/*
+ * Router backward to the selected logits: dlogits_sel[t,j] = d loss / d logits[t, topi[t,j]]
+ * given dgates [T,k], the gates and logits of rhp_route (r_dtype), for the
+ * same score / normalize / scale.  Logits of unselected experts get no gradient
+ * (the selection is piecewise constant).
+ */
+int rhp_route_bwd(const void* dgates, const void* gates, const void* logits, const int32_t* topi, int r_dtype,
+                  int64_t T, int E, int k, int score, int normalize, double scale, void* dlogits_sel,
+                  hipStream_t stream);
+
+/*
+ * Token-side backward:
+ *   dx[t] = dout[t] + sum_j dxp[pair_row[t*k+j]] + sum_j dlogits_sel[t,j] * router_w[topi[t,j]]
+ *           + sum_s shared_dx[s][t]
+ * (residual + scatter-add of the permuted input gradient + router input gradient).
+ * dout, dxp, dx, shared_dx: dtype; dlogits_sel, router_w: r_dtype.
+ */
+int rhp_token_bwd(const void* dout, const void* dxp, const int32_t* pair_row, const void* dlogits_sel,
+                  const int32_t* topi, const void* router_w, int r_dtype, const void* const* shared_dx, int n_shared,
+                  int dtype, int64_t T, int h, int E, int k, void* dx, hipStream_t stream);
+
+/* Workspace bytes rhp_router_wgrad needs. */
+size_t rhp_router_wgrad_workspace_bytes(int64_t T, int h, int E, int k, int r_dtype);
+
+/*
+ * Router weight gradient dW[e,:] = sum over pairs p = t*k+j routed to e of
+ * dlogits_sel[p] * x[t,:].  perm / offsets are a dispatch plan over ALL E
+ * experts (e0 = 0, e1 = E); each expert's rows are summed in plan order in
+ * pieces of 256 rows, and the pieces are added in ascending order, so the
+ * result is deterministic.  Accumulation in r_dtype.  dw: [E,h] r_dtype.
+ */
+int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, const int32_t* offsets, const void* x,
+                     int x_dtype, int r_dtype, int64_t T, int h, int E, int k, void* dw, void* workspace,
+                     size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------- expert grouped GEMMs */
+
+/*
+ * The four grouped expert GEMMs of a SwiGLU or GELU FFN (moe.py:82-83 applied
+ * to every local expert at once; moe.py:96-100, 213-223).  Group g (a local
+ * expert) owns M_g = offsets[g+1] - offsets[g] rows.  Row buffers are passed
+ * as host arrays of G device pointers; with rows_from_offsets = 1 group g's
+ * rows start at row offsets[g] of its buffer (routed experts: every entry is
+ * the same permuted buffer), with 0 at row 0 (shared experts: one buffer per
+ * group).  offsets is a device array of G+1 int32; rows_cap >= offsets[G]
+ * bounds the launch.  Weights are per-group device pointers, so each expert
+ * keeps its own parameter tensor.
+ *
+ *   fc1 weight w1[g]: [F1, h] row-major, F1 = 2f (SwiGLU: gate rows, then up rows) or f (GELU)
+ *   fc2 weight w2[g]: [h, f]
+ *
+ * dtype: BF16 (MFMA path, needs h % 64 == 0 and f % 64 == 0), F32 or F64.
+ * Groups beyond RHP_MAX_GROUPS_PER_LAUNCH are split into several launches.
+ */
+
+/* hpre[r] = xp[r] @ w1^T  ([M_g, F1]);  act[r] = silu(gate) * up  or  gelu(hpre)  ([M_g, f]). */
+int rhp_expert_fc1_fwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,
+                       int h, int f, const void* const* xp, const void* const* w1, void* const* hpre,
+                       void* const* act_out, hipStream_t stream);
+
+/* y[r] = act[r] @ w2^T  ([M_g, h]). */
+int rhp_expert_fc2_fwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int h,
+                       int f, const void* const* act_in, const void* const* w2, void* const* y, hipStream_t stream);
+
+/*
+ * Backward through fc2 and the activation:
+ *   dact = dy @ w2;  dhpre = activation backward of dact at hpre  ([M_g, F1])
+ *   dw2[g] = dy_g^T @ act_g  ([h, f])      (written, not accumulated)
+ */
+int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,
+                       int h, int f, const void* const* dy, const void* const* act_in, const void* const* hpre,
+                       const void* const* w2, void* const* dhpre, void* const* dw2, hipStream_t stream);
+
+/*
+ * Backward through fc1:
+ *   dxp = dhpre @ w1  ([M_g, h]);   dw1[g] = dhpre_g^T @ xp_g  ([F1, h])   (written, not accumulated)
+ * dxp may be NULL to skip the input gradient.
+ */
+int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,
+                       int h, int f, const void* const* dhpre, const void* const* xp, const void* const* w1,
+                       void* const* dxp, void* const* dw1, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RESIHP_MOE_H */

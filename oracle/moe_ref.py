@@ -244,12 +244,14 @@ def update_expert_bias(cfg, bias: torch.Tensor, loads: torch.Tensor) -> None:
 
 
 def layer_forward(cfg, params: dict[str, torch.Tensor], x: torch.Tensor, topi: torch.Tensor | None = None,
-                  update_bias: bool = True) -> torch.Tensor:
+                  update_bias: bool = True, local: tuple[int, int] | None = None) -> torch.Tensor:
     """resihp/runtime/moe.py:90-101 (+ shared experts).
 
     Combine order follows the reference: per expert in ascending id,
     ``combined.index_add(rows, g * y)``, then ``x + combined``.  Shared experts
-    (extension) are added after the routed sum with gate 1.
+    (extension) are added after the routed sum with gate 1.  ``local = (e0, e1)``
+    keeps only the experts of that window (one device's expert-parallel share,
+    moe.py:213-223); their weights are the only expert weights needed.
     """
     bias = params.get("router.expert_bias")
     topi, gates = route(cfg, x, params["router.weight"], bias, topi=topi)
@@ -257,7 +259,8 @@ def layer_forward(cfg, params: dict[str, torch.Tensor], x: torch.Tensor, topi: t
     if bias is not None and update_bias and cfg.bias_update_rate:
         update_expert_bias(cfg, bias, torch.bincount(topi.reshape(-1), minlength=cfg.num_experts).to(bias.dtype))
     combined = torch.zeros_like(x)
-    for e in range(cfg.num_experts):
+    e_lo, e_hi = local if local is not None else (0, cfg.num_experts)
+    for e in range(e_lo, e_hi):
         rows, slot = (topi == e).nonzero(as_tuple=True)
         if rows.numel():
             y = expert_ffn(x[rows], params[f"experts.{e}.fc1.weight"], params[f"experts.{e}.fc2.weight"], cfg.act)

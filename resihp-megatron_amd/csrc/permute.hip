@@ -1,0 +1,525 @@
+// Row-movement kernels for gfx950: permute (token -> expert-contiguous rows),
+// weighted unpermute + residual (combine), their backward, the token-side
+// backward and the router weight gradient.
+//
+// Reference: resihp/runtime/moe.py:99-101 and :212, :225-226 (gather, combine),
+// with their torch-autograd backward.
+//
+// All of these are HBM-bound row copies/reductions: one wavefront owns one
+// token row at a time and moves it in 8-element chunks (16 B per lane for
+// bfloat16), so every access of a wave is one contiguous, fully coalesced
+// segment of a row.  Reductions over a token's k slots happen in registers;
+// nothing uses atomics, so every result is deterministic.
+#pragma clang fp contract(off)
+
+#include <algorithm>
+
+#include "rhp_common.h"
+
+namespace rhp {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxShared = 8;
+constexpr int kChunksPerIter = 4;   // 8-element chunks each lane keeps in flight
+
+// 8 consecutive elements of type S, held as compute type A.
+template <class S, class A> struct Vec8;
+template <> struct Vec8<bf16, float> {
+    __device__ __forceinline__ static void load(const bf16* p, float* v) {
+        const uint4 q = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+    __device__ __forceinline__ static void store(bf16* p, const float* v) {
+        uint4 q;
+        q.x = pack_bf16x2(v[0], v[1]);
+        q.y = pack_bf16x2(v[2], v[3]);
+        q.z = pack_bf16x2(v[4], v[5]);
+        q.w = pack_bf16x2(v[6], v[7]);
+        *reinterpret_cast<uint4*>(p) = q;
+    }
+};
+template <> struct Vec8<float, float> {
+    __device__ __forceinline__ static void load(const float* p, float* v) {
+        const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    __device__ __forceinline__ static void store(float* p, const float* v) {
+        reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+        reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+};
+template <> struct Vec8<double, double> {
+    __device__ __forceinline__ static void load(const double* p, double* v) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const double2 a = reinterpret_cast<const double2*>(p)[i];
+            v[2 * i] = a.x;
+            v[2 * i + 1] = a.y;
+        }
+    }
+    __device__ __forceinline__ static void store(double* p, const double* v) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) reinterpret_cast<double2*>(p)[i] = make_double2(v[2 * i], v[2 * i + 1]);
+    }
+};
+
+// Raw 8-element chunk (bit copy, no conversion).
+template <class S> struct Raw8 {
+    static constexpr int kWords = sizeof(S) * 8 / 16;   // 16-byte words per chunk
+    uint4 w[kWords];
+    __device__ __forceinline__ void load(const S* p) {
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) w[i] = reinterpret_cast<const uint4*>(p)[i];
+    }
+    __device__ __forceinline__ void store(S* p) const {
+#pragma unroll
+        for (int i = 0; i < kWords; ++i) reinterpret_cast<uint4*>(p)[i] = w[i];
+    }
+};
+
+struct SharedPtrs {
+    const void* p[kMaxShared];
+};
+
+// ----------------------------------------------------------------------------- permute
+
+template <class S>
+__global__ __launch_bounds__(kThreads) void permute_kernel(const S* __restrict__ x, int64_t T, int h, int k,
+                                                           const int32_t* __restrict__ pair_row, S* __restrict__ xp) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (t >= T) return;
+    int32_t rows[kMaxTopK];
+    bool any = false;
+    for (int j = 0; j < k; ++j) {
+        rows[j] = pair_row[t * k + j];
+        any |= rows[j] >= 0;
+    }
+    if (!any) return;
+    const int nch = h / 8;
+    const S* src = x + t * h;
+    for (int c0 = lane; c0 < nch; c0 += 64 * kChunksPerIter) {
+        Raw8<S> v[kChunksPerIter];
+#pragma unroll
+        for (int u = 0; u < kChunksPerIter; ++u)
+            if (c0 + u * 64 < nch) v[u].load(src + (c0 + u * 64) * 8);
+        for (int j = 0; j < k; ++j) {
+            if (rows[j] < 0) continue;
+            S* dst = xp + static_cast<int64_t>(rows[j]) * h;
+#pragma unroll
+            for (int u = 0; u < kChunksPerIter; ++u)
+                if (c0 + u * 64 < nch) v[u].store(dst + (c0 + u * 64) * 8);
+        }
+    }
+}
+
+// Slot order of a token by ascending expert id (ids of one token are distinct).
+__device__ __forceinline__ void ascending_slots(const int32_t* topi_t, int k, int* order) {
+    for (int j = 0; j < k; ++j) {
+        int rank = 0;
+        for (int i = 0; i < k; ++i) rank += (topi_t[i] < topi_t[j]) || (topi_t[i] == topi_t[j] && i < j);
+        order[rank] = j;
+    }
+}
+
+// ----------------------------------------------------------------------------- combine
+
+template <class S, class G>
+__global__ __launch_bounds__(kThreads) void combine_kernel(const S* __restrict__ y, const S* __restrict__ x,
+                                                           const G* __restrict__ gates,
+                                                           const int32_t* __restrict__ topi,
+                                                           const int32_t* __restrict__ pair_row, SharedPtrs shared,
+                                                           int n_shared, int64_t T, int h, int k,
+                                                           S* __restrict__ out) {
+    using A = typename Elem<S>::acc;
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (t >= T) return;
+    int order[kMaxTopK];
+    int32_t tk[kMaxTopK];
+    for (int j = 0; j < k; ++j) tk[j] = topi[t * k + j];
+    ascending_slots(tk, k, order);
+    int32_t rows[kMaxTopK];
+    A g[kMaxTopK];
+    for (int r = 0; r < k; ++r) {
+        const int j = order[r];
+        rows[r] = pair_row[t * k + j];
+        g[r] = static_cast<A>(gates[t * k + j]);
+    }
+    const int nch = h / 8;
+    for (int c = lane; c < nch; c += 64) {
+        A acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = A(0);
+        for (int r = 0; r < k; ++r) {
+            if (rows[r] < 0) continue;
+            A v[8];
+            Vec8<S, A>::load(y + static_cast<int64_t>(rows[r]) * h + c * 8, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + g[r] * v[i];
+        }
+        A xv[8];
+        Vec8<S, A>::load(x + t * h + c * 8, xv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = xv[i] + acc[i];
+        for (int s = 0; s < n_shared; ++s) {
+            A v[8];
+            Vec8<S, A>::load(static_cast<const S*>(shared.p[s]) + t * h + c * 8, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = xv[i] + v[i];
+        }
+        Vec8<S, A>::store(out + t * h + c * 8, xv);
+    }
+}
+
+template <class S, class G>
+__global__ __launch_bounds__(kThreads) void combine_bwd_kernel(const S* __restrict__ dout, const S* __restrict__ y,
+                                                               const G* __restrict__ gates,
+                                                               const int32_t* __restrict__ pair_row, int64_t T, int h,
+                                                               int k, S* __restrict__ dy, G* __restrict__ dgates) {
+    using A = typename Elem<S>::acc;
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (t >= T) return;
+    int32_t rows[kMaxTopK];
+    A g[kMaxTopK];
+    G dot[kMaxTopK];
+    for (int j = 0; j < k; ++j) {
+        rows[j] = pair_row[t * k + j];
+        g[j] = static_cast<A>(gates[t * k + j]);
+        dot[j] = G(0);
+    }
+    const int nch = h / 8;
+    for (int c = lane; c < nch; c += 64) {
+        A dv[8];
+        Vec8<S, A>::load(dout + t * h + c * 8, dv);
+        for (int j = 0; j < k; ++j) {
+            if (rows[j] < 0) continue;
+            const int64_t off = static_cast<int64_t>(rows[j]) * h + c * 8;
+            A yv[8], o[8];
+            Vec8<S, A>::load(y + off, yv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                o[i] = g[j] * dv[i];
+                dot[j] = dot[j] + static_cast<G>(dv[i]) * static_cast<G>(yv[i]);
+            }
+            Vec8<S, A>::store(dy + off, o);
+        }
+    }
+    // Lane partials -> one value per slot by a fixed butterfly.
+    for (int j = 0; j < k; ++j) {
+        G v = dot[j];
+        for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
+        if (lane == 0) dgates[t * k + j] = v;
+    }
+}
+
+// ----------------------------------------------------------------------------- token backward
+
+template <class S, class R>
+__global__ __launch_bounds__(kThreads) void token_bwd_kernel(const S* __restrict__ dout, const S* __restrict__ dxp,
+                                                             const int32_t* __restrict__ pair_row,
+                                                             const R* __restrict__ dl, const int32_t* __restrict__ topi,
+                                                             const R* __restrict__ router_w, SharedPtrs shared,
+                                                             int n_shared, int64_t T, int h, int E, int k,
+                                                             S* __restrict__ dx) {
+    using A = typename Elem<S>::acc;
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (t >= T) return;
+    int32_t rows[kMaxTopK], ex[kMaxTopK];
+    R d[kMaxTopK];
+    for (int j = 0; j < k; ++j) {
+        rows[j] = pair_row[t * k + j];
+        ex[j] = topi[t * k + j];
+        d[j] = dl ? dl[t * k + j] : R(0);
+    }
+    const int nch = h / 8;
+    for (int c = lane; c < nch; c += 64) {
+        A acc[8];
+        Vec8<S, A>::load(dout + t * h + c * 8, acc);
+        for (int j = 0; j < k; ++j) {
+            if (rows[j] < 0) continue;
+            A v[8];
+            Vec8<S, A>::load(dxp + static_cast<int64_t>(rows[j]) * h + c * 8, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+        }
+        if (dl) {
+            for (int j = 0; j < k; ++j) {
+                if (ex[j] < 0 || ex[j] >= E) continue;   // dropped id: no router row
+                R wv[8];
+                Vec8<R, R>::load(router_w + static_cast<int64_t>(ex[j]) * h + c * 8, wv);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[i] = acc[i] + static_cast<A>(d[j] * wv[i]);
+            }
+        }
+        for (int s = 0; s < n_shared; ++s) {
+            A v[8];
+            Vec8<S, A>::load(static_cast<const S*>(shared.p[s]) + t * h + c * 8, v);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+        }
+        Vec8<S, A>::store(dx + t * h + c * 8, acc);
+    }
+}
+
+// ----------------------------------------------------------------------------- router weight gradient
+
+constexpr int kWgradRows = 256;   // rows of one expert segment summed by one block
+constexpr int kWgradCols = 512;   // columns per block (64 lanes x 8)
+
+__device__ __forceinline__ int pieces_of(int n) { return (n + kWgradRows - 1) / kWgradRows; }
+
+// Piece b -> (expert, first row, last row) of the full-expert plan.
+__device__ __forceinline__ bool find_piece(const int32_t* offsets, int E, int b, int* e_out, int* r0, int* r1) {
+    for (int e = 0; e < E; ++e) {
+        const int n = offsets[e + 1] - offsets[e];
+        const int np = pieces_of(n);
+        if (b < np) {
+            *e_out = e;
+            *r0 = offsets[e] + b * kWgradRows;
+            *r1 = std::min(*r0 + kWgradRows, offsets[e + 1]);
+            return true;
+        }
+        b -= np;
+    }
+    return false;
+}
+
+template <class S, class R>
+__global__ __launch_bounds__(64) void router_wgrad_partial_kernel(const R* __restrict__ dl,
+                                                                  const int32_t* __restrict__ perm,
+                                                                  const int32_t* __restrict__ offsets,
+                                                                  const S* __restrict__ x, int h, int E, int k,
+                                                                  R* __restrict__ partial) {
+    int e, r0, r1;
+    if (!find_piece(offsets, E, blockIdx.x, &e, &r0, &r1)) return;
+    const int c = blockIdx.y * 64 + threadIdx.x;   // 8-element column chunk
+    if (c * 8 >= h) return;
+    R acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = R(0);
+    for (int r = r0; r < r1; ++r) {
+        const int p = perm[r];
+        const R d = dl[p];
+        typename Elem<S>::acc v[8];
+        Vec8<S, typename Elem<S>::acc>::load(x + static_cast<int64_t>(p / k) * h + c * 8, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = acc[i] + d * static_cast<R>(v[i]);
+    }
+    Vec8<R, R>::store(partial + static_cast<int64_t>(blockIdx.x) * h + c * 8, acc);
+}
+
+template <class R>
+__global__ __launch_bounds__(64) void router_wgrad_reduce_kernel(const R* __restrict__ partial,
+                                                                 const int32_t* __restrict__ offsets, int h, int E,
+                                                                 R* __restrict__ dw) {
+    const int e = blockIdx.x;
+    const int c = blockIdx.y * 64 + threadIdx.x;
+    if (c * 8 >= h) return;
+    int first = 0;
+    for (int i = 0; i < e; ++i) first += pieces_of(offsets[i + 1] - offsets[i]);
+    const int np = pieces_of(offsets[e + 1] - offsets[e]);
+    R acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = R(0);
+    for (int q = 0; q < np; ++q) {
+        R v[8];
+        Vec8<R, R>::load(partial + static_cast<int64_t>(first + q) * h + c * 8, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+    }
+    Vec8<R, R>::store(dw + static_cast<int64_t>(e) * h + c * 8, acc);
+}
+
+int64_t wgrad_pieces_bound(int64_t T, int k, int E) { return (T * k + kWgradRows - 1) / kWgradRows + E; }
+
+unsigned row_blocks(int64_t T) { return static_cast<unsigned>((T + kWaves - 1) / kWaves); }
+
+int check_rows(const char* fn, int dtype, int64_t T, int h, int k) {
+    if (T < 0 || h <= 0 || k < 1 || k > kMaxTopK) return fail(std::string(fn) + ": need T >= 0, h > 0, 1 <= k <= 16");
+    if (h % 8) return fail(std::string(fn) + ": h must be a multiple of 8");
+    if (dtype != RHP_F64 && dtype != RHP_F32 && dtype != RHP_BF16)
+        return fail(std::string(fn) + ": unsupported dtype " + dtype_name(dtype));
+    return 0;
+}
+
+}  // namespace
+}  // namespace rhp
+
+using namespace rhp;
+
+extern "C" int rhp_permute(const void* x, int dtype, int64_t T, int h, int k, const int32_t* pair_row, void* xp,
+                           hipStream_t stream) {
+    clear_error();
+    if (int rc = check_rows("rhp_permute", dtype, T, h, k)) return rc;
+    if (T == 0) return 0;
+    RHP_REQUIRE(x && pair_row && xp && aligned16(x) && aligned16(xp), "rhp_permute: null or unaligned pointer");
+    const dim3 grid(row_blocks(T)), block(kThreads);
+    if (dtype == RHP_BF16)
+        hipLaunchKernelGGL(permute_kernel<bf16>, grid, block, 0, stream, static_cast<const bf16*>(x), T, h, k, pair_row,
+                           static_cast<bf16*>(xp));
+    else if (dtype == RHP_F32)
+        hipLaunchKernelGGL(permute_kernel<float>, grid, block, 0, stream, static_cast<const float*>(x), T, h, k,
+                           pair_row, static_cast<float*>(xp));
+    else
+        hipLaunchKernelGGL(permute_kernel<double>, grid, block, 0, stream, static_cast<const double*>(x), T, h, k,
+                           pair_row, static_cast<double*>(xp));
+    return check_launch("permute_kernel");
+}
+
+extern "C" int rhp_combine(const void* y, const void* x, const void* gates, int g_dtype, const int32_t* topi,
+                           const int32_t* pair_row, const void* const* shared_y, int n_shared, int dtype, int64_t T,
+                           int h, int k, void* out, hipStream_t stream) {
+    clear_error();
+    if (int rc = check_rows("rhp_combine", dtype, T, h, k)) return rc;
+    RHP_REQUIRE(n_shared >= 0 && n_shared <= kMaxShared, "rhp_combine: at most 8 shared experts");
+    if (T == 0) return 0;
+    RHP_REQUIRE(x && gates && topi && pair_row && out && aligned16(x) && aligned16(out),
+                "rhp_combine: null or unaligned pointer");
+    RHP_REQUIRE(y == nullptr ? true : aligned16(y), "rhp_combine: y must be 16-byte aligned");
+    SharedPtrs sp{};
+    for (int s = 0; s < n_shared; ++s) {
+        RHP_REQUIRE(shared_y && shared_y[s] && aligned16(shared_y[s]), "rhp_combine: null or unaligned shared_y");
+        sp.p[s] = shared_y[s];
+    }
+    const dim3 grid(row_blocks(T)), block(kThreads);
+    if (dtype == RHP_F64) {
+        RHP_REQUIRE(g_dtype == RHP_F64, "rhp_combine: float64 rows need float64 gates");
+        hipLaunchKernelGGL((combine_kernel<double, double>), grid, block, 0, stream, static_cast<const double*>(y),
+                           static_cast<const double*>(x), static_cast<const double*>(gates), topi, pair_row, sp,
+                           n_shared, T, h, k, static_cast<double*>(out));
+    } else {
+        RHP_REQUIRE(g_dtype == RHP_F32, "rhp_combine: float32 / bfloat16 rows need float32 gates");
+        if (dtype == RHP_BF16)
+            hipLaunchKernelGGL((combine_kernel<bf16, float>), grid, block, 0, stream, static_cast<const bf16*>(y),
+                               static_cast<const bf16*>(x), static_cast<const float*>(gates), topi, pair_row, sp,
+                               n_shared, T, h, k, static_cast<bf16*>(out));
+        else
+            hipLaunchKernelGGL((combine_kernel<float, float>), grid, block, 0, stream, static_cast<const float*>(y),
+                               static_cast<const float*>(x), static_cast<const float*>(gates), topi, pair_row, sp,
+                               n_shared, T, h, k, static_cast<float*>(out));
+    }
+    return check_launch("combine_kernel");
+}
+
+extern "C" int rhp_combine_bwd(const void* dout, const void* y, const void* gates, int g_dtype,
+                               const int32_t* pair_row, int dtype, int64_t T, int h, int k, void* dy, void* dgates,
+                               hipStream_t stream) {
+    clear_error();
+    if (int rc = check_rows("rhp_combine_bwd", dtype, T, h, k)) return rc;
+    if (T == 0) return 0;
+    RHP_REQUIRE(dout && gates && pair_row && dgates && aligned16(dout), "rhp_combine_bwd: null or unaligned pointer");
+    RHP_REQUIRE((y == nullptr || aligned16(y)) && (dy == nullptr || aligned16(dy)),
+                "rhp_combine_bwd: y and dy must be 16-byte aligned");
+    const dim3 grid(row_blocks(T)), block(kThreads);
+    if (dtype == RHP_F64) {
+        RHP_REQUIRE(g_dtype == RHP_F64, "rhp_combine_bwd: float64 rows need float64 gates");
+        hipLaunchKernelGGL((combine_bwd_kernel<double, double>), grid, block, 0, stream,
+                           static_cast<const double*>(dout), static_cast<const double*>(y),
+                           static_cast<const double*>(gates), pair_row, T, h, k, static_cast<double*>(dy),
+                           static_cast<double*>(dgates));
+    } else {
+        RHP_REQUIRE(g_dtype == RHP_F32, "rhp_combine_bwd: float32 / bfloat16 rows need float32 gates");
+        if (dtype == RHP_BF16)
+            hipLaunchKernelGGL((combine_bwd_kernel<bf16, float>), grid, block, 0, stream,
+                               static_cast<const bf16*>(dout), static_cast<const bf16*>(y),
+                               static_cast<const float*>(gates), pair_row, T, h, k, static_cast<bf16*>(dy),
+                               static_cast<float*>(dgates));
+        else
+            hipLaunchKernelGGL((combine_bwd_kernel<float, float>), grid, block, 0, stream,
+                               static_cast<const float*>(dout), static_cast<const float*>(y),
+                               static_cast<const float*>(gates), pair_row, T, h, k, static_cast<float*>(dy),
+                               static_cast<float*>(dgates));
+    }
+    return check_launch("combine_bwd_kernel");
+}
+
+extern "C" int rhp_token_bwd(const void* dout, const void* dxp, const int32_t* pair_row, const void* dlogits_sel,
+                             const int32_t* topi, const void* router_w, int r_dtype, const void* const* shared_dx,
+                             int n_shared, int dtype, int64_t T, int h, int E, int k, void* dx, hipStream_t stream) {
+    clear_error();
+    if (int rc = check_rows("rhp_token_bwd", dtype, T, h, k)) return rc;
+    RHP_REQUIRE(E >= 1 && n_shared >= 0 && n_shared <= kMaxShared, "rhp_token_bwd: bad E or n_shared");
+    if (T == 0) return 0;
+    RHP_REQUIRE(dout && pair_row && topi && dx && aligned16(dout) && aligned16(dx),
+                "rhp_token_bwd: null or unaligned pointer");
+    RHP_REQUIRE(dxp == nullptr || aligned16(dxp), "rhp_token_bwd: dxp must be 16-byte aligned");
+    RHP_REQUIRE(dlogits_sel == nullptr || (router_w && aligned16(router_w)),
+                "rhp_token_bwd: router_w must be given (16-byte aligned) with dlogits_sel");
+    SharedPtrs sp{};
+    for (int s = 0; s < n_shared; ++s) {
+        RHP_REQUIRE(shared_dx && shared_dx[s] && aligned16(shared_dx[s]), "rhp_token_bwd: null or unaligned shared_dx");
+        sp.p[s] = shared_dx[s];
+    }
+    const dim3 grid(row_blocks(T)), block(kThreads);
+    if (dtype == RHP_F64) {
+        RHP_REQUIRE(r_dtype == RHP_F64, "rhp_token_bwd: float64 rows need a float64 router");
+        hipLaunchKernelGGL((token_bwd_kernel<double, double>), grid, block, 0, stream, static_cast<const double*>(dout),
+                           static_cast<const double*>(dxp), pair_row, static_cast<const double*>(dlogits_sel), topi,
+                           static_cast<const double*>(router_w), sp, n_shared, T, h, E, k, static_cast<double*>(dx));
+    } else {
+        RHP_REQUIRE(r_dtype == RHP_F32, "rhp_token_bwd: float32 / bfloat16 rows need a float32 router");
+        if (dtype == RHP_BF16)
+            hipLaunchKernelGGL((token_bwd_kernel<bf16, float>), grid, block, 0, stream, static_cast<const bf16*>(dout),
+                               static_cast<const bf16*>(dxp), pair_row, static_cast<const float*>(dlogits_sel), topi,
+                               static_cast<const float*>(router_w), sp, n_shared, T, h, E, k, static_cast<bf16*>(dx));
+        else
+            hipLaunchKernelGGL((token_bwd_kernel<float, float>), grid, block, 0, stream,
+                               static_cast<const float*>(dout), static_cast<const float*>(dxp), pair_row,
+                               static_cast<const float*>(dlogits_sel), topi, static_cast<const float*>(router_w), sp,
+                               n_shared, T, h, E, k, static_cast<float*>(dx));
+    }
+    return check_launch("token_bwd_kernel");
+}
+
+extern "C" size_t rhp_router_wgrad_workspace_bytes(int64_t T, int h, int E, int k, int r_dtype) {
+    if (T < 0 || h <= 0 || E <= 0 || k <= 0) return 0;
+    return static_cast<size_t>(wgrad_pieces_bound(T, k, E)) * h * (r_dtype == RHP_F64 ? 8 : 4);
+}
+
+extern "C" int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, const int32_t* offsets, const void* x,
+                                int x_dtype, int r_dtype, int64_t T, int h, int E, int k, void* dw, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    if (int rc = check_rows("rhp_router_wgrad", x_dtype, T, h, k)) return rc;
+    RHP_REQUIRE(E >= 1, "rhp_router_wgrad: E must be positive");
+    RHP_REQUIRE(workspace_bytes >= rhp_router_wgrad_workspace_bytes(T, h, E, k, r_dtype),
+                "rhp_router_wgrad: workspace smaller than rhp_router_wgrad_workspace_bytes()");
+    RHP_REQUIRE(offsets && dw && aligned16(dw) && (T == 0 || (dlogits_sel && perm && x && aligned16(x))) &&
+                    (workspace == nullptr ? workspace_bytes == 0 : aligned16(workspace)),
+                "rhp_router_wgrad: null or unaligned pointer");
+    const int64_t pieces = wgrad_pieces_bound(T, k, E);
+    const unsigned col_blocks = static_cast<unsigned>((h / 8 + 63) / 64);
+    if (x_dtype == RHP_F64) {
+        RHP_REQUIRE(r_dtype == RHP_F64, "rhp_router_wgrad: float64 x needs a float64 router");
+        hipLaunchKernelGGL((router_wgrad_partial_kernel<double, double>), dim3(pieces, col_blocks), dim3(64), 0, stream,
+                           static_cast<const double*>(dlogits_sel), perm, offsets, static_cast<const double*>(x), h,
+                           E, k, static_cast<double*>(workspace));
+        if (int rc = check_launch("router_wgrad_partial_kernel")) return rc;
+        hipLaunchKernelGGL(router_wgrad_reduce_kernel<double>, dim3(E, col_blocks), dim3(64), 0, stream,
+                           static_cast<const double*>(workspace), offsets, h, E, static_cast<double*>(dw));
+    } else {
+        RHP_REQUIRE(r_dtype == RHP_F32, "rhp_router_wgrad: float32 / bfloat16 x needs a float32 router");
+        if (x_dtype == RHP_BF16)
+            hipLaunchKernelGGL((router_wgrad_partial_kernel<bf16, float>), dim3(pieces, col_blocks), dim3(64), 0,
+                               stream, static_cast<const float*>(dlogits_sel), perm, offsets,
+                               static_cast<const bf16*>(x), h, E, k, static_cast<float*>(workspace));
+        else
+            hipLaunchKernelGGL((router_wgrad_partial_kernel<float, float>), dim3(pieces, col_blocks), dim3(64), 0,
+                               stream, static_cast<const float*>(dlogits_sel), perm, offsets,
+                               static_cast<const float*>(x), h, E, k, static_cast<float*>(workspace));
+        if (int rc = check_launch("router_wgrad_partial_kernel")) return rc;
+        hipLaunchKernelGGL(router_wgrad_reduce_kernel<float>, dim3(E, col_blocks), dim3(64), 0, stream,
+                           static_cast<const float*>(workspace), offsets, h, E, static_cast<float*>(dw));
+    }
+    return check_launch("router_wgrad_reduce_kernel");
+}

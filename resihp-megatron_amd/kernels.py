@@ -1,0 +1,349 @@
+"""Torch-facing wrappers of the gfx950 kernels.
+
+Each function checks shapes, dtypes and devices (the C ABI sees raw pointers
+only), allocates its outputs and workspace through PyTorch's caching
+allocator, and enqueues the kernels on the current HIP stream of the tensors'
+device.  Nothing here computes on the CPU; every entry point goes through
+``libresihp_moe.so``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _capi as C
+
+_DT = {torch.float64: C.F64, torch.float32: C.F32, torch.bfloat16: C.BF16}
+
+# Optional per-entry-point timer: an object with start(name, stream) / stop(name, stream)
+# that records HIP events around every C call (None = no events).
+_timer = None
+
+
+def set_timer(timer) -> None:
+    """Installs (or with None removes) the event timer used around each C call."""
+    global _timer
+    _timer = timer
+
+
+def _call(name: str, dev: torch.device, *args) -> None:
+    """Calls entry point ``name`` with ``args`` and the current stream of ``dev``."""
+    stream = torch.cuda.current_stream(dev)
+    with torch.cuda.device(dev):
+        if _timer is not None:
+            _timer.start(name, stream)
+        C.call(name, *args, stream.cuda_stream)
+        if _timer is not None:
+            _timer.stop(name, stream)
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise KernelArgumentError(f"unsupported dtype {t.dtype}") from None
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _need_cuda(*ts: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("MoE kernels need tensors on a HIP device (cuda:N); got a CPU tensor")
+        if not t.is_contiguous():
+            raise RuntimeError("MoE kernels need contiguous tensors")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+class KernelArgumentError(RuntimeError):
+    """Arguments the kernels cannot take.  A RuntimeError, like every failure of the layer, so the
+    resilient trainer (resihp/train/resilient_loop.py:28) treats it as it treats the reference's."""
+
+
+def _expect(cond: bool, msg: str) -> None:
+    if not cond:
+        raise KernelArgumentError(msg)
+
+
+def _rows_of(t: torch.Tensor, name: str, cols: int, dtype: torch.dtype) -> int:
+    _expect(t.dim() == 2 and t.shape[1] == cols, f"{name} must be [rows, {cols}], got {tuple(t.shape)}")
+    _expect(t.dtype == dtype, f"{name} has dtype {t.dtype}, expected {dtype}")
+    return t.shape[0]
+
+
+def _index(t: torch.Tensor, name: str, shape: tuple[int, ...]) -> None:
+    _expect(t.dtype == torch.int32 and tuple(t.shape) == shape, f"{name} must be int32 {shape}")
+
+
+def score_code(score: str) -> int:
+    return {"softmax": C.SCORE_SOFTMAX, "sigmoid": C.SCORE_SIGMOID}[score]
+
+
+def act_code(act: str) -> int:
+    return {"gelu": C.ACT_GELU, "swiglu": C.ACT_SWIGLU}[act]
+
+
+# ----------------------------------------------------------------------------- routing
+
+
+def route(x: torch.Tensor, router_w: torch.Tensor, bias: torch.Tensor | None, k: int, score: str = "softmax",
+          normalize: bool = True, scale: float = 1.0) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Router logits [T,E], top-k expert ids [T,k] (int32) and gates [T,k] (router dtype)."""
+    dev = _need_cuda(x, router_w, bias)
+    T, h = x.shape
+    E = router_w.shape[0]
+    _rows_of(router_w, "router_w", h, router_w.dtype)
+    _expect(bias is None or (bias.dtype == router_w.dtype and tuple(bias.shape) == (E,)),
+            "bias must match the router dtype and have one entry per expert")
+    logits = torch.empty(T, E, dtype=router_w.dtype, device=dev)
+    topi = torch.empty(T, k, dtype=torch.int32, device=dev)
+    gates = torch.empty(T, k, dtype=router_w.dtype, device=dev)
+    _call("rhp_route", dev, _ptr(x), dtype_code(x), _ptr(router_w), dtype_code(router_w), _ptr(bias), T, h, E, k,
+          score_code(score), int(normalize), float(scale), _ptr(logits), _ptr(topi), _ptr(gates))
+    return logits, topi, gates
+
+
+@dataclass
+class DispatchPlan:
+    """Dispatch plan of the local experts [e0, e1) (all int32 device tensors)."""
+
+    counts: torch.Tensor       # [E + 1]; counts[E] = ids outside [0, E)
+    offsets: torch.Tensor      # [L + 1]
+    src_counts: torch.Tensor   # [n_src, L]
+    perm: torch.Tensor         # [T * k]; rows [0, offsets[L]) valid
+    pair_row: torch.Tensor     # [T * k]; -1 for pairs of other experts
+    e0: int
+    e1: int
+
+
+def dispatch(topi: torch.Tensor, E: int, e0: int = 0, e1: int | None = None, n_src: int = 1) -> DispatchPlan:
+    dev = _need_cuda(topi)
+    _expect(topi.dtype == torch.int32 and topi.dim() == 2, "topi must be int32 [T, k]")
+    e1 = E if e1 is None else e1
+    T, k = topi.shape
+    L = e1 - e0
+    counts = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    offsets = torch.empty(L + 1, dtype=torch.int32, device=dev)
+    src_counts = torch.empty(n_src, L, dtype=torch.int32, device=dev)
+    perm = torch.empty(max(1, T * k), dtype=torch.int32, device=dev)
+    pair_row = torch.empty(max(1, T * k), dtype=torch.int32, device=dev)
+    ws_bytes = C.lib().rhp_dispatch_workspace_bytes(T, k, E, n_src)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _call("rhp_dispatch", dev, _ptr(topi), T, k, E, e0, e1, n_src, _ptr(counts), _ptr(offsets), _ptr(src_counts),
+          _ptr(perm), _ptr(pair_row), _ptr(ws), ws_bytes)
+    return DispatchPlan(counts, offsets, src_counts, perm[: T * k], pair_row[: T * k], e0, e1)
+
+
+def update_expert_bias(bias: torch.Tensor, counts: torch.Tensor, rate: float) -> None:
+    """bias += rate * sign(mean(counts) - counts), in place (counts: int32 [E])."""
+    dev = _need_cuda(bias, counts)
+    _expect(counts.dtype == torch.int32 and counts.numel() >= bias.numel(), "counts must be int32, one per expert")
+    _call("rhp_update_expert_bias", dev, _ptr(bias), dtype_code(bias), _ptr(counts), bias.shape[0], float(rate))
+
+
+def route_bwd(dgates: torch.Tensor, gates: torch.Tensor, logits: torch.Tensor, topi: torch.Tensor, score: str,
+              normalize: bool, scale: float) -> torch.Tensor:
+    """Gradient of the selected logits [T,k] from the gate gradient."""
+    dev = _need_cuda(dgates, gates, logits, topi)
+    T, k = topi.shape
+    _index(topi, "topi", (T, k))
+    _expect(logits.shape[0] == T, "logits must have one row per token")
+    for name, t in (("dgates", dgates), ("gates", gates)):
+        _expect(t.dtype == logits.dtype and tuple(t.shape) == (T, k), f"{name} must be {logits.dtype} [T, k]")
+    dl = torch.empty(T, k, dtype=logits.dtype, device=dev)
+    _call("rhp_route_bwd", dev, _ptr(dgates), _ptr(gates), _ptr(logits), _ptr(topi), dtype_code(logits), T,
+          logits.shape[1], k, score_code(score), int(normalize), float(scale), _ptr(dl))
+    return dl
+
+
+# ----------------------------------------------------------------------------- rows
+
+
+def permute(x: torch.Tensor, pair_row: torch.Tensor, k: int, rows: int) -> torch.Tensor:
+    """Expert-contiguous copy of the token rows: out[pair_row[t*k+j]] = x[t]."""
+    dev = _need_cuda(x, pair_row)
+    T, h = x.shape
+    _index(pair_row, "pair_row", (T * k,))
+    xp = torch.empty(rows, h, dtype=x.dtype, device=dev)
+    if rows == 0:
+        return xp
+    _call("rhp_permute", dev, _ptr(x), dtype_code(x), T, h, k, _ptr(pair_row), _ptr(xp))
+    return xp
+
+
+def combine(y: torch.Tensor, x: torch.Tensor, gates: torch.Tensor, topi: torch.Tensor, pair_row: torch.Tensor,
+            shared: list[torch.Tensor] = ()) -> torch.Tensor:
+    """out = x + sum of gate-weighted expert rows (ascending expert id) + shared expert rows."""
+    dev = _need_cuda(y, x, gates, topi, pair_row, *shared)
+    T, h = x.shape
+    k = topi.shape[1]
+    _index(topi, "topi", (T, k))
+    _index(pair_row, "pair_row", (T * k,))
+    _rows_of(y, "y", h, x.dtype)
+    _expect(tuple(gates.shape) == (T, k), "gates must be [T, k]")
+    for i, t in enumerate(shared):
+        _expect(_rows_of(t, f"shared[{i}]", h, x.dtype) == T, "shared outputs need one row per token")
+    out = torch.empty_like(x)
+    arr = C.ptr_array([s.data_ptr() for s in shared])
+    _call("rhp_combine", dev, _ptr(y), _ptr(x), _ptr(gates), dtype_code(gates), _ptr(topi), _ptr(pair_row), arr,
+          len(shared), dtype_code(x), T, h, k, _ptr(out))
+    return out
+
+
+def combine_bwd(dout: torch.Tensor, y: torch.Tensor, gates: torch.Tensor, pair_row: torch.Tensor,
+                rows: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(dy [rows,h] = gate * dout row, dgates [T,k] = <dout, y row>)."""
+    dev = _need_cuda(dout, y, gates, pair_row)
+    T, h = dout.shape
+    k = gates.shape[1]
+    _index(pair_row, "pair_row", (T * k,))
+    _expect(_rows_of(y, "y", h, dout.dtype) >= rows, "y has fewer rows than the plan")
+    dy = torch.empty(rows, h, dtype=dout.dtype, device=dev)
+    dgates = torch.empty_like(gates)
+    _call("rhp_combine_bwd", dev, _ptr(dout), _ptr(y), _ptr(gates), dtype_code(gates), _ptr(pair_row),
+          dtype_code(dout), T, h, k, _ptr(dy), _ptr(dgates))
+    return dy, dgates
+
+
+def token_bwd(dout: torch.Tensor, dxp: torch.Tensor | None, pair_row: torch.Tensor, dl: torch.Tensor | None,
+              topi: torch.Tensor, router_w: torch.Tensor, shared_dx: list[torch.Tensor] = ()) -> torch.Tensor:
+    """dx = dout + sum of the token's permuted-row gradients + router input gradient + shared gradients."""
+    dev = _need_cuda(dout, dxp, pair_row, dl, topi, router_w, *shared_dx)
+    T, h = dout.shape
+    k = topi.shape[1]
+    _index(topi, "topi", (T, k))
+    _index(pair_row, "pair_row", (T * k,))
+    _rows_of(router_w, "router_w", h, router_w.dtype)
+    if dxp is not None:
+        _rows_of(dxp, "dxp", h, dout.dtype)
+    _expect(dl is None or (dl.dtype == router_w.dtype and tuple(dl.shape) == (T, k)), "dl must be router dtype [T,k]")
+    for i, t in enumerate(shared_dx):
+        _expect(_rows_of(t, f"shared_dx[{i}]", h, dout.dtype) == T, "shared gradients need one row per token")
+    dx = torch.empty_like(dout)
+    arr = C.ptr_array([s.data_ptr() for s in shared_dx])
+    _call("rhp_token_bwd", dev, _ptr(dout), _ptr(dxp), _ptr(pair_row), _ptr(dl), _ptr(topi), _ptr(router_w),
+          dtype_code(router_w), arr, len(shared_dx), dtype_code(dout), T, h, router_w.shape[0], k, _ptr(dx))
+    return dx
+
+
+def router_wgrad(dl: torch.Tensor, perm: torch.Tensor, offsets: torch.Tensor, x: torch.Tensor, E: int,
+                 r_dtype: torch.dtype) -> torch.Tensor:
+    """dW[e] = sum over pairs routed to e of dl * x[token]; perm/offsets from a plan over all E experts."""
+    dev = _need_cuda(dl, perm, offsets, x)
+    T, h = x.shape
+    k = dl.shape[1]
+    _expect(dl.dtype == r_dtype and tuple(dl.shape) == (T, k), "dl must be router dtype [T, k]")
+    _index(offsets, "offsets", (E + 1,))
+    _expect(perm.dtype == torch.int32 and perm.numel() == T * k, "perm must be int32 [T * k] over all experts")
+    dw = torch.empty(E, h, dtype=r_dtype, device=dev)
+    rc = _DT[r_dtype]
+    ws_bytes = C.lib().rhp_router_wgrad_workspace_bytes(T, h, E, k, rc)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _call("rhp_router_wgrad", dev, _ptr(dl), _ptr(perm), _ptr(offsets), _ptr(x), dtype_code(x), rc, T, h, E, k,
+          _ptr(dw), _ptr(ws), ws_bytes)
+    return dw
+
+
+# ----------------------------------------------------------------------------- expert GEMMs
+
+
+def _arr(ts) -> object:
+    return C.ptr_array([t.data_ptr() for t in ts])
+
+
+def _check_groups(what: str, ts: list[torch.Tensor], G: int, dtype: torch.dtype, cols: int,
+                  rows: int | None = None, exact_shape: tuple[int, int] | None = None) -> None:
+    """Every group tensor must have the kernel's dtype and shape; the kernels cannot see either."""
+    _expect(len(ts) == G, f"{what}: expected {G} tensors, got {len(ts)}")
+    for i, t in enumerate(ts):
+        _expect(t.dtype == dtype, f"{what}[{i}] has dtype {t.dtype}, expected {dtype}")
+        _expect(t.dim() == 2, f"{what}[{i}] must be 2-D")
+        _expect(exact_shape is None or tuple(t.shape) == exact_shape,
+                f"{what}[{i}] has shape {tuple(t.shape)}, expected {exact_shape}")
+        _expect(t.shape[1] == cols, f"{what}[{i}] has {t.shape[1]} columns, expected {cols}")
+        _expect(rows is None or t.shape[0] >= rows, f"{what}[{i}] has {t.shape[0]} rows, fewer than {rows}")
+
+
+def _check_offsets(offsets: torch.Tensor, G: int) -> None:
+    _expect(offsets.dtype == torch.int32 and offsets.numel() == G + 1, f"offsets must be int32 with {G + 1} entries")
+
+
+def _shared_rows(rows_from_offsets: bool, rows_cap: int) -> int | None:
+    # Routed experts share one buffer indexed by the offsets: it must hold rows_cap rows.
+    return rows_cap if rows_from_offsets else None
+
+
+def expert_fc1_fwd(xs: list[torch.Tensor], offsets: torch.Tensor, rows_from_offsets: bool, rows_cap: int,
+                   w1: list[torch.Tensor], f: int, act: str, hpre: list[torch.Tensor],
+                   act_out: list[torch.Tensor]) -> None:
+    dev = _need_cuda(offsets, *xs, *w1, *hpre, *act_out)
+    G, dt, h = len(w1), w1[0].dtype, w1[0].shape[1]
+    F1 = 2 * f if act == "swiglu" else f
+    rows = _shared_rows(rows_from_offsets, rows_cap)
+    _check_offsets(offsets, G)
+    _check_groups("w1", w1, G, dt, h, exact_shape=(F1, h))
+    _check_groups("x", xs, G, dt, h, rows)
+    _check_groups("hpre", hpre, G, dt, F1, rows)
+    _check_groups("act", act_out, G, dt, f, rows)
+    _call("rhp_expert_fc1_fwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w1[0]),
+          act_code(act), h, f, _arr(xs), _arr(w1), _arr(hpre), _arr(act_out))
+
+
+def expert_fc2_fwd(acts: list[torch.Tensor], offsets: torch.Tensor, rows_from_offsets: bool, rows_cap: int,
+                   w2: list[torch.Tensor], ys: list[torch.Tensor]) -> None:
+    dev = _need_cuda(offsets, *acts, *w2, *ys)
+    G, dt, (h, f) = len(w2), w2[0].dtype, tuple(w2[0].shape)
+    rows = _shared_rows(rows_from_offsets, rows_cap)
+    _check_offsets(offsets, G)
+    _check_groups("w2", w2, G, dt, f, exact_shape=(h, f))
+    _check_groups("act", acts, G, dt, f, rows)
+    _check_groups("y", ys, G, dt, h, rows)
+    _call("rhp_expert_fc2_fwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w2[0]), h, f,
+          _arr(acts), _arr(w2), _arr(ys))
+
+
+def expert_fc2_bwd(dys: list[torch.Tensor], acts: list[torch.Tensor], hpres: list[torch.Tensor],
+                   offsets: torch.Tensor, rows_from_offsets: bool, rows_cap: int, w2: list[torch.Tensor], act: str,
+                   dhpre: list[torch.Tensor], dw2: list[torch.Tensor]) -> None:
+    dev = _need_cuda(offsets, *dys, *acts, *hpres, *w2, *dhpre, *dw2)
+    G, dt, (h, f) = len(w2), w2[0].dtype, tuple(w2[0].shape)
+    F1 = 2 * f if act == "swiglu" else f
+    rows = _shared_rows(rows_from_offsets, rows_cap)
+    _check_offsets(offsets, G)
+    _check_groups("w2", w2, G, dt, f, exact_shape=(h, f))
+    _check_groups("dw2", dw2, G, dt, f, exact_shape=(h, f))
+    _check_groups("dy", dys, G, dt, h, rows)
+    _check_groups("act", acts, G, dt, f, rows)
+    _check_groups("hpre", hpres, G, dt, F1, rows)
+    _check_groups("dhpre", dhpre, G, dt, F1, rows)
+    _call("rhp_expert_fc2_bwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w2[0]),
+          act_code(act), h, f, _arr(dys), _arr(acts), _arr(hpres), _arr(w2), _arr(dhpre), _arr(dw2))
+
+
+def expert_fc1_bwd(dhpre: list[torch.Tensor], xs: list[torch.Tensor], offsets: torch.Tensor,
+                   rows_from_offsets: bool, rows_cap: int, w1: list[torch.Tensor], f: int, act: str,
+                   dxs: list[torch.Tensor] | None, dw1: list[torch.Tensor]) -> None:
+    dev = _need_cuda(offsets, *dhpre, *xs, *w1, *(dxs or []), *dw1)
+    G, dt, h = len(w1), w1[0].dtype, w1[0].shape[1]
+    F1 = 2 * f if act == "swiglu" else f
+    rows = _shared_rows(rows_from_offsets, rows_cap)
+    _check_offsets(offsets, G)
+    _check_groups("w1", w1, G, dt, h, exact_shape=(F1, h))
+    _check_groups("dw1", dw1, G, dt, h, exact_shape=(F1, h))
+    _check_groups("dhpre", dhpre, G, dt, F1, rows)
+    _check_groups("x", xs, G, dt, h, rows)
+    if dxs:
+        _check_groups("dx", dxs, G, dt, h, rows)
+    _call("rhp_expert_fc1_bwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w1[0]),
+          act_code(act), h, f, _arr(dhpre), _arr(xs), _arr(w1), _arr(dxs) if dxs else None, _arr(dw1))

@@ -1,0 +1,151 @@
+"""The fused MoE layer: route -> dispatch -> permute -> grouped expert GEMMs -> combine, and its backward.
+
+One ``torch.autograd.Function`` drives the gfx950 kernels of
+``libresihp_moe.so``.  Its semantics are those of ``reference_forward``
+(resihp/runtime/moe.py:90-101) for the experts in the local window
+[e0, e1): ``out = x + sum over local slots of gate * expert(x) + sum of shared
+experts(x)``.  With the full window it is the whole layer; with a partial
+window it is one GPU's expert-parallel share with its tokens already received.
+
+Expert weights stay separate tensors (one per expert and matrix), so the
+autograd graph, the optimizer and expert re-placement see per-expert
+parameters exactly as in the reference; the kernels reach them through
+per-group pointers.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import kernels as K
+
+
+@dataclass(frozen=True)
+class LayerMeta:
+    num_experts: int
+    top_k: int
+    ffn: int
+    act: str = "gelu"
+    score: str = "softmax"
+    normalize: bool = True
+    gate_scale: float = 1.0
+    e0: int = 0
+    e1: int | None = None
+    n_src: int = 1
+    num_shared: int = 0
+    shared_ffn: int = 0
+
+    @property
+    def window(self) -> tuple[int, int]:
+        return self.e0, self.num_experts if self.e1 is None else self.e1
+
+    @property
+    def full(self) -> bool:
+        return self.window == (0, self.num_experts)
+
+
+def _fc1_rows(act: str, f: int) -> int:
+    return 2 * f if act == "swiglu" else f
+
+
+class _MoELayerFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, meta: LayerMeta, x, router_w, bias, *weights):
+        e0, e1 = meta.window
+        G = e1 - e0
+        S = meta.num_shared
+        fc1s, fc2s = list(weights[:G]), list(weights[G:2 * G])
+        sfc1s, sfc2s = list(weights[2 * G:2 * G + S]), list(weights[2 * G + S:2 * G + 2 * S])
+        T, h = x.shape
+        k, f = meta.top_k, meta.ffn
+        logits, topi, gates = K.route(x, router_w, bias, k, meta.score, meta.normalize, meta.gate_scale)
+        plan = K.dispatch(topi, meta.num_experts, e0, e1, meta.n_src)
+        # The reference materialises counts on the host here too (moe.py:210-211);
+        # with every expert local the row count is known without a sync.
+        P = T * k if meta.full else int(plan.offsets[-1].item())
+        F1 = _fc1_rows(meta.act, f)
+        xp = K.permute(x, plan.pair_row, k, P)
+        hpre = x.new_empty(P, F1)
+        act = x.new_empty(P, f)
+        y = x.new_empty(P, h)
+        if P > 0:
+            K.expert_fc1_fwd([xp] * G, plan.offsets, True, P, fc1s, f, meta.act, [hpre] * G, [act] * G)
+            K.expert_fc2_fwd([act] * G, plan.offsets, True, P, fc2s, [y] * G)
+        shared_off = shared_h = shared_a = shared_y = None
+        if S:
+            fs = meta.shared_ffn or f
+            shared_off = torch.arange(S + 1, dtype=torch.int32, device=x.device) * T
+            shared_h = [x.new_empty(T, _fc1_rows(meta.act, fs)) for _ in range(S)]
+            shared_a = [x.new_empty(T, fs) for _ in range(S)]
+            shared_y = [x.new_empty(T, h) for _ in range(S)]
+            if T > 0:
+                K.expert_fc1_fwd([x] * S, shared_off, False, T, sfc1s, fs, meta.act, shared_h, shared_a)
+                K.expert_fc2_fwd(shared_a, shared_off, False, T, sfc2s, shared_y)
+        out = K.combine(y, x, gates, topi, plan.pair_row, shared_y or [])
+        ctx.meta = meta
+        ctx.dims = (T, h, P, G, S)
+        ctx.save_for_backward(x, router_w, logits, topi, gates, plan.perm, plan.offsets, plan.pair_row, xp, hpre,
+                              act, y, *fc1s, *fc2s, *sfc1s, *sfc2s)
+        ctx.shared = (shared_off, shared_h, shared_a)
+        ctx.mark_non_differentiable(plan.counts)
+        return out, plan.counts
+
+    @staticmethod
+    def backward(ctx, dout, _dcounts):
+        meta = ctx.meta
+        T, h, P, G, S = ctx.dims
+        (x, router_w, logits, topi, gates, perm, offsets, pair_row, xp, hpre, act, y, *ws) = ctx.saved_tensors
+        fc1s, fc2s = ws[:G], ws[G:2 * G]
+        sfc1s, sfc2s = ws[2 * G:2 * G + S], ws[2 * G + S:]
+        shared_off, shared_h, shared_a = ctx.shared
+        f = meta.ffn
+        dout = dout.contiguous()
+        need_x = ctx.needs_input_grad[1]
+        dy, dgates = K.combine_bwd(dout, y, gates, pair_row, P)
+        dw2 = [torch.empty_like(w) for w in fc2s]
+        dw1 = [torch.empty_like(w) for w in fc1s]
+        dxp = x.new_empty(P, h) if need_x else None
+        if P > 0:
+            dhpre = x.new_empty(P, _fc1_rows(meta.act, f))
+            K.expert_fc2_bwd([dy] * G, [act] * G, [hpre] * G, offsets, True, P, fc2s, meta.act, [dhpre] * G, dw2)
+            K.expert_fc1_bwd([dhpre] * G, [xp] * G, offsets, True, P, fc1s, f, meta.act,
+                             [dxp] * G if need_x else None, dw1)
+        else:
+            for w in (*dw1, *dw2):
+                w.zero_()
+        sdw1 = [torch.empty_like(w) for w in sfc1s]
+        sdw2 = [torch.empty_like(w) for w in sfc2s]
+        shared_dx = []
+        if S and T > 0:
+            fs = meta.shared_ffn or f
+            dh = [x.new_empty(T, _fc1_rows(meta.act, fs)) for _ in range(S)]
+            K.expert_fc2_bwd([dout] * S, shared_a, shared_h, shared_off, False, T, list(sfc2s), meta.act, dh, sdw2)
+            shared_dx = [x.new_empty(T, h) for _ in range(S)] if need_x else []
+            K.expert_fc1_bwd(dh, [x] * S, shared_off, False, T, list(sfc1s), fs, meta.act, shared_dx or None, sdw1)
+        dl = K.route_bwd(dgates, gates, logits, topi, meta.score, meta.normalize, meta.gate_scale)
+        dx = K.token_bwd(dout, dxp, pair_row, dl, topi, router_w, shared_dx) if need_x else None
+        dwr = None
+        if ctx.needs_input_grad[2]:
+            if meta.full:
+                rperm, roff = perm, offsets
+            else:
+                full_plan = K.dispatch(topi, meta.num_experts)
+                rperm, roff = full_plan.perm, full_plan.offsets
+            dwr = K.router_wgrad(dl, rperm, roff, x, meta.num_experts, router_w.dtype)
+        return (None, dx, dwr, None, *dw1, *dw2, *sdw1, *sdw2)
+
+
+def moe_layer(meta: LayerMeta, x: torch.Tensor, router_w: torch.Tensor, bias: torch.Tensor | None,
+              fc1s: list[torch.Tensor], fc2s: list[torch.Tensor], shared_fc1s: list[torch.Tensor] = (),
+              shared_fc2s: list[torch.Tensor] = ()) -> tuple[torch.Tensor, torch.Tensor]:
+    """Layer output and the int32 per-expert counts (``counts[E]`` counts invalid ids)."""
+    e0, e1 = meta.window
+    if len(fc1s) != e1 - e0 or len(fc2s) != e1 - e0:
+        raise ValueError(f"need one fc1 and one fc2 weight per local expert ({e1 - e0})")
+    if len(shared_fc1s) != meta.num_shared or len(shared_fc2s) != meta.num_shared:
+        raise ValueError(f"need {meta.num_shared} shared expert weight pairs")
+    return _MoELayerFn.apply(meta, x.contiguous(), router_w.contiguous(),
+                             None if bias is None else bias.detach().contiguous(),
+                             *fc1s, *fc2s, *shared_fc1s, *shared_fc2s)

@@ -1,0 +1,137 @@
+"""Grouped expert GEMMs on the GPU against float64.
+
+Each entry point is checked in isolation: the float64 reference consumes
+exactly the (rounded) inputs the kernel consumed, so the bar is the output
+rounding of the storage type.  Cases cover the bfloat16 MFMA path (ragged and
+empty groups, partial tiles in every dimension, more groups than one launch
+takes, per-group buffers as used by shared experts) and the generic path
+(float32, float64, shapes the MFMA path does not take).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _helpers import DEV, rel_err, say, seeded
+from resihp_megatron_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+# Isolated-kernel bars: output rounding of the storage type (bf16 8 bits).
+BAR = {torch.bfloat16: 1e-2, torch.float32: 1e-5, torch.float64: 1e-12}
+
+CASES = [
+    # (name, dtype, h, f, counts)
+    ("bf16-ragged", torch.bfloat16, 512, 384, [300, 0, 17, 700, 1, 256]),
+    ("bf16-multi-tile", torch.bfloat16, 1024, 1024, [1024, 513]),
+    ("bf16-70-groups", torch.bfloat16, 128, 128, [(7 * i) % 41 for i in range(70)]),
+    ("bf16-generic-shape", torch.bfloat16, 40, 24, [9, 3, 0]),
+    ("f32", torch.float32, 64, 128, [33, 0, 100, 5]),
+    ("f64", torch.float64, 64, 128, [33, 0, 100, 5]),
+    ("f64-reference-default", torch.float64, 8, 12, [10, 20, 0, 18]),
+]
+
+
+def _act(act, hp, f):
+    if act == "swiglu":
+        return F.silu(hp[:, :f]) * hp[:, f:]
+    return F.gelu(hp)
+
+
+def _act_bwd(act, da, hp, f):
+    if act == "swiglu":
+        g, u = hp[:, :f], hp[:, f:]
+        s = torch.sigmoid(g)
+        return torch.cat([da * u * s * (1 + g * (1 - s)), da * g * s], 1)
+    phi = torch.exp(-0.5 * hp * hp) / (2 * torch.pi) ** 0.5
+    cdf = 0.5 * (1 + torch.erf(hp / 2 ** 0.5))
+    return da * (cdf + hp * phi)
+
+
+@pytest.mark.parametrize("act", ["swiglu", "gelu"])
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_grouped_expert_gemms(case, act):
+    name, dt, h, f, counts = case
+    G = len(counts)
+    F1 = 2 * f if act == "swiglu" else f
+    offs = torch.tensor([0] + list(torch.tensor(counts).cumsum(0).tolist()), dtype=torch.int32)
+    P = int(offs[-1])
+    xp = seeded((P, h), 1, 1.0, dt)
+    w1 = [seeded((F1, h), 10 + g, 0.05, dt) for g in range(G)]
+    w2 = [seeded((h, f), 100 + g, 0.05, dt) for g in range(G)]
+    d = lambda t: t.to(DEV)  # noqa: E731
+    xp_d, offs_d = d(xp), d(offs)
+    w1_d, w2_d = [d(w) for w in w1], [d(w) for w in w2]
+    say(f"gemm {name} {act}: G={G} P={P} h={h} f={f}")
+
+    hpre = torch.empty(P, F1, dtype=dt, device=DEV)
+    a = torch.empty(P, f, dtype=dt, device=DEV)
+    y = torch.empty(P, h, dtype=dt, device=DEV)
+    K.expert_fc1_fwd([xp_d] * G, offs_d, True, P, w1_d, f, act, [hpre] * G, [a] * G)
+    K.expert_fc2_fwd([a] * G, offs_d, True, P, w2_d, [y] * G)
+    dy = seeded((P, h), 2, 1.0, dt)
+    dhpre = torch.empty(P, F1, dtype=dt, device=DEV)
+    dw2 = [torch.empty_like(w) for w in w2_d]
+    K.expert_fc2_bwd([d(dy)] * G, [a] * G, [hpre] * G, offs_d, True, P, w2_d, act, [dhpre] * G, dw2)
+    dxp = torch.empty(P, h, dtype=dt, device=DEV)
+    dw1 = [torch.empty_like(w) for w in w1_d]
+    K.expert_fc1_bwd([dhpre] * G, [xp_d] * G, offs_d, True, P, w1_d, f, act, [dxp] * G, dw1)
+    torch.cuda.synchronize()
+
+    bar = BAR[dt]
+    c64 = lambda t: t.detach().cpu().double()  # noqa: E731
+    hp_g, a_g, dh_g = c64(hpre), c64(a), c64(dhpre)
+    for g in range(G):
+        r0, r1 = int(offs[g]), int(offs[g + 1])
+        xs = c64(xp[r0:r1])
+        ref_h = xs @ c64(w1[g]).t()
+        assert rel_err(hp_g[r0:r1], ref_h) <= bar, ("hpre", g)
+        assert rel_err(a_g[r0:r1], _act(act, ref_h, f)) <= bar, ("act", g)
+        ref_y = a_g[r0:r1] @ c64(w2[g]).t()
+        assert rel_err(c64(y)[r0:r1], ref_y) <= bar, ("y", g)
+        dys = c64(dy[r0:r1])
+        ref_dh = _act_bwd(act, dys @ c64(w2[g]), hp_g[r0:r1], f)
+        assert rel_err(dh_g[r0:r1], ref_dh) <= bar, ("dhpre", g)
+        assert rel_err(c64(dw2[g]), dys.t() @ a_g[r0:r1]) <= bar, ("dw2", g)
+        assert rel_err(c64(dxp)[r0:r1], dh_g[r0:r1] @ c64(w1[g])) <= bar, ("dxp", g)
+        assert rel_err(c64(dw1[g]), dh_g[r0:r1].t() @ xs) <= bar, ("dw1", g)
+
+
+def test_per_group_buffers_shared_expert_mode():
+    """rows_from_offsets = 0: each group reads its own buffer from row 0 (shared experts)."""
+    dt, h, f, T, S = torch.bfloat16, 256, 128, 200, 2
+    offs = torch.arange(S + 1, dtype=torch.int32) * T
+    xs = [seeded((T, h), 5 + s, 1.0, dt) for s in range(S)]
+    w1 = [seeded((2 * f, h), 50 + s, 0.05, dt) for s in range(S)]
+    w2 = [seeded((h, f), 60 + s, 0.05, dt) for s in range(S)]
+    say("gemm shared-expert buffers")
+    hs = [torch.empty(T, 2 * f, dtype=dt, device=DEV) for _ in range(S)]
+    as_ = [torch.empty(T, f, dtype=dt, device=DEV) for _ in range(S)]
+    ys = [torch.empty(T, h, dtype=dt, device=DEV) for _ in range(S)]
+    K.expert_fc1_fwd([x.to(DEV) for x in xs], offs.to(DEV), False, T, [w.to(DEV) for w in w1], f, "swiglu", hs, as_)
+    K.expert_fc2_fwd(as_, offs.to(DEV), False, T, [w.to(DEV) for w in w2], ys)
+    torch.cuda.synchronize()
+    for s in range(S):
+        ref = (F.silu(xs[s].double() @ w1[s].double()[:f].t()) * (xs[s].double() @ w1[s].double()[f:].t()))
+        assert rel_err(as_[s], ref) <= 1e-2
+        assert rel_err(ys[s], as_[s].cpu().double() @ w2[s].double().t()) <= 1e-2
+
+
+def test_gemm_deterministic():
+    dt, h, f = torch.bfloat16, 512, 256
+    counts = [400, 333]
+    offs = torch.tensor([0, 400, 733], dtype=torch.int32).to(DEV)
+    xp = seeded((733, h), 1, 1.0, dt).to(DEV)
+    w1 = [seeded((2 * f, h), 3 + g, 0.05, dt).to(DEV) for g in range(2)]
+    say("gemm determinism")
+    outs = []
+    for _ in range(2):
+        hp = torch.empty(733, 2 * f, dtype=dt, device=DEV)
+        a = torch.empty(733, f, dtype=dt, device=DEV)
+        K.expert_fc1_fwd([xp] * 2, offs, True, 733, w1, f, "swiglu", [hp] * 2, [a] * 2)
+        outs.append((hp, a))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert sum(counts) == 733

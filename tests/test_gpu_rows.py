@@ -1,0 +1,135 @@
+"""Row kernels (permute, combine, their backward, token backward, router weight gradient) on the GPU.
+
+Permute, combine, the combine input-gradient and the token backward are
+checked bit for bit against a numpy emulation that performs the same IEEE
+operations in the same order (the kernels are built without contraction);
+the two reductions (gate gradient, router weight gradient) against float64.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import DEV, rel_err, say, seeded
+from oracle import route_c as R
+from resihp_megatron_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.bfloat16, torch.float32, torch.float64]
+NP_ACC = {torch.bfloat16: np.float32, torch.float32: np.float32, torch.float64: np.float64}
+
+
+def _plan_inputs(T, k, E, e0, e1, seed):
+    g = torch.Generator().manual_seed(seed)
+    keys = torch.randn(T, E, generator=g)
+    topi = torch.sort(keys, dim=1, descending=True, stable=True).indices[:, :k].to(torch.int32)
+    ref = R.dispatch(topi.numpy(), E, e0, e1, 1)
+    return topi, ref
+
+
+def _to_np(t: torch.Tensor, acc) -> np.ndarray:
+    return t.detach().cpu().to(torch.float64 if acc is np.float64 else torch.float32).numpy()
+
+
+def _store(a: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+@pytest.mark.parametrize("window", [(0, 10), (3, 7)], ids=["all", "share"])
+def test_permute_combine_token_bwd_bit_exact(dtype, window):
+    T, h, k, E = 300, 256, 3, 10
+    e0, e1 = window
+    acc = NP_ACC[dtype]
+    gdt = torch.float64 if dtype == torch.float64 else torch.float32
+    topi, plan = _plan_inputs(T, k, E, e0, e1, 11)
+    P = int(plan["offsets"][-1])
+    x = seeded((T, h), 1, 1.0, dtype)
+    y = seeded((P, h), 2, 1.0, dtype)
+    gates = seeded((T, k), 3, 0.5, gdt).abs()
+    shared = [seeded((T, h), 4, 1.0, dtype)]
+    pair_row = torch.from_numpy(plan["pair_row"].astype(np.int32))
+    say(f"rows {dtype} window={window} T={T} h={h} k={k} P={P}")
+
+    xp = K.permute(x.to(DEV), pair_row.to(DEV), k, P)
+    out = K.combine(y.to(DEV), x.to(DEV), gates.to(DEV), topi.to(DEV), pair_row.to(DEV), [shared[0].to(DEV)])
+    torch.cuda.synchronize()
+
+    # permute: an exact row copy
+    ref_xp = torch.empty(P, h, dtype=dtype)
+    for p in range(T * k):
+        r = plan["pair_row"][p]
+        if r >= 0:
+            ref_xp[r] = x[p // k]
+    assert torch.equal(xp.cpu(), ref_xp)
+
+    # combine: acc = 0; acc += g * y in ascending expert id; out = x + acc + shared
+    xn, yn, gn, sn = _to_np(x, acc), _to_np(y, acc), gates.numpy().astype(acc), _to_np(shared[0], acc)
+    order = np.argsort(topi.numpy(), axis=1, kind="stable")
+    accum = np.zeros((T, h), acc)
+    rows = plan["pair_row"].reshape(T, k)
+    for rk in range(k):
+        j = order[:, rk]
+        r = rows[np.arange(T), j]
+        gj = gn[np.arange(T), j][:, None]
+        contrib = gj * yn[np.clip(r, 0, None)]
+        accum = np.where((r >= 0)[:, None], accum + contrib, accum)
+    ref_out = _store((xn + accum) + sn, dtype)
+    assert torch.equal(out.cpu(), ref_out)
+
+    # combine backward: dy = g * dout (exact); dgates = <dout, y> (reduction)
+    dout = seeded((T, h), 5, 1.0, dtype)
+    dy, dgates = K.combine_bwd(dout.to(DEV), y.to(DEV), gates.to(DEV), pair_row.to(DEV), P)
+    torch.cuda.synchronize()
+    dn = _to_np(dout, acc)
+    ref_dy = np.zeros((P, h), acc)
+    ref_dg = np.zeros((T, k))
+    for j in range(k):
+        r = rows[:, j]
+        m = r >= 0
+        ref_dy[r[m]] = gn[m, j][:, None] * dn[m]
+        ref_dg[m, j] = (dout[m].double() * y[r[m]].double()).sum(1).numpy()
+    assert torch.equal(dy.cpu(), _store(ref_dy, dtype))
+    assert rel_err(dgates, torch.from_numpy(ref_dg)) <= (1e-12 if dtype == torch.float64 else 1e-5)
+
+    # token backward: acc = dout; += dxp rows in slot order; += dl_j * w[topi_j]; += shared dx
+    dxp = seeded((P, h), 6, 1.0, dtype)
+    dl = seeded((T, k), 7, 0.3, gdt)
+    w = seeded((E, h), 8, 0.05, gdt)
+    sdx = [seeded((T, h), 9, 1.0, dtype)]
+    dx = K.token_bwd(dout.to(DEV), dxp.to(DEV), pair_row.to(DEV), dl.to(DEV), topi.to(DEV), w.to(DEV),
+                     [sdx[0].to(DEV)])
+    torch.cuda.synchronize()
+    a = dn.copy()
+    dxpn = _to_np(dxp, acc)
+    for j in range(k):
+        r = rows[:, j]
+        a = np.where((r >= 0)[:, None], a + dxpn[np.clip(r, 0, None)], a)
+    dln, wn = dl.numpy(), w.numpy()
+    for j in range(k):
+        a = a + (dln[:, j][:, None] * wn[topi.numpy()[:, j]]).astype(acc)
+    a = a + _to_np(sdx[0], acc)
+    assert torch.equal(dx.cpu(), _store(a, dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=str)
+def test_router_wgrad(dtype):
+    T, h, k, E = 700, 512, 4, 12
+    gdt = torch.float64 if dtype == torch.float64 else torch.float32
+    topi, plan = _plan_inputs(T, k, E, 0, E, 21)
+    x = seeded((T, h), 1, 1.0, dtype)
+    dl = seeded((T, k), 2, 0.3, gdt)
+    say(f"router wgrad {dtype}")
+    dw = K.router_wgrad(dl.to(DEV), torch.from_numpy(plan["perm"]).to(DEV),
+                        torch.from_numpy(plan["offsets"].astype(np.int32)).to(DEV), x.to(DEV), E, gdt)
+    torch.cuda.synchronize()
+    ref = torch.zeros(E, h, dtype=torch.float64)
+    ref.index_add_(0, topi.reshape(-1).long(), dl.reshape(-1, 1).double() * x.double().repeat_interleave(k, 0))
+    assert rel_err(dw, ref) <= (1e-12 if dtype == torch.float64 else 1e-5)
+    # deterministic: a second run gives the same bits
+    dw2 = K.router_wgrad(dl.to(DEV), torch.from_numpy(plan["perm"]).to(DEV),
+                         torch.from_numpy(plan["offsets"].astype(np.int32)).to(DEV), x.to(DEV), E, gdt)
+    assert torch.equal(dw, dw2)
