@@ -15,14 +15,13 @@
 // X tile, whose rows are the contiguous dimension of the output (n or i); the
 // "B" operand is the Y tile, whose rows are the output's row dimension (token
 // rows or o).  Each lane then holds 4 consecutive output columns, so stores are
-// 8-byte vectors along rows.  Both tiles live in LDS as [rows][64] bf16 with
-// 16-byte chunks XOR-swizzled by (row & 7); operands stored with K as the slow
-// dimension are transposed 8x8 in registers on their way into LDS.
+// 8-byte vectors along rows.  Operands whose K is the contiguous dimension are
+// read with ds_read_b128; operands stored with K as the slow dimension are read
+// with gfx950's transposing LDS load (details at the kernel).
 //
-// Work unit: a 256 x 256 output tile, 256 threads = 4 waves of 128 x 128
-// (4 x 4 MFMA tiles each), K step 64, two LDS stages (128 KiB).  Tiles are
-// ordered group-major, then by output column block, then by row block, and
-// block ids are remapped so each XCD runs a contiguous range of that order.
+// Work unit: a 256 x 256 output tile.  Tiles are ordered group-major, then by
+// output column block, then by row block, and block ids are remapped so each
+// XCD runs a contiguous range of that order.
 #include <algorithm>
 
 #include "rhp_common.h"
@@ -79,7 +78,6 @@ __device__ __forceinline__ double dgelu_f(double v) {
 // ------------------------------------------------------------------ tile scheduling
 
 constexpr int kTile = 256;   // output tile edge (X rows and Y rows)
-constexpr int kBK = 64;
 
 struct Tile {
     int g;
@@ -151,16 +149,60 @@ __device__ __forceinline__ bool find_tile(const Params& p, int xt_cols, int yt_r
 template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI == kEpiSwigluFwd ? 128 : 256; }
 
 // ------------------------------------------------------------------ MFMA kernel (bf16)
+//
+// A 256 x 256 output tile per workgroup of W waves (W = 4: one wave per SIMD,
+// 128 x 128 per wave, accumulators in AGPRs; W = 8: two waves per SIMD,
+// 128 x 64 per wave).  Wave w owns X rows [128 (w % 2), +128) and Y rows
+// [(256 / (W / 2)) (w / 2), +256 / (W / 2)).  K advances by the K step (64).
+//
+// Operands sit in LDS in their global layout, so the HBM -> LDS copy is a
+// plain 16-byte-vector copy:
+//   K-major tile  [256 rows][K step]  (64- or 144-byte rows) -> fragments by ds_read_b128
+//   MN-major tile [K step][256 rows]  (512-byte rows)         -> fragments by two
+//     ds_read_b64_tr_b16, which transpose 4 x 16 blocks across each 16-lane group
+// K-major rows are padded so that a 16-lane ds_read_b128 hits 16 distinct bank
+// slots.  MN-major rows keep 16-byte chunk c at position c ^ 4 (k & 3), so the
+// 8 k rows of one transposed read fall on distinct 64-byte bank groups.
+//
+// Pipeline: two LDS stages and two register staging sets.  Step kt computes
+// from one stage while the loads of step kt + 2 are in flight and the data of
+// step kt + 1 (loaded one step earlier) is written to the other stage.
+
+#ifndef RHP_GG_WAVES
+#define RHP_GG_WAVES 8
+#endif
+#ifndef RHP_GG_PREFETCH
+#define RHP_GG_PREFETCH 1
+#endif
+#ifndef RHP_GG_KSTEP
+#define RHP_GG_KSTEP 64
+#endif
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kThreadsMfma = 256;
-constexpr int kRowBytes = kBK * 2;                   // 128 B per LDS row
-constexpr int kTileBytes = kTile * kRowBytes;        // 32 KiB per operand tile
-constexpr int kStageBytes = 2 * kTileBytes;          // X + Y
+constexpr int kWaves = RHP_GG_WAVES;
+constexpr int kThreadsMfma = 64 * kWaves;
+constexpr int kKStep = RHP_GG_KSTEP;
+// K-major rows: 2 * kKStep bytes, padded to 144 bytes for kKStep = 64 so that
+// the 16 rows of one 16-lane fragment read land on 16 distinct 16-byte bank
+// slots (row * 9 mod 16 is a bijection); 64-byte rows need no padding.
+constexpr int kKPitch = kKStep == 64 ? 144 : 64;
+constexpr int kKChunks = kKStep / 8;                       // 16-byte chunks per K-major row
+constexpr int kTileBytes = kTile * kKPitch;               // also holds an MN-major tile (kKStep * 512)
+constexpr int kStageBytes = 2 * kTileBytes;                // X + Y
+constexpr int kChunks = kTile * kKStep * 2 / 16 / kThreadsMfma;   // 16-byte chunks per thread per operand
+constexpr int kWaveY = kTile / (kWaves / 2);               // Y rows per wave
+constexpr int kFragY = kWaveY / 32;                        // Y fragments per wave
+static_assert(kWaves == 4 || kWaves == 8, "4 or 8 waves per tile");
+static_assert(kKStep == 32 || kKStep == 64, "K step 32 or 64");
+static_assert(kTileBytes >= kKStep * 512, "an MN-major tile must fit");
 
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * kRowBytes + ((chunk ^ (row & 7)) << 4); }
+__device__ __forceinline__ int kmaj_off(int row, int chunk) { return row * kKPitch + chunk * 16; }
+__device__ __forceinline__ int mnmaj_off(int k, int mn) {
+    return k * 512 + (((mn >> 3) ^ ((k & 3) << 2)) << 4) + ((mn & 7) << 1);
+}
 
 // Raw buffer view of [base, base + bytes); loads beyond it return zeros.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
@@ -171,57 +213,93 @@ __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-// Selects the low (even row) or high (odd row) bfloat16 halves of two dwords.
-__device__ __forceinline__ uint32_t pick_halves(uint32_t a, uint32_t b, int odd) {
-    return __builtin_amdgcn_perm(b, a, odd ? 0x07060302u : 0x05040100u);
-}
-
-__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
-    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
-}
-
-// Registers holding one operand tile on its way from HBM to LDS.
+// One operand tile of one K step on its way from HBM to LDS.
 struct Stage {
-    uint4 v[8];
+    uint4 v[kChunks];
 };
 
-// K-contiguous operand: element (row, k) at byte (src_row(row) * ld + k) * 2.
-// Thread t loads 16-byte chunk (t % 8) of tile rows q * 32 + t / 8; voff[q]
-// holds the byte offset of that chunk at k = 0.
-__device__ __forceinline__ void load_kc(Stage& s, __amdgpu_buffer_rsrc_t r, const uint32_t* voff, int k0) {
+// Per-thread byte offsets of one operand, fixed for the whole K loop.
+//   gl[q]  global offset of the thread's q-th 16-byte chunk at k = 0
+//   st[q]  LDS offset (within a tile) the chunk is stored at
+//   fr[i]  LDS offset of the thread's part of fragment i at k16 block 0
+// K steps, stages, k16 blocks and the two halves of a transposed read only
+// add constants, which fold into the instructions' offset fields.
+struct OperandMap {
+    uint32_t gl[kChunks];
+    uint32_t st[kChunks];
+    uint32_t fr[4];
+    bool ok;   // MN-major: this thread's chunks lie inside the valid rows
+};
+
+// K-major operand ([rows][k], element (row, k) at (src_row(row) * ld + k) * 2).
+// Thread t copies chunk t % C of tile rows q * (threads / C) + t / C, C = kKChunks.
+template <class RowOf>
+__device__ __forceinline__ void map_kmaj(OperandMap& m, uint32_t ld, int frag_row0, int nfrag, RowOf src_row) {
+    const int t = threadIdx.x, L = t & 63;
+    const int c = t % kKChunks;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) s.v[q] = bload(r, voff[q], static_cast<uint32_t>(k0) * 2u);
-}
-__device__ __forceinline__ void store_kc(const Stage& s, uint8_t* tile) {
-    const int t = threadIdx.x;
+    for (int q = 0; q < kChunks; ++q) {
+        const int r = q * (kThreadsMfma / kKChunks) + t / kKChunks;
+        m.gl[q] = (static_cast<uint32_t>(src_row(r)) * ld + c * 8) * 2u;
+        m.st[q] = kmaj_off(r, c);
+    }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) *reinterpret_cast<uint4*>(tile + lds_off(q * 32 + (t >> 3), t & 7)) = s.v[q];
+    for (int i = 0; i < 4; ++i) m.fr[i] = i < nfrag ? kmaj_off(frag_row0 + i * 32 + (L & 31), L >> 5) : 0;
+    m.ok = true;
 }
 
-// K-strided operand: element (row, k) at byte (k * ld + row) * 2.  Thread t
-// owns the 8 x 8 block of tile rows (t / 8) * 8 and k (t % 8) * 8; voff is the
-// byte offset of its first element at k = 0, or ~0u (reads zero) when its rows
-// lie beyond the tile's valid rows.  ld_bytes * k must stay below 2^31.
-__device__ __forceinline__ void load_ks(Stage& s, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t ld_bytes, int k0) {
-    const uint32_t kb = threadIdx.x & 7;
+// MN-major operand ([k][rows], element (k, mn) at (k * ld + mn) * 2).  Thread t
+// copies chunk t % 32 (8 mn values) of k rows q * (threads / 32) + t / 32;
+// chunks at or beyond mn_lim read as zero.  Fragment lanes follow the
+// transposed-read pattern: lane r of 16-lane group g points at
+// k = 8 (g / 2) + r / 4 and mn = 16 (g % 2) + 4 (r % 4) of the fragment's rows.
+__device__ __forceinline__ void map_mnmaj(OperandMap& m, uint32_t ld, int mn0, int mn_lim, int frag_row0, int nfrag) {
+    const int t = threadIdx.x, L = t & 63;
+    const int c = t & 31;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-        s.v[kk] = voff == ~0u ? make_uint4(0, 0, 0, 0)
-                              : bload(r, voff, (static_cast<uint32_t>(k0) + kb * 8 + kk) * ld_bytes);
-}
-__device__ __forceinline__ void store_ks(const Stage& s, uint8_t* tile) {
-    const int t = threadIdx.x;
-    const int rb = t >> 3, kb = t & 7;
-#pragma unroll
-    for (int rr = 0; rr < 8; ++rr) {
-        uint4 o;
-        const int w = rr >> 1, odd = rr & 1;
-        o.x = pick_halves(word_of(s.v[0], w), word_of(s.v[1], w), odd);
-        o.y = pick_halves(word_of(s.v[2], w), word_of(s.v[3], w), odd);
-        o.z = pick_halves(word_of(s.v[4], w), word_of(s.v[5], w), odd);
-        o.w = pick_halves(word_of(s.v[6], w), word_of(s.v[7], w), odd);
-        *reinterpret_cast<uint4*>(tile + lds_off(rb * 8 + rr, kb)) = o;
+    for (int q = 0; q < kChunks; ++q) {
+        const int k = q * (kThreadsMfma / 32) + (t >> 5);
+        m.gl[q] = (static_cast<uint32_t>(k) * ld + static_cast<uint32_t>(mn0 + c * 8)) * 2u;
+        m.st[q] = mnmaj_off(k, c * 8);
     }
+    const int g = L >> 4, r = L & 15;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        m.fr[i] = i < nfrag ? mnmaj_off(8 * (g >> 1) + (r >> 2), frag_row0 + i * 32 + 16 * (g & 1) + 4 * (r & 3)) : 0;
+    m.ok = c * 8 < mn_lim;
+}
+
+__device__ __forceinline__ void load_kmaj(Stage& s, __amdgpu_buffer_rsrc_t r, const OperandMap& m, int k0) {
+    const uint32_t soff = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(k0) * 2u);
+#pragma unroll
+    for (int q = 0; q < kChunks; ++q) s.v[q] = bload(r, m.gl[q], soff);
+}
+// The K offset goes into the per-lane offset, which the buffer range check
+// covers, so rows past the view (a group's end) read as zero.
+__device__ __forceinline__ void load_mnmaj(Stage& s, __amdgpu_buffer_rsrc_t r, const OperandMap& m, uint32_t ld,
+                                           int k0) {
+    const uint32_t koff = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(k0) * ld * 2u);
+#pragma unroll
+    for (int q = 0; q < kChunks; ++q) s.v[q] = m.ok ? bload(r, m.gl[q] + koff, 0) : make_uint4(0, 0, 0, 0);
+}
+__device__ __forceinline__ void store_stage(const Stage& s, uint8_t* tile, const OperandMap& m) {
+#pragma unroll
+    for (int q = 0; q < kChunks; ++q) *reinterpret_cast<uint4*>(tile + m.st[q]) = s.v[q];
+}
+
+// v_mfma_f32_32x32x16_bf16 operand for 32 rows at k16 block kk: lane L holds row
+// L % 32 and k 8 (L / 32) .. +7.
+__device__ __forceinline__ bf16x8_t frag_kmaj(const uint8_t* tile, uint32_t fr, int kk) {
+    return *reinterpret_cast<const bf16x8_t*>(tile + fr + kk * 32);
+}
+// Two transposed reads, k rows kb .. kb + 3 and kb + 4 .. kb + 7 (512 B apart per k row).
+__device__ __forceinline__ bf16x8_t frag_mnmaj(const uint8_t* tile, uint32_t fr, int kk) {
+    typedef s16x4_t __attribute__((address_space(3))) * lds_v4;
+    const uint8_t* p = tile + fr + kk * 16 * 512;
+    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(p)));
+    const s16x4_t hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(p + 4 * 512)));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 __device__ __forceinline__ void store_bf16x4(uint16_t* p, float a, float b, float c, float d) {
@@ -243,142 +321,140 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
     __shared__ __align__(16) uint8_t lds[2 * kStageBytes];
     Tile t;
     if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
+    // The tile is the same for every lane; say so, so that pointers and buffer
+    // descriptors derived from it live in scalar registers.
+    t.g = __builtin_amdgcn_readfirstlane(t.g);
+    t.x0 = __builtin_amdgcn_readfirstlane(t.x0);
+    t.x_lim = __builtin_amdgcn_readfirstlane(t.x_lim);
+    t.y0 = __builtin_amdgcn_readfirstlane(t.y0);
+    t.y_lim = __builtin_amdgcn_readfirstlane(t.y_lim);
+    t.row0 = __builtin_amdgcn_readfirstlane(static_cast<int>(t.row0));
+    t.k_begin = __builtin_amdgcn_readfirstlane(t.k_begin);
+    t.k_end = __builtin_amdgcn_readfirstlane(t.k_end);
     const int g = t.g;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wx = wave & 1, wy = wave >> 1;
+    // X is K-major for FWD (weights [N, K]) and MN-major otherwise; Y is K-major
+    // except for WGRAD.
+    constexpr bool kXK = MODE == kFwd;
+    constexpr bool kYK = MODE != kWgrad;
 
-    // Buffer views and per-thread offsets of the two operands.
-    //   FWD:   X = W rows (K-contiguous), Y = A rows (K-contiguous)
-    //   DGRAD: X = W^T (W is [K, N], K-strided), Y = A rows (K-contiguous)
-    //   WGRAD: X = V^T, Y = G^T (both [rows, *], K-strided)
     const uint16_t* A = static_cast<const uint16_t*>(p.a[g]);
     const uint16_t* B = static_cast<const uint16_t*>(p.b[g]);
+    const uint32_t ldb = static_cast<uint32_t>(p.ldb), lda = static_cast<uint32_t>(p.lda);
     __amdgpu_buffer_rsrc_t rx, ry;
-    uint32_t voff_x[8], voff_y[8];
-    uint32_t ks_x = 0, ks_y = 0;
+    OperandMap mx, my;
     if (MODE == kWgrad) {
         const int64_t rows = t.k_end;   // group rows; reads past them return zero
         rx = make_rsrc(B + t.row0 * p.ldb, rows * p.ldb * 2);
         ry = make_rsrc(A + t.row0 * p.lda, rows * p.lda * 2);
-        const int rb = tid >> 3;
-        ks_x = (rb * 8 < t.x_lim) ? static_cast<uint32_t>(t.x0 + rb * 8) * 2u : ~0u;
-        ks_y = (rb * 8 < t.y_lim) ? static_cast<uint32_t>(t.y0 + rb * 8) * 2u : ~0u;
+        map_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
+        map_mnmaj(my, lda, t.y0, t.y_lim, wy * kWaveY, kFragY);
     } else {
-        const int64_t my_rows = t.y_lim;
-        ry = make_rsrc(A + (t.row0 + t.y0) * p.lda, my_rows * p.lda * 2);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int r = q * 32 + (tid >> 3);
-            const int m = r < t.y_lim ? r : t.y_lim - 1;
-            voff_y[q] = (static_cast<uint32_t>(m) * p.lda + (tid & 7) * 8) * 2u;
-        }
+        ry = make_rsrc(A + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda * 2);
+        const int y_last = t.y_lim - 1;
+        map_kmaj(my, lda, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
         if (MODE == kFwd) {
             rx = make_rsrc(B, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb * 2);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int r = q * 32 + (tid >> 3);
-                int src;
+            map_kmaj(mx, ldb, wx * 128, 4, [&](int r) {
                 if (EPI == kEpiSwigluFwd) {
+                    // 256 weight rows = [gate 64 | up 64] for each half of 128 activation columns.
                     const int half = r >> 7, qq = r & 127;
                     int col = t.x0 + half * 64 + (qq & 63);
                     col = col < p.f ? col : 0;
-                    src = qq < 64 ? col : p.f + col;
-                } else {
-                    const int n = t.x0 + r;
-                    src = n < p.N ? n : 0;
+                    return qq < 64 ? col : p.f + col;
                 }
-                voff_x[q] = (static_cast<uint32_t>(src) * p.ldb + (tid & 7) * 8) * 2u;
-            }
+                const int n = t.x0 + r;
+                return n < p.N ? n : 0;
+            });
         } else {
             rx = make_rsrc(B, static_cast<int64_t>(p.K) * p.ldb * 2);
-            const int rb = tid >> 3;
-            ks_x = (rb * 8 < t.x_lim) ? static_cast<uint32_t>(t.x0 + rb * 8) * 2u : ~0u;
+            map_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
         }
     }
-    const uint32_t ldbx = static_cast<uint32_t>(p.ldb) * 2u, ldby = static_cast<uint32_t>(p.lda) * 2u;
 
-    Stage sx, sy;
-    auto load = [&](int k0) {
-        if (MODE == kFwd) {
-            load_kc(sx, rx, voff_x, k0);
-            load_kc(sy, ry, voff_y, k0);
-        } else if (MODE == kDgrad) {
-            load_ks(sx, rx, ks_x, ldbx, k0);
-            load_kc(sy, ry, voff_y, k0);
-        } else {
-            load_ks(sx, rx, ks_x, ldbx, k0);
-            load_ks(sy, ry, ks_y, ldby, k0);
-        }
+    auto issue = [&, rx, ry](Stage& sx, Stage& sy, int k0) {
+        if (kXK) load_kmaj(sx, rx, mx, k0);
+        else load_mnmaj(sx, rx, mx, ldb, k0);
+        if (kYK) load_kmaj(sy, ry, my, k0);
+        else load_mnmaj(sy, ry, my, lda, k0);
     };
-    auto store = [&](int stage) {
+    auto commit = [&](const Stage& sx, const Stage& sy, int stage) {
         uint8_t* xt = lds + stage * kStageBytes;
-        uint8_t* yt = xt + kTileBytes;
-        if (MODE == kFwd) {
-            store_kc(sx, xt);
-            store_kc(sy, yt);
-        } else if (MODE == kDgrad) {
-            store_ks(sx, xt);
-            store_kc(sy, yt);
-        } else {
-            store_ks(sx, xt);
-            store_ks(sy, yt);
-        }
+        store_stage(sx, xt, mx);
+        store_stage(sy, xt + kTileBytes, my);
     };
 
-    f32x16_t acc[4][4];
+    f32x16_t acc[4][kFragY];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+        for (int j = 0; j < kFragY; ++j) acc[i][j] = f32x16_t{};
 
-    const int nk = (t.k_end - t.k_begin + kBK - 1) / kBK;
-    if (nk > 0) {
-        load(t.k_begin);
-        store(0);
-        __syncthreads();
-    }
-    const int frag_row = lane & 31, frag_chunk = lane >> 5;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) load(t.k_begin + (kt + 1) * kBK);
-        const uint8_t* xt = lds + cur * kStageBytes;
+    auto compute = [&](int stage) {
+        const uint8_t* xt = lds + stage * kStageBytes;
         const uint8_t* yt = xt + kTileBytes;
-        bf16x8_t xf[2][4], yf[2][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            xf[0][i] = *reinterpret_cast<const bf16x8_t*>(xt + lds_off(wx * 128 + i * 32 + frag_row, frag_chunk));
-            yf[0][i] = *reinterpret_cast<const bf16x8_t*>(yt + lds_off(wy * 128 + i * 32 + frag_row, frag_chunk));
-        }
+        for (int kk = 0; kk < kKStep / 16; ++kk) {
+            bf16x8_t xf[4], yf[kFragY];
 #pragma unroll
-        for (int kk = 0; kk < kBK / 16; ++kk) {
-            const int b = kk & 1;
-            if (kk + 1 < kBK / 16) {
+            for (int i = 0; i < 4; ++i) xf[i] = kXK ? frag_kmaj(xt, mx.fr[i], kk) : frag_mnmaj(xt, mx.fr[i], kk);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    xf[b ^ 1][i] = *reinterpret_cast<const bf16x8_t*>(
-                        xt + lds_off(wx * 128 + i * 32 + frag_row, (kk + 1) * 2 + frag_chunk));
-                    yf[b ^ 1][i] = *reinterpret_cast<const bf16x8_t*>(
-                        yt + lds_off(wy * 128 + i * 32 + frag_row, (kk + 1) * 2 + frag_chunk));
-                }
-            }
+            for (int j = 0; j < kFragY; ++j) yf[j] = kYK ? frag_kmaj(yt, my.fr[j], kk) : frag_mnmaj(yt, my.fr[j], kk);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[b][i], yf[b][j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < kFragY; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[i], yf[j], acc[i][j], 0, 0, 0);
         }
-        // Keep the next stage's LDS writes after this stage's MFMA reads, so
-        // the global loads stay in flight across the whole compute phase.
+    };
+
+    const int nk = (t.k_end - t.k_begin + kKStep - 1) / kKStep;
+#if RHP_GG_PREFETCH == 1
+    // One staging set: the loads of step kt + 1 are in flight during step kt.
+    Stage sx, sy;
+    if (nk > 0) {
+        issue(sx, sy, t.k_begin);
+        commit(sx, sy, 0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) issue(sx, sy, t.k_begin + (kt + 1) * kKStep);
+        compute(cur);
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        if (kt + 1 < nk) store(cur ^ 1);
+        if (kt + 1 < nk) commit(sx, sy, cur ^ 1);
         __syncthreads();
     }
+#else
+    // Two staging sets: the loads of step kt + 2 are in flight during step kt.
+    Stage s0x, s0y, s1x, s1y;
+    if (nk > 0) issue(s0x, s0y, t.k_begin);
+    if (nk > 1) issue(s1x, s1y, t.k_begin + kKStep);
+    if (nk > 0) commit(s0x, s0y, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+        if (kt + 2 < nk) issue(s0x, s0y, t.k_begin + (kt + 2) * kKStep);
+        compute(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + 1 < nk) commit(s1x, s1y, 1);
+        __syncthreads();
+        if (kt + 1 >= nk) break;
+        if (kt + 3 < nk) issue(s1x, s1y, t.k_begin + (kt + 3) * kKStep);
+        compute(1);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + 2 < nk) commit(s0x, s0y, 0);
+        __syncthreads();
+    }
+#endif
 
-    // Epilogue.  Lane holds, for MFMA tile (i, j), output row y = j-tile row
-    // (lane & 31) and the 4 consecutive columns x = 8*q + 4*(lane >> 5) + 0..3,
-    // q = 0..3, in acc[i][j][4q .. 4q+3].
+    // Epilogue.  For MFMA tile (i, j) the lane holds output row
+    // y = wy * kWaveY + 32 j + (lane & 31) and columns x = wx*128 + 32 i + 8 q + 4 (lane >> 5) + e
+    // in acc[i][j][4 q + e].
     const int xl = 4 * (lane >> 5);
     if (EPI == kEpiSwigluFwd) {
         uint16_t* hpre = static_cast<uint16_t*>(p.c[g]);
@@ -386,8 +462,8 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int y = wy * 128 + j * 32 + (lane & 31);
+            for (int j = 0; j < kFragY; ++j) {
+                const int y = wy * kWaveY + j * 32 + (lane & 31);
                 const int64_t row = t.row0 + t.y0 + y;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -411,8 +487,8 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int y = wy * 128 + j * 32 + (lane & 31);
+        for (int j = 0; j < kFragY; ++j) {
+            const int y = wy * kWaveY + j * 32 + (lane & 31);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int xr = wx * 128 + i * 32 + q * 8 + xl;
