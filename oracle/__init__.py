@@ -1,7 +1,7 @@
 """CPU oracle for the MoE layer hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker or as the timed
+``bench.py`` may import this package, and only to check results or as the timed
 CPU baseline.  The product (``resihp-megatron_amd/``) never imports it.
 
 Contents:
@@ -15,6 +15,7 @@ Contents:
               build adds (SwiGLU experts, sigmoid scoring, shared experts,
               FP8 delayed scaling).
 
-Parity status of every oracle function is listed in DESIGN.md; the pins
-themselves live in ``tests/test_oracle_*.py``.
+Every oracle function is pinned by a check in ``tests/test_oracle_*.py``:
+the reference's own recorded float64 outputs (``tests/golden``), a closed
+form, brute force on tiny inputs, or a library routine.
 """

@@ -2,7 +2,7 @@
  * CPU oracle for the MoE routing path -- TEST INFRASTRUCTURE ONLY.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
- * this library, and only as the checker.  The product never links it.
+ * this library, and only to check results.  The product never links it.
  *
  * It restates, in plain C with IEEE single/double arithmetic and no
  * floating-point contraction (built with -ffp-contract=off), the routing

@@ -1,4 +1,4 @@
-"""The fused MoE layer (forward + backward) on the GPU against the float64 oracle, per BASELINE config,
+"""The fused MoE layer (forward + backward) on the GPU against the float64 oracle, per benchmark configuration,
 and the drop-in API against the reference's own recorded outputs.
 
 Every layer case runs the GPU layer, takes its routing (bit-exact with the C

@@ -1,7 +1,7 @@
 """Routing and dispatch on the GPU, bit for bit against the C oracle (oracle/route_ref.c).
 
 Logits, top-k ids, gates, per-expert counts, offsets, per-source counts and the
-permutation must be identical bit patterns, on the BASELINE shapes (router on
+permutation must be identical bit patterns, on the benchmark shapes (router on
 full token counts for the Mixtral and DeepSeek-like layers) and on edge cases:
 exact ties, NaN logits, empty experts, one token, invalid ids.
 """
