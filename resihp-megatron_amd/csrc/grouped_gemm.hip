@@ -172,7 +172,7 @@ template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI =
 #define RHP_GG_WAVES 8
 #endif
 #ifndef RHP_GG_PREFETCH
-#define RHP_GG_PREFETCH 1
+#define RHP_GG_PREFETCH 3
 #endif
 #ifndef RHP_GG_KSTEP
 #define RHP_GG_KSTEP 64
@@ -316,6 +316,133 @@ __device__ __forceinline__ void load_bf16x4(const uint16_t* p, float* o) {
     o[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
+// Epilogue staging: half a tile of fp32 accumulators, rows padded by 16 bytes
+// so that the 16 lanes of a ds_write_b128 (16 consecutive rows) hit distinct
+// bank groups.
+constexpr int kEpRows = 128;
+constexpr int kEpPitchF = 256 + 4;   // floats per staged row
+static_assert(kEpRows * kEpPitchF * 4 <= 2 * kStageBytes, "epilogue staging must fit in the stage buffers");
+
+__device__ __forceinline__ float4 lds_f4(const float* ep, int r, int x) {
+    return *reinterpret_cast<const float4*>(ep + r * kEpPitchF + x);
+}
+
+// Rows [r0, r0 + 128) of the tile, staged in ep.  Thread t handles 4-column
+// pieces t, t + 512, ...; a wave covers one row (or two rows of 128 columns).
+template <int MODE, int EPI>
+__device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, const float* ep, int r0) {
+    const int g = t.g;
+    if (EPI == kEpiSwigluFwd) {
+        // X columns of the tile are [gate 64 | up 64] for each half of 128
+        // activation columns; piece a covers activation columns 4a .. 4a + 3.
+        uint16_t* hpre = static_cast<uint16_t*>(p.c[g]);
+        uint16_t* act = static_cast<uint16_t*>(p.c2[g]);
+#pragma unroll 4
+        for (int idx = threadIdx.x; idx < kEpRows * 32; idx += kThreadsMfma) {
+            const int r = idx >> 5, a = (idx & 31) * 4;
+            const int yr = r0 + r, col = t.x0 + a;
+            if (yr >= t.y_lim || col >= p.N) continue;
+            const int xg = (a >> 6) * 128 + (a & 63);
+            const float4 gv = lds_f4(ep, r, xg), uv = lds_f4(ep, r, xg + 64);
+            const int64_t row = t.row0 + t.y0 + yr;
+            store_bf16x4(hpre + row * p.ldc + col, gv.x, gv.y, gv.z, gv.w);
+            store_bf16x4(hpre + row * p.ldc + p.f + col, uv.x, uv.y, uv.z, uv.w);
+            store_bf16x4(act + row * p.ldc2 + col, silu_f(gv.x) * uv.x, silu_f(gv.y) * uv.y, silu_f(gv.z) * uv.z,
+                         silu_f(gv.w) * uv.w);
+        }
+        return;
+    }
+    uint16_t* out = static_cast<uint16_t*>(p.c[g]);
+#pragma unroll 4
+    for (int idx = threadIdx.x; idx < kEpRows * 64; idx += kThreadsMfma) {
+        const int r = idx >> 6, x = (idx & 63) * 4;
+        const int yr = r0 + r;
+        if (yr >= t.y_lim || x >= t.x_lim) continue;
+        const int col = t.x0 + x;
+        const float4 v = lds_f4(ep, r, x);
+        if (MODE == kWgrad) {
+            store_bf16x4(out + static_cast<int64_t>(t.y0 + yr) * p.ldc + col, v.x, v.y, v.z, v.w);
+            continue;
+        }
+        const int64_t row = t.row0 + t.y0 + yr;
+        if (EPI == kEpiStore) {
+            store_bf16x4(out + row * p.ldc + col, v.x, v.y, v.z, v.w);
+        } else if (EPI == kEpiGeluFwd) {
+            uint16_t* act = static_cast<uint16_t*>(p.c2[g]);
+            store_bf16x4(out + row * p.ldc + col, v.x, v.y, v.z, v.w);
+            store_bf16x4(act + row * p.ldc2 + col, gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w));
+        } else if (EPI == kEpiGeluBwd) {
+            const uint16_t* hp = static_cast<const uint16_t*>(p.aux[g]);
+            float hv[4];
+            load_bf16x4(hp + row * p.ldaux + col, hv);
+            store_bf16x4(out + row * p.ldc + col, v.x * dgelu_f(hv[0]), v.y * dgelu_f(hv[1]), v.z * dgelu_f(hv[2]),
+                         v.w * dgelu_f(hv[3]));
+        } else if (EPI == kEpiSwigluBwd) {
+            const uint16_t* hp = static_cast<const uint16_t*>(p.aux[g]);
+            float gv[4], uv[4];
+            load_bf16x4(hp + row * p.ldaux + col, gv);
+            load_bf16x4(hp + row * p.ldaux + p.f + col, uv);
+            const float dv[4] = {v.x, v.y, v.z, v.w};
+            float dg[4], du[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                dg[e] = dv[e] * uv[e] * dsilu_f(gv[e]);
+                du[e] = dv[e] * silu_f(gv[e]);
+            }
+            store_bf16x4(out + row * p.ldc + col, dg[0], dg[1], dg[2], dg[3]);
+            store_bf16x4(out + row * p.ldc + p.f + col, du[0], du[1], du[2], du[3]);
+        }
+    }
+}
+
+// Epilogue, in two halves of 128 Y rows.  The waves owning a half write
+// their fp32 accumulators to LDS ([128 rows][256 X] at kEpPitchF floats per
+// row); then every thread takes 4-column pieces, so each wave instruction
+// reads or writes whole contiguous row segments in HBM.  For MFMA tile (i, j)
+// a lane holds Y row wy * kWaveY + 32 j + (lane & 31) and X columns
+// wx * 128 + 32 i + 8 q + 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller
+// guarantees that no wave still reads or writes the LDS buffer.
+template <int MODE, int EPI>
+__device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][kFragY],
+                                         int wx, int wy, int lane) {
+    float* ep = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        __syncthreads();
+        if ((wy * kWaveY) / kEpRows == half) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < kFragY; ++j) {
+                    const int y = wy * kWaveY + j * 32 + (lane & 31) - half * kEpRows;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int x = wx * 128 + i * 32 + q * 8 + 4 * (lane >> 5);
+                        float4 v;
+                        v.x = acc[i][j][4 * q + 0];
+                        v.y = acc[i][j][4 * q + 1];
+                        v.z = acc[i][j][4 * q + 2];
+                        v.w = acc[i][j][4 * q + 3];
+                        *reinterpret_cast<float4*>(ep + y * kEpPitchF + x) = v;
+                    }
+                }
+        }
+        __syncthreads();
+        epilogue_half<MODE, EPI>(p, t, ep, half * kEpRows);
+    }
+}
+
+// Scheduling hint: MF MFMAs with RD LDS reads spread evenly between them.
+template <int Q, int MF, int RD>
+__device__ __forceinline__ void interleave_reads() {
+    if constexpr (Q < MF) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        constexpr int n = RD * (Q + 1) / MF - RD * Q / MF;
+        if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
+        interleave_reads<Q + 1, MF, RD>();
+    }
+}
+
 template <int MODE, int EPI>
 __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
     __shared__ __align__(16) uint8_t lds[2 * kStageBytes];
@@ -411,7 +538,61 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
     };
 
     const int nk = (t.k_end - t.k_begin + kKStep - 1) / kKStep;
-#if RHP_GG_PREFETCH == 1
+#if RHP_GG_PREFETCH == 3
+    // One staging set, and MFMA fragments double-buffered in registers: the
+    // fragments of k16 block kk + 1 are read from LDS while the MFMAs of block
+    // kk run, and block 0 of the next stage is read right after the barrier.
+    typedef bf16x8_t FragSet[4 + kFragY];
+    auto read_frags = [&](FragSet& f, int stage, int kk) {
+        const uint8_t* xt = lds + stage * kStageBytes;
+        const uint8_t* yt = xt + kTileBytes;
+        // Y fragments first: every MFMA of a block uses one, so the next
+        // block's Y reads need registers of their own and are issued early.
+#pragma unroll
+        for (int j = 0; j < kFragY; ++j) f[4 + j] = kYK ? frag_kmaj(yt, my.fr[j], kk) : frag_mnmaj(yt, my.fr[j], kk);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[i] = kXK ? frag_kmaj(xt, mx.fr[i], kk) : frag_mnmaj(xt, mx.fr[i], kk);
+    };
+    auto mfmas = [&](const FragSet& f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < kFragY; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[4 + j], acc[i][j], 0, 0, 0);
+    };
+    constexpr int kReads = (kXK ? 4 : 8) + (kYK ? kFragY : 2 * kFragY);   // LDS read instructions per block
+    Stage sx, sy;
+    FragSet fa, fb;
+    if (nk > 0) {
+        issue(sx, sy, t.k_begin);
+        commit(sx, sy, 0);
+    }
+    __syncthreads();
+    if (nk > 0) read_frags(fa, 0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) issue(sx, sy, t.k_begin + (kt + 1) * kKStep);
+#pragma unroll
+        for (int kk = 0; kk < kKStep / 16; kk += 2) {
+            read_frags(fb, cur, kk + 1);
+            mfmas(fa);
+            interleave_reads<0, 4 * kFragY, kReads>();
+            if (kk + 2 < kKStep / 16) {
+                read_frags(fa, cur, kk + 2);
+                mfmas(fb);
+                interleave_reads<0, 4 * kFragY, kReads>();
+            } else {
+                mfmas(fb);
+            }
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) commit(sx, sy, cur ^ 1);
+        __syncthreads();
+        if (more) read_frags(fa, cur ^ 1, 0);
+    }
+#elif RHP_GG_PREFETCH == 1
     // One staging set: the loads of step kt + 1 are in flight during step kt.
     Stage sx, sy;
     if (nk > 0) {
@@ -452,85 +633,263 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
     }
 #endif
 
-    // Epilogue.  For MFMA tile (i, j) the lane holds output row
-    // y = wy * kWaveY + 32 j + (lane & 31) and columns x = wx*128 + 32 i + 8 q + 4 (lane >> 5) + e
-    // in acc[i][j][4 q + e].
-    const int xl = 4 * (lane >> 5);
-    if (EPI == kEpiSwigluFwd) {
-        uint16_t* hpre = static_cast<uint16_t*>(p.c[g]);
-        uint16_t* act = static_cast<uint16_t*>(p.c2[g]);
+    epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane);
+}
+
+// ------------------------------------------------------------------ MFMA kernel, direct HBM -> LDS loads
+//
+// Same tiles, wave layout, fragments and epilogue as gg_bf16_kernel, but the
+// operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds
+// (no staging registers, no LDS stores), K step 32, kDmaStages LDS stages.
+// One such load moves 64 lanes x 16 bytes into 1 KB of LDS at M0 + 16 * lane,
+// so a stage is built from 1 KB blocks whose lanes pick the global chunk that
+// belongs at their LDS position.
+//
+//   K-major tile  [256 rows][32 k], 64-byte rows, chunk c of row r at position
+//                 c ^ ((r >> 2) & 3): the 16 rows of one ds_read_b128 hit 16
+//                 distinct 16-byte bank slots.
+//   MN-major tile [32 k][256 mn], 512-byte rows, chunk c at c ^ 4 (k & 3) (as above).
+//
+// Pipeline (S = kDmaStages): the loads of step kt + S - 1 are issued right
+// after the barrier that opens step kt.  That barrier also guarantees that
+// the stages of steps kt and kt + 1 are complete, so the fragments of step
+// kt + 1's first k16 block are read during step kt's second block and no wave
+// waits on LDS after a barrier.  Stage (kt - 1) mod S, which the new loads
+// overwrite, was last read before that barrier.
+//
+// The loads are written as inline assembly so that the compiler, which does
+// not see them, does not make every LDS read wait for all of them; the code
+// counts them itself (s_waitcnt vmcnt) before each barrier.
+
+#ifndef RHP_GG_DMA
+#define RHP_GG_DMA 1
+#endif
+#ifndef RHP_GG_STAGES
+#define RHP_GG_STAGES 4
+#endif
+constexpr int kDmaK = 32;
+constexpr int kDmaStages = RHP_GG_STAGES;
+constexpr int kDmaTileBytes = kTile * kDmaK * 2;          // 16 KB per operand
+constexpr int kDmaStageBytes = 2 * kDmaTileBytes;         // X + Y
+constexpr int kDmaBlocks = kDmaTileBytes / 1024;          // 1 KB blocks per operand
+constexpr int kDmaPerWave = kDmaBlocks / kWaves;          // loads per wave per operand per step
+constexpr int kDmaPerStep = 2 * kDmaPerWave;              // loads per wave per step
+constexpr int kDmaLdsBytes = kDmaStages * kDmaStageBytes > kEpRows * kEpPitchF * 4 ? kDmaStages * kDmaStageBytes
+                                                                                    : kEpRows * kEpPitchF * 4;
+static_assert(kDmaStages >= 3 && kDmaLdsBytes <= 163840, "3 to 5 stages of 32 KB");
+static_assert(kDmaBlocks % kWaves == 0, "whole loads per wave");
+constexpr uint32_t kOutOfRange = 0x80000000u;             // a buffer offset past every view: reads zero
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+struct Rsrc {
+    i32x4_t d;
+};
+__device__ __forceinline__ Rsrc make_dma_rsrc(const void* base, int64_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    Rsrc r;
+    r.d[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a));
+    r.d[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));
+    r.d[2] = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes > 0x7ffffff0 ? 0x7ffffff0 : bytes));
+    r.d[3] = 0x00020000;
+    return r;
+}
+// 16 bytes per lane from the buffer at voff + soff into LDS at lds + 16 * lane.
+__device__ __forceinline__ void dma16(const Rsrc& r, uint32_t voff, uint32_t soff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(r.d), "s"(__builtin_amdgcn_readfirstlane(soff)),
+                   "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+// Wait until at most n steps' worth of this wave's loads are still in flight.
+__device__ __forceinline__ void wait_dma_steps(int n) {
+    static_assert(2 * kDmaPerStep < 64, "vmcnt field");
+    if (n >= 2) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * kDmaPerStep) & 15) | (((2 * kDmaPerStep) >> 4) << 14));
+    } else if (n == 1) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (kDmaPerStep & 15) | ((kDmaPerStep >> 4) << 14));
+    } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+    }
+}
+
+__device__ __forceinline__ int dkmaj_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
+
+// Per-lane offsets of one operand.  vo[j]: global byte offset (at k = 0) of
+// this lane's chunk in load j of this wave; fr[i][b]: LDS offset of fragment
+// i at k16 block b of a stage (MN-major: block 1 adds a constant).
+struct DmaMap {
+    uint32_t vo[kDmaPerWave];
+    uint32_t fr[4][2];
+};
+
+template <class RowOf>
+__device__ __forceinline__ void dmap_kmaj(DmaMap& m, uint32_t ld, int frag_row0, int nfrag, RowOf src_row) {
+    const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < kFragY; ++j) {
-                const int y = wy * kWaveY + j * 32 + (lane & 31);
-                const int64_t row = t.row0 + t.y0 + y;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int col = t.x0 + wx * 64 + i * 32 + q * 8 + xl;
-                    if (y < t.y_lim && col < p.N) {
-                        float gv[4], uv[4], av[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            gv[e] = acc[i][j][q * 4 + e];
-                            uv[e] = acc[i + 2][j][q * 4 + e];
-                            av[e] = silu_f(gv[e]) * uv[e];
-                        }
-                        store_bf16x4(hpre + row * p.ldc + col, gv[0], gv[1], gv[2], gv[3]);
-                        store_bf16x4(hpre + row * p.ldc + p.f + col, uv[0], uv[1], uv[2], uv[3]);
-                        store_bf16x4(act + row * p.ldc2 + col, av[0], av[1], av[2], av[3]);
-                    }
-                }
-            }
-        return;
+    for (int j = 0; j < kDmaPerWave; ++j) {
+        const int row = (j * kWaves + w) * 16 + (L >> 2);
+        const int chunk = (L & 3) ^ ((row >> 2) & 3);
+        m.vo[j] = (static_cast<uint32_t>(src_row(row)) * ld + chunk * 8) * 2u;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < kFragY; ++j) {
-            const int y = wy * kWaveY + j * 32 + (lane & 31);
+        for (int b = 0; b < 2; ++b)
+            m.fr[i][b] = i < nfrag ? dkmaj_off(frag_row0 + i * 32 + (L & 31), 2 * b + (L >> 5)) : 0;
+}
+
+__device__ __forceinline__ void dmap_mnmaj(DmaMap& m, uint32_t ld, int mn0, int mn_lim, int frag_row0, int nfrag) {
+    const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int xr = wx * 128 + i * 32 + q * 8 + xl;
-                if (y >= t.y_lim || xr >= t.x_lim) continue;
-                const int col = t.x0 + xr;
-                float v[4];
+    for (int j = 0; j < kDmaPerWave; ++j) {
+        const int k = (j * kWaves + w) * 2 + (L >> 5);
+        const int chunk = (L & 31) ^ ((k & 3) << 2);
+        m.vo[j] = chunk * 8 < mn_lim ? (static_cast<uint32_t>(k) * ld + static_cast<uint32_t>(mn0 + chunk * 8)) * 2u
+                                     : kOutOfRange;
+    }
+    const int g = L >> 4, r = L & 15;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[i][j][q * 4 + e];
-                if (MODE == kWgrad) {
-                    uint16_t* dw = static_cast<uint16_t*>(p.c[g]);
-                    store_bf16x4(dw + static_cast<int64_t>(t.y0 + y) * p.ldc + col, v[0], v[1], v[2], v[3]);
-                    continue;
+    for (int i = 0; i < 4; ++i) {
+        m.fr[i][0] = i < nfrag ? mnmaj_off(8 * (g >> 1) + (r >> 2), frag_row0 + i * 32 + 16 * (g & 1) + 4 * (r & 3)) : 0;
+        m.fr[i][1] = m.fr[i][0] + 16 * 512;
+    }
+}
+
+template <int MODE, int EPI>
+__global__ __launch_bounds__(kThreadsMfma) void gg_bf16_dma_kernel(Params p) {
+    __shared__ __align__(1024) uint8_t lds[kDmaLdsBytes];
+    Tile t;
+    if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
+    t.g = __builtin_amdgcn_readfirstlane(t.g);
+    t.x0 = __builtin_amdgcn_readfirstlane(t.x0);
+    t.x_lim = __builtin_amdgcn_readfirstlane(t.x_lim);
+    t.y0 = __builtin_amdgcn_readfirstlane(t.y0);
+    t.y_lim = __builtin_amdgcn_readfirstlane(t.y_lim);
+    t.row0 = __builtin_amdgcn_readfirstlane(static_cast<int>(t.row0));
+    t.k_begin = __builtin_amdgcn_readfirstlane(t.k_begin);
+    t.k_end = __builtin_amdgcn_readfirstlane(t.k_end);
+    const int g = t.g;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wx = wave & 1, wy = wave >> 1;
+    constexpr bool kXK = MODE == kFwd;
+    constexpr bool kYK = MODE != kWgrad;
+
+    const uint16_t* A = static_cast<const uint16_t*>(p.a[g]);
+    const uint16_t* B = static_cast<const uint16_t*>(p.b[g]);
+    const uint32_t ldb = static_cast<uint32_t>(p.ldb), lda = static_cast<uint32_t>(p.lda);
+    Rsrc rx, ry;
+    DmaMap mx, my;
+    if (MODE == kWgrad) {
+        const int64_t rows = t.k_end;   // group rows; reads past them return zero
+        rx = make_dma_rsrc(B + t.row0 * p.ldb, rows * p.ldb * 2);
+        ry = make_dma_rsrc(A + t.row0 * p.lda, rows * p.lda * 2);
+        dmap_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
+        dmap_mnmaj(my, lda, t.y0, t.y_lim, wy * kWaveY, kFragY);
+    } else {
+        ry = make_dma_rsrc(A + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda * 2);
+        const int y_last = t.y_lim - 1;
+        dmap_kmaj(my, lda, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
+        if (MODE == kFwd) {
+            rx = make_dma_rsrc(B, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb * 2);
+            dmap_kmaj(mx, ldb, wx * 128, 4, [&](int r) {
+                if (EPI == kEpiSwigluFwd) {
+                    // 256 weight rows = [gate 64 | up 64] for each half of 128 activation columns.
+                    const int half = r >> 7, qq = r & 127;
+                    int col = t.x0 + half * 64 + (qq & 63);
+                    col = col < p.f ? col : 0;
+                    return qq < 64 ? col : p.f + col;
                 }
-                const int64_t row = t.row0 + t.y0 + y;
-                uint16_t* out = static_cast<uint16_t*>(p.c[g]);
-                if (EPI == kEpiStore) {
-                    store_bf16x4(out + row * p.ldc + col, v[0], v[1], v[2], v[3]);
-                } else if (EPI == kEpiGeluFwd) {
-                    uint16_t* act = static_cast<uint16_t*>(p.c2[g]);
-                    store_bf16x4(out + row * p.ldc + col, v[0], v[1], v[2], v[3]);
-                    store_bf16x4(act + row * p.ldc2 + col, gelu_f(v[0]), gelu_f(v[1]), gelu_f(v[2]), gelu_f(v[3]));
-                } else if (EPI == kEpiGeluBwd) {
-                    const uint16_t* hp = static_cast<const uint16_t*>(p.aux[g]);
-                    float hv[4];
-                    load_bf16x4(hp + row * p.ldaux + col, hv);
-                    store_bf16x4(out + row * p.ldc + col, v[0] * dgelu_f(hv[0]), v[1] * dgelu_f(hv[1]),
-                                 v[2] * dgelu_f(hv[2]), v[3] * dgelu_f(hv[3]));
-                } else if (EPI == kEpiSwigluBwd) {
-                    const uint16_t* hp = static_cast<const uint16_t*>(p.aux[g]);
-                    float gv[4], uv[4], dg[4], du[4];
-                    load_bf16x4(hp + row * p.ldaux + col, gv);
-                    load_bf16x4(hp + row * p.ldaux + p.f + col, uv);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        dg[e] = v[e] * uv[e] * dsilu_f(gv[e]);
-                        du[e] = v[e] * silu_f(gv[e]);
-                    }
-                    store_bf16x4(out + row * p.ldc + col, dg[0], dg[1], dg[2], dg[3]);
-                    store_bf16x4(out + row * p.ldc + p.f + col, du[0], du[1], du[2], du[3]);
-                }
-            }
+                const int n = t.x0 + r;
+                return n < p.N ? n : 0;
+            });
+        } else {
+            rx = make_dma_rsrc(B, static_cast<int64_t>(p.K) * p.ldb * 2);
+            dmap_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
         }
+    }
+
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+    auto issue = [&](int step, int stage) {
+        const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kDmaK);
+        const uint32_t base = lds0 + stage * kDmaStageBytes + wave * 1024;
+#pragma unroll
+        for (int j = 0; j < kDmaPerWave; ++j) {
+            const uint32_t at = base + j * kWaves * 1024;
+            if (kXK) dma16(rx, mx.vo[j], k0 * 2u, at);
+            else dma16(rx, mx.vo[j] + k0 * ldb * 2u, 0, at);
+            if (kYK) dma16(ry, my.vo[j], k0 * 2u, at + kDmaTileBytes);
+            else dma16(ry, my.vo[j] + k0 * lda * 2u, 0, at + kDmaTileBytes);
+        }
+    };
+
+    f32x16_t acc[4][kFragY];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < kFragY; ++j) acc[i][j] = f32x16_t{};
+
+    typedef bf16x8_t FragSet[4 + kFragY];
+    auto read_frags = [&](FragSet& f, int stage, int b) {
+        const uint8_t* xt = lds + stage * kDmaStageBytes;
+        const uint8_t* yt = xt + kDmaTileBytes;
+#pragma unroll
+        for (int j = 0; j < kFragY; ++j)
+            f[4 + j] = kYK ? *reinterpret_cast<const bf16x8_t*>(yt + my.fr[j][b]) : frag_mnmaj(yt, my.fr[j][b], 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            f[i] = kXK ? *reinterpret_cast<const bf16x8_t*>(xt + mx.fr[i][b]) : frag_mnmaj(xt, mx.fr[i][b], 0);
+    };
+    auto mfmas = [&](const FragSet& f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < kFragY; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[4 + j], acc[i][j], 0, 0, 0);
+    };
+    constexpr int kReads = (kXK ? 4 : 8) + (kYK ? kFragY : 2 * kFragY);
+    // All waves see every LDS write of the stages the wait covered; LDS
+    // accesses do not move across it.
+    auto barrier = [] {
+        __builtin_amdgcn_sched_barrier(0);   // this step's MFMAs (and their LDS waits) stay before it
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    const int nk = (t.k_end - t.k_begin + kDmaK - 1) / kDmaK;
+    FragSet fa, fb;
+    if (nk > 0) {
+#pragma unroll
+        for (int s = 0; s < kDmaStages - 1; ++s)
+            if (s < nk) issue(s, s);
+        wait_dma_steps(min(kDmaStages - 2, nk - 1) - min(1, nk - 1));
+        barrier();
+        read_frags(fa, 0, 0);
+    }
+    int stage = 0, next = 1 % kDmaStages, fill = kDmaStages - 1;   // stages of steps kt, kt + 1, kt + S - 1
+    // The body is the same for every step (the last one reads a stale block
+    // it does not use), so the accumulators never need copies between paths.
+    for (int kt = 0; kt < nk; ++kt) {
+        if (kt + kDmaStages - 1 < nk) issue(kt + kDmaStages - 1, fill);
+        read_frags(fb, stage, 1);
+        mfmas(fa);
+        interleave_reads<0, 4 * kFragY, kReads>();
+        read_frags(fa, next, 0);
+        mfmas(fb);
+        interleave_reads<0, 4 * kFragY, kReads>();
+        // Steps up to min(kt + S - 1, nk - 1) are issued; step kt + 2 must be complete.
+        wait_dma_steps(min(kt + kDmaStages - 1, nk - 1) - min(kt + 2, nk - 1));
+        barrier();
+        stage = next;
+        next = next + 1 == kDmaStages ? 0 : next + 1;
+        fill = fill + 1 == kDmaStages ? 0 : fill + 1;
+    }
+    // Every load was waited for (the last barrier's wait covered all of them,
+    // or there was one step only and the prologue waited), and every wave has
+    // consumed its LDS reads, so the stage memory can hold the epilogue.
+    epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane);
 }
 
 // ------------------------------------------------------------------ generic kernel (any dtype)
@@ -630,7 +989,11 @@ template <int MODE, int EPI>
 void launch_one(const Job& j, const Params& p, hipStream_t s) {
     if (j.mfma) {
         const unsigned nb = mfma_blocks<MODE, EPI>(p, j.rows_cap);
+#if RHP_GG_DMA
+        if (nb) hipLaunchKernelGGL((gg_bf16_dma_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+#else
         if (nb) hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+#endif
         return;
     }
     const unsigned nb = simt_blocks<MODE>(p, j.rows_cap);
