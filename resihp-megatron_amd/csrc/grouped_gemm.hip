@@ -148,150 +148,49 @@ __device__ __forceinline__ bool find_tile(const Params& p, int xt_cols, int yt_r
 // columns (their 256 weight rows are 128 gate + 128 up rows).
 template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI == kEpiSwigluFwd ? 128 : 256; }
 
-// ------------------------------------------------------------------ MFMA kernel (bf16)
+// ------------------------------------------------------------------ MFMA kernels (bf16)
 //
-// A 256 x 256 output tile per workgroup of W waves (W = 4: one wave per SIMD,
-// 128 x 128 per wave, accumulators in AGPRs; W = 8: two waves per SIMD,
-// 128 x 64 per wave).  Wave w owns X rows [128 (w % 2), +128) and Y rows
-// [(256 / (W / 2)) (w / 2), +256 / (W / 2)).  K advances by the K step (64).
+// A 256 x 256 output tile per workgroup of 8 waves (two per SIMD).  Wave w
+// owns X rows [128 (w % 2), +128) and Y rows [64 (w / 2), +64): 4 x 2
+// accumulators of v_mfma_f32_32x32x16_bf16 (128 registers).
 //
-// Operands sit in LDS in their global layout, so the HBM -> LDS copy is a
-// plain 16-byte-vector copy:
-//   K-major tile  [256 rows][K step]  (64- or 144-byte rows) -> fragments by ds_read_b128
-//   MN-major tile [K step][256 rows]  (512-byte rows)         -> fragments by two
-//     ds_read_b64_tr_b16, which transpose 4 x 16 blocks across each 16-lane group
-// K-major rows are padded so that a 16-lane ds_read_b128 hits 16 distinct bank
-// slots.  MN-major rows keep 16-byte chunk c at position c ^ 4 (k & 3), so the
-// 8 k rows of one transposed read fall on distinct 64-byte bank groups.
+// Operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds:
+// no staging registers and no LDS stores.  One such load moves 64 lanes x 16
+// bytes into 1 KB of LDS at M0 + 16 * lane, so a stage is built from 1 KB
+// blocks whose lanes pick the global chunk that belongs at their position.
+//   K-major tiles (K contiguous in HBM: FWD both operands, DGRAD token rows)
+//     keep rows of K-step elements with the 16-byte chunks XOR-swizzled by
+//     row, so the 16 rows of one ds_read_b128 hit 16 distinct bank slots.
+//   MN-major tiles (K is the slow dimension: DGRAD weights, both WGRAD
+//     operands) keep 512-byte k rows with chunk c at position c ^ 4 (k & 3)
+//     and are read with gfx950's ds_read_b64_tr_b16, which transposes 4 x 16
+//     blocks across each 16-lane group; two such reads give one fragment.
+// No transposed copy of any operand is made in HBM.
 //
-// Pipeline: two LDS stages and two register staging sets.  Step kt computes
-// from one stage while the loads of step kt + 2 are in flight and the data of
-// step kt + 1 (loaded one step earlier) is written to the other stage.
-
-#ifndef RHP_GG_WAVES
-#define RHP_GG_WAVES 8
-#endif
-#ifndef RHP_GG_PREFETCH
-#define RHP_GG_PREFETCH 3
-#endif
-#ifndef RHP_GG_KSTEP
-#define RHP_GG_KSTEP 64
-#endif
+// The loads are inline assembly so that the compiler, which does not see them,
+// does not make every LDS read wait for all of them; each kernel counts them
+// itself (s_waitcnt vmcnt) before its barriers.  Fragments are double-buffered
+// in registers: the reads of the next k16 block are interleaved with the
+// MFMAs of the current one.
+//
+// FWD runs gg_bf16_k64_kernel (K step 64: each row of a stage is a whole
+// 128-byte line, so L2 sees half the requests); DGRAD and WGRAD run
+// gg_bf16_k32_kernel (K step 32, four stages, loads two steps ahead), which
+// measured faster for the transposed operands.
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kWaves = RHP_GG_WAVES;
+constexpr int kWaves = 8;
 constexpr int kThreadsMfma = 64 * kWaves;
-constexpr int kKStep = RHP_GG_KSTEP;
-// K-major rows: 2 * kKStep bytes, padded to 144 bytes for kKStep = 64 so that
-// the 16 rows of one 16-lane fragment read land on 16 distinct 16-byte bank
-// slots (row * 9 mod 16 is a bijection); 64-byte rows need no padding.
-constexpr int kKPitch = kKStep == 64 ? 144 : 64;
-constexpr int kKChunks = kKStep / 8;                       // 16-byte chunks per K-major row
-constexpr int kTileBytes = kTile * kKPitch;               // also holds an MN-major tile (kKStep * 512)
-constexpr int kStageBytes = 2 * kTileBytes;                // X + Y
-constexpr int kChunks = kTile * kKStep * 2 / 16 / kThreadsMfma;   // 16-byte chunks per thread per operand
 constexpr int kWaveY = kTile / (kWaves / 2);               // Y rows per wave
 constexpr int kFragY = kWaveY / 32;                        // Y fragments per wave
-static_assert(kWaves == 4 || kWaves == 8, "4 or 8 waves per tile");
-static_assert(kKStep == 32 || kKStep == 64, "K step 32 or 64");
-static_assert(kTileBytes >= kKStep * 512, "an MN-major tile must fit");
 
-__device__ __forceinline__ int kmaj_off(int row, int chunk) { return row * kKPitch + chunk * 16; }
 __device__ __forceinline__ int mnmaj_off(int k, int mn) {
     return k * 512 + (((mn >> 3) ^ ((k & 3) << 2)) << 4) + ((mn & 7) << 1);
 }
 
-// Raw buffer view of [base, base + bytes); loads beyond it return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-    const int n = bytes > 0x7ffffff0 ? 0x7ffffff0 : static_cast<int>(bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), n, 0x00020000);
-}
-__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-
-// One operand tile of one K step on its way from HBM to LDS.
-struct Stage {
-    uint4 v[kChunks];
-};
-
-// Per-thread byte offsets of one operand, fixed for the whole K loop.
-//   gl[q]  global offset of the thread's q-th 16-byte chunk at k = 0
-//   st[q]  LDS offset (within a tile) the chunk is stored at
-//   fr[i]  LDS offset of the thread's part of fragment i at k16 block 0
-// K steps, stages, k16 blocks and the two halves of a transposed read only
-// add constants, which fold into the instructions' offset fields.
-struct OperandMap {
-    uint32_t gl[kChunks];
-    uint32_t st[kChunks];
-    uint32_t fr[4];
-    bool ok;   // MN-major: this thread's chunks lie inside the valid rows
-};
-
-// K-major operand ([rows][k], element (row, k) at (src_row(row) * ld + k) * 2).
-// Thread t copies chunk t % C of tile rows q * (threads / C) + t / C, C = kKChunks.
-template <class RowOf>
-__device__ __forceinline__ void map_kmaj(OperandMap& m, uint32_t ld, int frag_row0, int nfrag, RowOf src_row) {
-    const int t = threadIdx.x, L = t & 63;
-    const int c = t % kKChunks;
-#pragma unroll
-    for (int q = 0; q < kChunks; ++q) {
-        const int r = q * (kThreadsMfma / kKChunks) + t / kKChunks;
-        m.gl[q] = (static_cast<uint32_t>(src_row(r)) * ld + c * 8) * 2u;
-        m.st[q] = kmaj_off(r, c);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) m.fr[i] = i < nfrag ? kmaj_off(frag_row0 + i * 32 + (L & 31), L >> 5) : 0;
-    m.ok = true;
-}
-
-// MN-major operand ([k][rows], element (k, mn) at (k * ld + mn) * 2).  Thread t
-// copies chunk t % 32 (8 mn values) of k rows q * (threads / 32) + t / 32;
-// chunks at or beyond mn_lim read as zero.  Fragment lanes follow the
-// transposed-read pattern: lane r of 16-lane group g points at
-// k = 8 (g / 2) + r / 4 and mn = 16 (g % 2) + 4 (r % 4) of the fragment's rows.
-__device__ __forceinline__ void map_mnmaj(OperandMap& m, uint32_t ld, int mn0, int mn_lim, int frag_row0, int nfrag) {
-    const int t = threadIdx.x, L = t & 63;
-    const int c = t & 31;
-#pragma unroll
-    for (int q = 0; q < kChunks; ++q) {
-        const int k = q * (kThreadsMfma / 32) + (t >> 5);
-        m.gl[q] = (static_cast<uint32_t>(k) * ld + static_cast<uint32_t>(mn0 + c * 8)) * 2u;
-        m.st[q] = mnmaj_off(k, c * 8);
-    }
-    const int g = L >> 4, r = L & 15;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        m.fr[i] = i < nfrag ? mnmaj_off(8 * (g >> 1) + (r >> 2), frag_row0 + i * 32 + 16 * (g & 1) + 4 * (r & 3)) : 0;
-    m.ok = c * 8 < mn_lim;
-}
-
-__device__ __forceinline__ void load_kmaj(Stage& s, __amdgpu_buffer_rsrc_t r, const OperandMap& m, int k0) {
-    const uint32_t soff = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(k0) * 2u);
-#pragma unroll
-    for (int q = 0; q < kChunks; ++q) s.v[q] = bload(r, m.gl[q], soff);
-}
-// The K offset goes into the per-lane offset, which the buffer range check
-// covers, so rows past the view (a group's end) read as zero.
-__device__ __forceinline__ void load_mnmaj(Stage& s, __amdgpu_buffer_rsrc_t r, const OperandMap& m, uint32_t ld,
-                                           int k0) {
-    const uint32_t koff = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(k0) * ld * 2u);
-#pragma unroll
-    for (int q = 0; q < kChunks; ++q) s.v[q] = m.ok ? bload(r, m.gl[q] + koff, 0) : make_uint4(0, 0, 0, 0);
-}
-__device__ __forceinline__ void store_stage(const Stage& s, uint8_t* tile, const OperandMap& m) {
-#pragma unroll
-    for (int q = 0; q < kChunks; ++q) *reinterpret_cast<uint4*>(tile + m.st[q]) = s.v[q];
-}
-
-// v_mfma_f32_32x32x16_bf16 operand for 32 rows at k16 block kk: lane L holds row
-// L % 32 and k 8 (L / 32) .. +7.
-__device__ __forceinline__ bf16x8_t frag_kmaj(const uint8_t* tile, uint32_t fr, int kk) {
-    return *reinterpret_cast<const bf16x8_t*>(tile + fr + kk * 32);
-}
 // Two transposed reads, k rows kb .. kb + 3 and kb + 4 .. kb + 7 (512 B apart per k row).
 __device__ __forceinline__ bf16x8_t frag_mnmaj(const uint8_t* tile, uint32_t fr, int kk) {
     typedef s16x4_t __attribute__((address_space(3))) * lds_v4;
@@ -321,7 +220,7 @@ __device__ __forceinline__ void load_bf16x4(const uint16_t* p, float* o) {
 // bank groups.
 constexpr int kEpRows = 128;
 constexpr int kEpPitchF = 256 + 4;   // floats per staged row
-static_assert(kEpRows * kEpPitchF * 4 <= 2 * kStageBytes, "epilogue staging must fit in the stage buffers");
+constexpr int kEpBytes = kEpRows * kEpPitchF * 4;
 
 __device__ __forceinline__ float4 lds_f4(const float* ep, int r, int x) {
     return *reinterpret_cast<const float4*>(ep + r * kEpPitchF + x);
@@ -443,241 +342,6 @@ __device__ __forceinline__ void interleave_reads() {
     }
 }
 
-template <int MODE, int EPI>
-__global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
-    __shared__ __align__(16) uint8_t lds[2 * kStageBytes];
-    Tile t;
-    if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
-    // The tile is the same for every lane; say so, so that pointers and buffer
-    // descriptors derived from it live in scalar registers.
-    t.g = __builtin_amdgcn_readfirstlane(t.g);
-    t.x0 = __builtin_amdgcn_readfirstlane(t.x0);
-    t.x_lim = __builtin_amdgcn_readfirstlane(t.x_lim);
-    t.y0 = __builtin_amdgcn_readfirstlane(t.y0);
-    t.y_lim = __builtin_amdgcn_readfirstlane(t.y_lim);
-    t.row0 = __builtin_amdgcn_readfirstlane(static_cast<int>(t.row0));
-    t.k_begin = __builtin_amdgcn_readfirstlane(t.k_begin);
-    t.k_end = __builtin_amdgcn_readfirstlane(t.k_end);
-    const int g = t.g;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wx = wave & 1, wy = wave >> 1;
-    // X is K-major for FWD (weights [N, K]) and MN-major otherwise; Y is K-major
-    // except for WGRAD.
-    constexpr bool kXK = MODE == kFwd;
-    constexpr bool kYK = MODE != kWgrad;
-
-    const uint16_t* A = static_cast<const uint16_t*>(p.a[g]);
-    const uint16_t* B = static_cast<const uint16_t*>(p.b[g]);
-    const uint32_t ldb = static_cast<uint32_t>(p.ldb), lda = static_cast<uint32_t>(p.lda);
-    __amdgpu_buffer_rsrc_t rx, ry;
-    OperandMap mx, my;
-    if (MODE == kWgrad) {
-        const int64_t rows = t.k_end;   // group rows; reads past them return zero
-        rx = make_rsrc(B + t.row0 * p.ldb, rows * p.ldb * 2);
-        ry = make_rsrc(A + t.row0 * p.lda, rows * p.lda * 2);
-        map_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
-        map_mnmaj(my, lda, t.y0, t.y_lim, wy * kWaveY, kFragY);
-    } else {
-        ry = make_rsrc(A + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda * 2);
-        const int y_last = t.y_lim - 1;
-        map_kmaj(my, lda, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
-        if (MODE == kFwd) {
-            rx = make_rsrc(B, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb * 2);
-            map_kmaj(mx, ldb, wx * 128, 4, [&](int r) {
-                if (EPI == kEpiSwigluFwd) {
-                    // 256 weight rows = [gate 64 | up 64] for each half of 128 activation columns.
-                    const int half = r >> 7, qq = r & 127;
-                    int col = t.x0 + half * 64 + (qq & 63);
-                    col = col < p.f ? col : 0;
-                    return qq < 64 ? col : p.f + col;
-                }
-                const int n = t.x0 + r;
-                return n < p.N ? n : 0;
-            });
-        } else {
-            rx = make_rsrc(B, static_cast<int64_t>(p.K) * p.ldb * 2);
-            map_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
-        }
-    }
-
-    auto issue = [&, rx, ry](Stage& sx, Stage& sy, int k0) {
-        if (kXK) load_kmaj(sx, rx, mx, k0);
-        else load_mnmaj(sx, rx, mx, ldb, k0);
-        if (kYK) load_kmaj(sy, ry, my, k0);
-        else load_mnmaj(sy, ry, my, lda, k0);
-    };
-    auto commit = [&](const Stage& sx, const Stage& sy, int stage) {
-        uint8_t* xt = lds + stage * kStageBytes;
-        store_stage(sx, xt, mx);
-        store_stage(sy, xt + kTileBytes, my);
-    };
-
-    f32x16_t acc[4][kFragY];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < kFragY; ++j) acc[i][j] = f32x16_t{};
-
-    auto compute = [&](int stage) {
-        const uint8_t* xt = lds + stage * kStageBytes;
-        const uint8_t* yt = xt + kTileBytes;
-#pragma unroll
-        for (int kk = 0; kk < kKStep / 16; ++kk) {
-            bf16x8_t xf[4], yf[kFragY];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) xf[i] = kXK ? frag_kmaj(xt, mx.fr[i], kk) : frag_mnmaj(xt, mx.fr[i], kk);
-#pragma unroll
-            for (int j = 0; j < kFragY; ++j) yf[j] = kYK ? frag_kmaj(yt, my.fr[j], kk) : frag_mnmaj(yt, my.fr[j], kk);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < kFragY; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[i], yf[j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    const int nk = (t.k_end - t.k_begin + kKStep - 1) / kKStep;
-#if RHP_GG_PREFETCH == 3
-    // One staging set, and MFMA fragments double-buffered in registers: the
-    // fragments of k16 block kk + 1 are read from LDS while the MFMAs of block
-    // kk run, and block 0 of the next stage is read right after the barrier.
-    typedef bf16x8_t FragSet[4 + kFragY];
-    auto read_frags = [&](FragSet& f, int stage, int kk) {
-        const uint8_t* xt = lds + stage * kStageBytes;
-        const uint8_t* yt = xt + kTileBytes;
-        // Y fragments first: every MFMA of a block uses one, so the next
-        // block's Y reads need registers of their own and are issued early.
-#pragma unroll
-        for (int j = 0; j < kFragY; ++j) f[4 + j] = kYK ? frag_kmaj(yt, my.fr[j], kk) : frag_mnmaj(yt, my.fr[j], kk);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = kXK ? frag_kmaj(xt, mx.fr[i], kk) : frag_mnmaj(xt, mx.fr[i], kk);
-    };
-    auto mfmas = [&](const FragSet& f) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < kFragY; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[4 + j], acc[i][j], 0, 0, 0);
-    };
-    constexpr int kReads = (kXK ? 4 : 8) + (kYK ? kFragY : 2 * kFragY);   // LDS read instructions per block
-    Stage sx, sy;
-    FragSet fa, fb;
-    if (nk > 0) {
-        issue(sx, sy, t.k_begin);
-        commit(sx, sy, 0);
-    }
-    __syncthreads();
-    if (nk > 0) read_frags(fa, 0, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) issue(sx, sy, t.k_begin + (kt + 1) * kKStep);
-#pragma unroll
-        for (int kk = 0; kk < kKStep / 16; kk += 2) {
-            read_frags(fb, cur, kk + 1);
-            mfmas(fa);
-            interleave_reads<0, 4 * kFragY, kReads>();
-            if (kk + 2 < kKStep / 16) {
-                read_frags(fa, cur, kk + 2);
-                mfmas(fb);
-                interleave_reads<0, 4 * kFragY, kReads>();
-            } else {
-                mfmas(fb);
-            }
-        }
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        if (more) commit(sx, sy, cur ^ 1);
-        __syncthreads();
-        if (more) read_frags(fa, cur ^ 1, 0);
-    }
-#elif RHP_GG_PREFETCH == 1
-    // One staging set: the loads of step kt + 1 are in flight during step kt.
-    Stage sx, sy;
-    if (nk > 0) {
-        issue(sx, sy, t.k_begin);
-        commit(sx, sy, 0);
-    }
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) issue(sx, sy, t.k_begin + (kt + 1) * kKStep);
-        compute(cur);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        if (kt + 1 < nk) commit(sx, sy, cur ^ 1);
-        __syncthreads();
-    }
-#else
-    // Two staging sets: the loads of step kt + 2 are in flight during step kt.
-    Stage s0x, s0y, s1x, s1y;
-    if (nk > 0) issue(s0x, s0y, t.k_begin);
-    if (nk > 1) issue(s1x, s1y, t.k_begin + kKStep);
-    if (nk > 0) commit(s0x, s0y, 0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt += 2) {
-        if (kt + 2 < nk) issue(s0x, s0y, t.k_begin + (kt + 2) * kKStep);
-        compute(0);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        if (kt + 1 < nk) commit(s1x, s1y, 1);
-        __syncthreads();
-        if (kt + 1 >= nk) break;
-        if (kt + 3 < nk) issue(s1x, s1y, t.k_begin + (kt + 3) * kKStep);
-        compute(1);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        if (kt + 2 < nk) commit(s0x, s0y, 0);
-        __syncthreads();
-    }
-#endif
-
-    epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane);
-}
-
-// ------------------------------------------------------------------ MFMA kernel, direct HBM -> LDS loads
-//
-// Same tiles, wave layout, fragments and epilogue as gg_bf16_kernel, but the
-// operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds
-// (no staging registers, no LDS stores), K step 32, kDmaStages LDS stages.
-// One such load moves 64 lanes x 16 bytes into 1 KB of LDS at M0 + 16 * lane,
-// so a stage is built from 1 KB blocks whose lanes pick the global chunk that
-// belongs at their LDS position.
-//
-//   K-major tile  [256 rows][32 k], 64-byte rows, chunk c of row r at position
-//                 c ^ ((r >> 2) & 3): the 16 rows of one ds_read_b128 hit 16
-//                 distinct 16-byte bank slots.
-//   MN-major tile [32 k][256 mn], 512-byte rows, chunk c at c ^ 4 (k & 3) (as above).
-//
-// Pipeline (S = kDmaStages): the loads of step kt + S - 1 are issued right
-// after the barrier that opens step kt.  That barrier also guarantees that
-// the stages of steps kt and kt + 1 are complete, so the fragments of step
-// kt + 1's first k16 block are read during step kt's second block and no wave
-// waits on LDS after a barrier.  Stage (kt - 1) mod S, which the new loads
-// overwrite, was last read before that barrier.
-//
-// The loads are written as inline assembly so that the compiler, which does
-// not see them, does not make every LDS read wait for all of them; the code
-// counts them itself (s_waitcnt vmcnt) before each barrier.
-
-#ifndef RHP_GG_DMA
-#define RHP_GG_DMA 1
-#endif
-#ifndef RHP_GG_STAGES
-#define RHP_GG_STAGES 4
-#endif
-constexpr int kDmaK = 32;
-constexpr int kDmaStages = RHP_GG_STAGES;
-constexpr int kDmaTileBytes = kTile * kDmaK * 2;          // 16 KB per operand
-constexpr int kDmaStageBytes = 2 * kDmaTileBytes;         // X + Y
-constexpr int kDmaBlocks = kDmaTileBytes / 1024;          // 1 KB blocks per operand
-constexpr int kDmaPerWave = kDmaBlocks / kWaves;          // loads per wave per operand per step
-constexpr int kDmaPerStep = 2 * kDmaPerWave;              // loads per wave per step
-constexpr int kDmaLdsBytes = kDmaStages * kDmaStageBytes > kEpRows * kEpPitchF * 4 ? kDmaStages * kDmaStageBytes
-                                                                                    : kEpRows * kEpPitchF * 4;
-static_assert(kDmaStages >= 3 && kDmaLdsBytes <= 163840, "3 to 5 stages of 32 KB");
-static_assert(kDmaBlocks % kWaves == 0, "whole loads per wave");
 constexpr uint32_t kOutOfRange = 0x80000000u;             // a buffer offset past every view: reads zero
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
@@ -702,6 +366,29 @@ __device__ __forceinline__ void dma16(const Rsrc& r, uint32_t voff, uint32_t sof
                    "s"(__builtin_amdgcn_readfirstlane(lds))
                  : "memory");
 }
+
+// ------------------------------------------------------------------ K step 32, four stages
+//
+// K-major tile [256 rows][32 k], 64-byte rows, chunk c of row r at position
+// c ^ ((r >> 2) & 3).  MN-major tile [32 k][256 mn].
+//
+// Pipeline (S = 4 stages): the loads of step kt + S - 1 are issued during step
+// kt, after the barrier that opens it.  That barrier also guarantees that the
+// stages of steps kt and kt + 1 are complete, so the fragments of step kt + 1's
+// first k16 block are read during step kt's second block and no wave waits on
+// LDS after a barrier.  Stage (kt - 1) mod S, which the new loads overwrite,
+// was last read before that barrier.
+
+constexpr int kDmaK = 32;
+constexpr int kDmaStages = 4;
+constexpr int kDmaTileBytes = kTile * kDmaK * 2;          // 16 KB per operand
+constexpr int kDmaStageBytes = 2 * kDmaTileBytes;         // X + Y
+constexpr int kDmaPerWave = kDmaTileBytes / 1024 / kWaves;   // loads per wave per operand per step
+constexpr int kDmaPerStep = 2 * kDmaPerWave;              // loads per wave per step
+constexpr int kDmaLdsBytes = kDmaStages * kDmaStageBytes > kEpBytes ? kDmaStages * kDmaStageBytes : kEpBytes;
+static_assert(kDmaLdsBytes <= 163840, "LDS per workgroup");
+static_assert(kDmaPerWave == 2, "one load pair per k16 block");
+
 // Wait until at most n steps' worth of this wave's loads are still in flight.
 __device__ __forceinline__ void wait_dma_steps(int n) {
     static_assert(2 * kDmaPerStep < 64, "vmcnt field");
@@ -758,7 +445,7 @@ __device__ __forceinline__ void dmap_mnmaj(DmaMap& m, uint32_t ld, int mn0, int 
 }
 
 template <int MODE, int EPI>
-__global__ __launch_bounds__(kThreadsMfma) void gg_bf16_dma_kernel(Params p) {
+__global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k32_kernel(Params p) {
     __shared__ __align__(1024) uint8_t lds[kDmaLdsBytes];
     Tile t;
     if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
@@ -811,17 +498,18 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_dma_kernel(Params p) {
     }
 
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-    auto issue = [&](int step, int stage) {
+    // Load j of both operands of one step.
+    auto issue_part = [&](int step, int stage, int j) {
         const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kDmaK);
-        const uint32_t base = lds0 + stage * kDmaStageBytes + wave * 1024;
-#pragma unroll
-        for (int j = 0; j < kDmaPerWave; ++j) {
-            const uint32_t at = base + j * kWaves * 1024;
-            if (kXK) dma16(rx, mx.vo[j], k0 * 2u, at);
-            else dma16(rx, mx.vo[j] + k0 * ldb * 2u, 0, at);
-            if (kYK) dma16(ry, my.vo[j], k0 * 2u, at + kDmaTileBytes);
-            else dma16(ry, my.vo[j] + k0 * lda * 2u, 0, at + kDmaTileBytes);
-        }
+        const uint32_t at = lds0 + stage * kDmaStageBytes + wave * 1024 + j * kWaves * 1024;
+        if (kXK) dma16(rx, mx.vo[j], k0 * 2u, at);
+        else dma16(rx, mx.vo[j] + k0 * ldb * 2u, 0, at);
+        if (kYK) dma16(ry, my.vo[j], k0 * 2u, at + kDmaTileBytes);
+        else dma16(ry, my.vo[j] + k0 * lda * 2u, 0, at + kDmaTileBytes);
+    };
+    auto issue = [&](int step, int stage) {
+        issue_part(step, stage, 0);
+        issue_part(step, stage, 1);
     };
 
     f32x16_t acc[4][kFragY];
@@ -859,6 +547,10 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_dma_kernel(Params p) {
     };
 
     const int nk = (t.k_end - t.k_begin + kDmaK - 1) / kDmaK;
+    // A wave whose Y rows all lie past the tile's valid rows (the partial last
+    // tile of a group) only loads its share and joins the barriers; its SIMD
+    // then runs the other wave's MFMAs alone.
+    const bool idle = wy * kWaveY >= t.y_lim;
     FragSet fa, fb;
     if (nk > 0) {
 #pragma unroll
@@ -866,16 +558,29 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_dma_kernel(Params p) {
             if (s < nk) issue(s, s);
         wait_dma_steps(min(kDmaStages - 2, nk - 1) - min(1, nk - 1));
         barrier();
-        read_frags(fa, 0, 0);
+        if (!idle) read_frags(fa, 0, 0);
     }
     int stage = 0, next = 1 % kDmaStages, fill = kDmaStages - 1;   // stages of steps kt, kt + 1, kt + S - 1
+    if (idle) {
+        for (int kt = 0; kt < nk; ++kt) {
+            if (kt + kDmaStages - 1 < nk) issue(kt + kDmaStages - 1, fill);
+            wait_dma_steps(min(kt + kDmaStages - 1, nk - 1) - min(kt + 2, nk - 1));
+            barrier();
+            fill = fill + 1 == kDmaStages ? 0 : fill + 1;
+        }
+    }
     // The body is the same for every step (the last one reads a stale block
     // it does not use), so the accumulators never need copies between paths.
-    for (int kt = 0; kt < nk; ++kt) {
-        if (kt + kDmaStages - 1 < nk) issue(kt + kDmaStages - 1, fill);
+    for (int kt = 0; kt < (idle ? 0 : nk); ++kt) {
+        // The step's loads are spread over its two k16 blocks, so the memory
+        // pipeline never holds a wave's whole burst in front of its MFMAs.
+        const bool more_dma = kt + kDmaStages - 1 < nk;
+        if (more_dma) issue_part(kt + kDmaStages - 1, fill, 0);
         read_frags(fb, stage, 1);
         mfmas(fa);
         interleave_reads<0, 4 * kFragY, kReads>();
+        __builtin_amdgcn_sched_barrier(0);
+        if (more_dma) issue_part(kt + kDmaStages - 1, fill, 1);
         read_frags(fa, next, 0);
         mfmas(fb);
         interleave_reads<0, 4 * kFragY, kReads>();
@@ -892,6 +597,201 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_dma_kernel(Params p) {
     epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane);
 }
 
+// ------------------------------------------------------------------ K step 64, two stages
+//
+// K-major tile [256 rows][64 k], 128-byte rows, chunk c of row r at position
+// c ^ ((r >> 1) & 7): the 16 rows of one ds_read_b128 hit 16 distinct bank
+// slots, and a lane's offset for k16 block b is its block-0 offset XOR 32 b.
+// MN-major tile [64 k][256 mn].
+//
+// Pipeline: the loads of step kt + 1 are issued right after the barrier that
+// opens step kt and waited for before the barrier that closes it.  That
+// barrier comes before the MFMAs of the last k16 block, so those MFMAs cover
+// the LDS latency of the next stage's first block.
+
+constexpr int kK64 = 64;
+constexpr int kT64Bytes = kTile * kK64 * 2;                // 32 KB per operand
+constexpr int kS64Bytes = 2 * kT64Bytes;                   // X + Y
+constexpr int kD64PerWave = kT64Bytes / 1024 / kWaves;     // loads per wave per operand per step
+constexpr int kLds64Bytes = 2 * kS64Bytes > kEpBytes ? 2 * kS64Bytes : kEpBytes;
+static_assert(kLds64Bytes <= 163840, "two 64 KB stages");
+static_assert((kT64Bytes / 1024) % kWaves == 0, "whole loads per wave");
+
+__device__ __forceinline__ uint32_t k64_off(int row, int chunk) {
+    return static_cast<uint32_t>(row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4));
+}
+
+struct Dma64Map {
+    uint32_t vo[kD64PerWave];
+    uint32_t fr[4];   // K-major: block-0 offset (block b: XOR 32 b); MN-major: block-0 offset (block b: + 8192 b)
+};
+
+template <class RowOf>
+__device__ __forceinline__ void d64_kmaj(Dma64Map& m, uint32_t ld, int frag_row0, int nfrag, RowOf src_row) {
+    const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < kD64PerWave; ++j) {
+        const int row = (j * kWaves + w) * 8 + (L >> 3);
+        const int chunk = (L & 7) ^ ((row >> 1) & 7);
+        m.vo[j] = (static_cast<uint32_t>(src_row(row)) * ld + chunk * 8) * 2u;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m.fr[i] = i < nfrag ? k64_off(frag_row0 + i * 32 + (L & 31), L >> 5) : 0;
+}
+
+__device__ __forceinline__ void d64_mnmaj(Dma64Map& m, uint32_t ld, int mn0, int mn_lim, int frag_row0, int nfrag) {
+    const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < kD64PerWave; ++j) {
+        const int k = (j * kWaves + w) * 2 + (L >> 5);
+        const int chunk = (L & 31) ^ ((k & 3) << 2);
+        m.vo[j] = chunk * 8 < mn_lim ? (static_cast<uint32_t>(k) * ld + static_cast<uint32_t>(mn0 + chunk * 8)) * 2u
+                                     : kOutOfRange;
+    }
+    const int g = L >> 4, r = L & 15;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        m.fr[i] = i < nfrag ? mnmaj_off(8 * (g >> 1) + (r >> 2), frag_row0 + i * 32 + 16 * (g & 1) + 4 * (r & 3)) : 0;
+}
+
+template <int MODE, int EPI>
+__global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k64_kernel(Params p) {
+    __shared__ __align__(1024) uint8_t lds[kLds64Bytes];
+    Tile t;
+    if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
+    t.g = __builtin_amdgcn_readfirstlane(t.g);
+    t.x0 = __builtin_amdgcn_readfirstlane(t.x0);
+    t.x_lim = __builtin_amdgcn_readfirstlane(t.x_lim);
+    t.y0 = __builtin_amdgcn_readfirstlane(t.y0);
+    t.y_lim = __builtin_amdgcn_readfirstlane(t.y_lim);
+    t.row0 = __builtin_amdgcn_readfirstlane(static_cast<int>(t.row0));
+    t.k_begin = __builtin_amdgcn_readfirstlane(t.k_begin);
+    t.k_end = __builtin_amdgcn_readfirstlane(t.k_end);
+    const int g = t.g;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wx = wave & 1, wy = wave >> 1;
+    constexpr bool kXK = MODE == kFwd;
+    constexpr bool kYK = MODE != kWgrad;
+
+    const uint16_t* A = static_cast<const uint16_t*>(p.a[g]);
+    const uint16_t* B = static_cast<const uint16_t*>(p.b[g]);
+    const uint32_t ldb = static_cast<uint32_t>(p.ldb), lda = static_cast<uint32_t>(p.lda);
+    Rsrc rx, ry;
+    Dma64Map mx, my;
+    if (MODE == kWgrad) {
+        const int64_t rows = t.k_end;   // group rows; reads past them return zero
+        rx = make_dma_rsrc(B + t.row0 * p.ldb, rows * p.ldb * 2);
+        ry = make_dma_rsrc(A + t.row0 * p.lda, rows * p.lda * 2);
+        d64_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
+        d64_mnmaj(my, lda, t.y0, t.y_lim, wy * kWaveY, kFragY);
+    } else {
+        ry = make_dma_rsrc(A + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda * 2);
+        const int y_last = t.y_lim - 1;
+        d64_kmaj(my, lda, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
+        if (MODE == kFwd) {
+            rx = make_dma_rsrc(B, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb * 2);
+            d64_kmaj(mx, ldb, wx * 128, 4, [&](int r) {
+                if (EPI == kEpiSwigluFwd) {
+                    // 256 weight rows = [gate 64 | up 64] for each half of 128 activation columns.
+                    const int half = r >> 7, qq = r & 127;
+                    int col = t.x0 + half * 64 + (qq & 63);
+                    col = col < p.f ? col : 0;
+                    return qq < 64 ? col : p.f + col;
+                }
+                const int n = t.x0 + r;
+                return n < p.N ? n : 0;
+            });
+        } else {
+            rx = make_dma_rsrc(B, static_cast<int64_t>(p.K) * p.ldb * 2);
+            d64_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
+        }
+    }
+
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+    auto issue = [&](int step, int stage) {
+        const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kK64);
+        const uint32_t base = lds0 + stage * kS64Bytes + wave * 1024;
+#pragma unroll
+        for (int j = 0; j < kD64PerWave; ++j) {
+            const uint32_t at = base + j * kWaves * 1024;
+            if (kXK) dma16(rx, mx.vo[j], k0 * 2u, at);
+            else dma16(rx, mx.vo[j] + k0 * ldb * 2u, 0, at);
+            if (kYK) dma16(ry, my.vo[j], k0 * 2u, at + kT64Bytes);
+            else dma16(ry, my.vo[j] + k0 * lda * 2u, 0, at + kT64Bytes);
+        }
+    };
+
+    f32x16_t acc[4][kFragY];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < kFragY; ++j) acc[i][j] = f32x16_t{};
+
+    typedef bf16x8_t FragSet[4 + kFragY];
+    auto kfrag = [](const uint8_t* tile, uint32_t fr, int b) {
+        return *reinterpret_cast<const bf16x8_t*>(tile + (fr ^ static_cast<uint32_t>(b << 5)));
+    };
+    auto read_frags = [&](FragSet& f, int stage, int b) {
+        const uint8_t* xt = lds + stage * kS64Bytes;
+        const uint8_t* yt = xt + kT64Bytes;
+#pragma unroll
+        for (int j = 0; j < kFragY; ++j)
+            f[4 + j] = kYK ? kfrag(yt, my.fr[j], b) : frag_mnmaj(yt, my.fr[j], b);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[i] = kXK ? kfrag(xt, mx.fr[i], b) : frag_mnmaj(xt, mx.fr[i], b);
+    };
+    auto mfmas = [&](const FragSet& f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < kFragY; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[4 + j], acc[i][j], 0, 0, 0);
+    };
+    constexpr int kReads = (kXK ? 4 : 8) + (kYK ? kFragY : 2 * kFragY);
+
+    const int nk = (t.k_end - t.k_begin + kK64 - 1) / kK64;
+    // A wave whose Y rows all lie past the tile's valid rows only loads its
+    // share and joins the barriers.
+    const bool idle = wy * kWaveY >= t.y_lim;
+    FragSet fa, fb;
+    if (nk > 0) {
+        issue(0, 0);
+        wait_dma_steps(0);
+        __syncthreads();
+        if (!idle) read_frags(fa, 0, 0);
+    }
+    if (idle) {
+        for (int kt = 0; kt < nk; ++kt) {
+            if (kt + 1 < nk) issue(kt + 1, (kt & 1) ^ 1);
+            wait_dma_steps(0);
+            __syncthreads();
+        }
+    }
+    // Same body for every step (the last one reads a stale block it does not
+    // use), so the accumulators never need copies between paths.
+    for (int kt = 0; kt < (idle ? 0 : nk); ++kt) {
+        const int st = kt & 1;
+        if (kt + 1 < nk) issue(kt + 1, st ^ 1);
+        read_frags(fb, st, 1);
+        mfmas(fa);
+        interleave_reads<0, 4 * kFragY, kReads>();
+        read_frags(fa, st, 2);
+        mfmas(fb);
+        interleave_reads<0, 4 * kFragY, kReads>();
+        read_frags(fb, st, 3);
+        mfmas(fa);
+        interleave_reads<0, 4 * kFragY, kReads>();
+        // The loads of step kt + 1 have landed in every wave's share and no wave
+        // still reads stage st (its block-3 reads complete before the barrier).
+        wait_dma_steps(0);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        read_frags(fa, st ^ 1, 0);
+        mfmas(fb);
+        interleave_reads<0, 4 * kFragY, kReads>();
+    }
+    epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane);
+}
 // ------------------------------------------------------------------ generic kernel (any dtype)
 
 // One thread per 4 outputs of a 32 x 32 tile, reading operands straight from
@@ -989,11 +889,11 @@ template <int MODE, int EPI>
 void launch_one(const Job& j, const Params& p, hipStream_t s) {
     if (j.mfma) {
         const unsigned nb = mfma_blocks<MODE, EPI>(p, j.rows_cap);
-#if RHP_GG_DMA
-        if (nb) hipLaunchKernelGGL((gg_bf16_dma_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
-#else
-        if (nb) hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
-#endif
+        if (!nb) return;
+        if constexpr (MODE == kFwd)
+            hipLaunchKernelGGL((gg_bf16_k64_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+        else
+            hipLaunchKernelGGL((gg_bf16_k32_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
         return;
     }
     const unsigned nb = simt_blocks<MODE>(p, j.rows_cap);
