@@ -213,6 +213,63 @@ int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_offsets, int
                        int h, int f, const void* const* dhpre, const void* const* xp, const void* const* w1,
                        void* const* dxp, void* const* dw1, hipStream_t stream);
 
+/* ------------------------------------------------------------------ fp8 experts (delayed scaling) */
+
+/*
+ * FP8 expert GEMMs with per-tensor delayed scaling.  The reference keeps an
+ * FP8-style amax history per layer (resihp/runtime/reference_model.py:44-46,
+ * 204-207): a buffer of hist_len entries, the iteration's amax prepended
+ * newest-first when the iteration ends (:212-216).  Here every quantised
+ * tensor (the expert-input rows, the SwiGLU output rows, their gradients and
+ * each expert weight) has such a history (float32 [hist_len]) and a pending
+ * amax (uint32 holding float bits, reset to 0 by the roll).
+ *
+ * Scale of a cast: fp8_max / max(history) / 2^margin (1 if that maximum is not
+ * a positive finite number); q = fp8(clamp(x * scale, -fp8_max, fp8_max)),
+ * round to nearest even, OCP e4m3 (max 448) or e5m2 (max 57344).
+ */
+
+/* poff[g+1] = poff[g] + roundup(offsets[g+1] - offsets[g], align); align a multiple of 128. */
+int rhp_fp8_padded_offsets(const int32_t* offsets, int G, int align, int32_t* poff, hipStream_t stream);
+
+/*
+ * Cast bf16 rows to fp8 (fmt RHP_E4M3 or RHP_E5M2) with the scale of `history`:
+ *   x:   [rows, cols] bf16, row pitch ldx; expert g owns rows [offsets[g], offsets[g+1])
+ *   q:   row-major fp8 copy [rows, cols] (row pitch cols), or NULL
+ *   qt:  transposed copy per expert, [cols, R_g] at qt + cols * poff[g] with
+ *        R_g = poff[g+1] - poff[g]; rows past the expert's count are zero; or NULL
+ * Raises *amax_bits to max |x| over the cast rows (float bits, atomic max) and
+ * writes *scale_inv = 1 / scale.  cols must be a multiple of 64; rows_cap
+ * bounds offsets[G] - offsets[0].
+ */
+int rhp_fp8_cast(const void* x, int x_dtype, int64_t ldx, int cols, int G, const int32_t* offsets,
+                 const int32_t* poff, int64_t rows_cap, const float* history, int hist_len, int fmt, int margin,
+                 uint32_t* amax_bits, float* scale_inv, void* q, void* qt, hipStream_t stream);
+
+/* End of iteration for n tensors: history[i] = [amax_i, history[i][0 .. hist_len-2]], amax_i = 0 (reference_model.py:215). */
+int rhp_fp8_amax_roll(float* history, uint32_t* amax_bits, int n, int hist_len, hipStream_t stream);
+
+/*
+ * Grouped fp8 product, bf16 output, with the epilogues of the bf16 entry points.
+ * Replaces the expert FFN products of resihp/runtime/moe.py:82-83 and their
+ * autograd backward when the experts run in fp8.  Both operands have K
+ * contiguous ("NT"); the result is multiplied by y_scale_inv[0] * x_scale_inv[g * x_scale_stride].
+ *   kgroups = 0: out[r, n] = sum_k y[g][r, k] x[g][n, k] for the rows r of expert g
+ *                (offsets; y[g] holds all rows, row pitch ldy; x[g]: [N or 2f, K], pitch ldx).
+ *                epi: 0 store, 1 SwiGLU forward (x rows [gate; up], out = hpre [.., 2f], c2 = act,
+ *                N = f), 2 GELU forward (c2 = act), 3 SwiGLU backward, 4 GELU backward
+ *                (aux = hpre); K a multiple of 128.
+ *   kgroups = 1: out_g[o, n] = sum_t y_g[o, t] x_g[n, t] over the R_g padded rows of expert g,
+ *                with y_g = y[0] + Mo * poff[g], x_g = x[0] + N * poff[g] (the qt copies of
+ *                rhp_fp8_cast; offsets = poff), row pitch R_g; epi must be 0.
+ * y_fmt is the format of y, x_fmt of x (RHP_E4M3 / RHP_E5M2); x must be e4m3.
+ * Outputs c[g] (and c2[g]) are bf16 with row pitches ldc (ldc2).
+ */
+int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt, int x_fmt, int N,
+                 int K, int Mo, int f, const void* const* y, int64_t ldy, const void* const* x, int64_t ldx,
+                 void* const* c, int64_t ldc, void* const* c2, int64_t ldc2, const void* const* aux, int64_t ldaux,
+                 const float* y_scale_inv, const float* x_scale_inv, int x_scale_stride, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,513 @@
+// FP8 expert GEMMs with per-tensor delayed scaling, for gfx950.
+//
+// Reference: the FP8-style amax history of resihp/runtime/reference_model.py
+// (buffer of L entries initialised by the caller, the iteration's amax
+// prepended newest-first at :215, the pending amax reset), applied to the
+// expert FFN of resihp/runtime/moe.py:82-83.  The quantisation recipe is this
+// library's: scale = fp8_max / max(history) / 2^margin (1 when the history
+// holds no positive finite value); q = fp8(clamp(x * scale, -max, max)) with
+// round-to-nearest-even, OCP e4m3 (max 448) for weights and activations,
+// e5m2 (max 57344) for gradients.
+//
+// Every fp8 GEMM is "NT": both operands have K as their contiguous
+// dimension.  The cast kernel writes, besides the row-major fp8 copy, a
+// transposed copy per expert ([cols][rows], rows padded to a multiple of 128
+// with zeros), so the backward GEMMs read K-contiguous operands as well:
+//   fc1 fwd    y[t, n]  = sum_k xq[t, k]  w1q[n, k]      K = h
+//   fc2 fwd    y[t, n]  = sum_k aq[t, k]  w2q[n, k]      K = f
+//   fc2 dgrad  y[t, n]  = sum_k dyq[t, k] w2qT[n, k]     K = h
+//   fc1 dgrad  y[t, n]  = sum_k dhq[t, k] w1qT[n, k]     K = 2f
+//   wgrad      dW[o, i] = sum_t gT[o, t]  vT[i, t]       K = padded rows of the expert
+// The MFMA is v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales; the
+// per-tensor scales are divided out in the epilogue, which then runs the same
+// SwiGLU / GELU / store code as the bf16 kernels (bf16 outputs).
+#include "gemm_common.h"
+
+namespace rhp {
+namespace {
+
+constexpr int kFmtE4m3 = 0;   // MFMA operand format codes (cbsz / blgp)
+constexpr int kFmtE5m2 = 1;
+
+__host__ __device__ constexpr float fp8_max(int fmt) { return fmt == kFmtE4m3 ? 448.0f : 57344.0f; }
+
+// scale = fp8_max / max(history) / 2^margin, evaluated in double and rounded
+// once to float; 1 when the maximum is not a positive finite number.
+__device__ __forceinline__ float history_scale(const float* hist, int L, float fmax, int margin) {
+    float a = -__builtin_huge_valf();
+    bool nan = false;
+    for (int i = 0; i < L; ++i) {
+        const float v = hist[i];
+        nan |= v != v;
+        a = v > a ? v : a;
+    }
+    if (nan || !(a > 0.0f) || a == __builtin_huge_valf()) return 1.0f;
+    return static_cast<float>(static_cast<double>(fmax) / static_cast<double>(a) / __builtin_ldexp(1.0, margin));
+}
+
+template <int FMT>
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
+    uint32_t w;
+    if (FMT == kFmtE4m3) {
+        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
+        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(w), true));
+    } else {
+        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false));
+        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(c, d, static_cast<int>(w), true));
+    }
+    return w;
+}
+
+// ------------------------------------------------------------------ cast + transpose
+
+struct CastParams {
+    const uint16_t* x;        // bf16 rows
+    int64_t ldx;              // elements
+    int cols;                 // multiple of 64
+    int G;
+    const int32_t* offsets;   // [G + 1] rows of each expert in x and q
+    const int32_t* poff;      // [G + 1] padded rows (multiples of 128) of each expert in qt
+    const float* hist;
+    int L, margin;
+    uint32_t* amax_bits;      // running max of |x| (float bits), updated with atomicMax
+    float* scale_inv;         // 1 / scale, written once
+    uint8_t* q;               // [rows][cols] or null
+    uint8_t* qt;              // expert g: [cols][R_g] at qt + cols * poff[g], or null
+};
+
+constexpr int kCastTile = 64;
+
+// One block: 64 rows x 64 columns of one expert; thread t covers row t / 4 and
+// 16 columns.  Rows past the expert's count quantise to zero (qt padding).
+template <int FMT>
+__global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
+    __shared__ uint8_t tr[kCastTile][kCastTile + 16];
+    __shared__ float wave_max[4];
+    const int ct_n = c.cols / kCastTile;
+    uint32_t b = blockIdx.x;
+    int g = 0, rt = 0, ct = 0, count = 0, rpad = 0;
+    bool found = false;
+    for (; g < c.G; ++g) {
+        count = c.offsets[g + 1] - c.offsets[g];
+        rpad = c.poff[g + 1] - c.poff[g];
+        const uint32_t n = static_cast<uint32_t>(rpad / kCastTile) * ct_n;
+        if (b < n) {
+            rt = b / ct_n;
+            ct = b % ct_n;
+            found = true;
+            break;
+        }
+        b -= n;
+    }
+    const float scale = history_scale(c.hist, c.L, fp8_max(FMT), c.margin);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *c.scale_inv = 1.0f / scale;
+    if (!found) return;
+
+    const int t = threadIdx.x, r = t >> 2, cs = (t & 3) * 16;
+    const int row = rt * kCastTile + r;                 // relative to the expert
+    const int col = ct * kCastTile + cs;
+    const bool valid = row < count;
+    float v[16];
+    if (valid) {
+        const uint4* src = reinterpret_cast<const uint4*>(c.x + (c.offsets[g] + row) * c.ldx + col);
+        const uint4 u0 = src[0], u1 = src[1];
+        const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    const float lim = fp8_max(FMT);
+    uint32_t packed[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = fminf(fmaxf(v[4 * i + e] * scale, -lim), lim);
+        packed[i] = pack4<FMT>(y[0], y[1], y[2], y[3]);
+    }
+    if (valid && c.q)
+        *reinterpret_cast<uint4*>(c.q + (static_cast<int64_t>(c.offsets[g]) + row) * c.cols + col) =
+            make_uint4(packed[0], packed[1], packed[2], packed[3]);
+
+    // amax: wave maximum, then one atomic per block (non-negative floats order like their bits)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((t & 63) == 0) wave_max[t >> 6] = m;
+    if (c.qt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tr[cs + i][r] = static_cast<uint8_t>(packed[i >> 2] >> (8 * (i & 3)));
+    }
+    __syncthreads();
+    if (t == 0) {
+        const float bm = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+        if (bm > 0.0f) atomicMax(c.amax_bits, __float_as_uint(bm));
+    }
+    if (c.qt) {
+        const int cc = t >> 2, rs = (t & 3) * 16;
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = static_cast<uint32_t>(tr[cc][rs + 4 * i]) | (static_cast<uint32_t>(tr[cc][rs + 4 * i + 1]) << 8) |
+                   (static_cast<uint32_t>(tr[cc][rs + 4 * i + 2]) << 16) |
+                   (static_cast<uint32_t>(tr[cc][rs + 4 * i + 3]) << 24);
+        uint8_t* dst = c.qt + static_cast<int64_t>(c.cols) * c.poff[g] +
+                       static_cast<int64_t>(ct * kCastTile + cc) * rpad + rt * kCastTile + rs;
+        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// poff[g + 1] = poff[g] + roundup(offsets[g + 1] - offsets[g], align)
+__global__ void fp8_pad_offsets_kernel(const int32_t* offsets, int G, int align, int32_t* poff) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    int32_t acc = 0;
+    poff[0] = 0;
+    for (int g = 0; g < G; ++g) {
+        const int32_t n = offsets[g + 1] - offsets[g];
+        acc += (n + align - 1) / align * align;
+        poff[g + 1] = acc;
+    }
+}
+
+// history[i] = [amax_i, history[i][0 .. L - 2]], amax_i = 0 (reference_model.py:215).
+__global__ void fp8_roll_kernel(float* hist, uint32_t* amax_bits, int n, int L) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float* h = hist + static_cast<int64_t>(i) * L;
+    for (int j = L - 1; j > 0; --j) h[j] = h[j - 1];
+    h[0] = __uint_as_float(amax_bits[i]);
+    amax_bits[i] = 0u;
+}
+
+// ------------------------------------------------------------------ fp8 GEMM
+//
+// Tiles, waves and epilogue as the bf16 kernels; K step 128 (one 128-byte
+// line per operand row), two LDS stages filled by direct loads.  A k64 block
+// is one v_mfma_scale_f32_32x32x64_f8f6f4: lane L holds row L % 32 and 32
+// consecutive k bytes, 32 (L / 32) .. +31, of both operands (the same k
+// assignment on both sides, so any consistent choice is a valid product).
+//
+// MODE kFwd: rows grouped by offsets, K fixed (fwd and dgrad).
+// MODE kWgrad: K grouped: expert g contributes K = R_g padded rows; Y rows
+// are the Mo output rows; operands are expert g's transposed copies at
+// a[0] + Mo * poff[g] and b[0] + N * poff[g], both with row pitch R_g.
+
+constexpr int kF8K = 128;
+constexpr int kF8TileBytes = kTile * kF8K;                  // 32 KB per operand
+constexpr int kF8StageBytes = 2 * kF8TileBytes;
+constexpr int kF8PerWave = kF8TileBytes / 1024 / kWaves;   // loads per wave per operand per step
+constexpr int kF8LdsBytes = 2 * kF8StageBytes > kEpBytes ? 2 * kF8StageBytes : kEpBytes;
+static_assert(kF8LdsBytes <= 163840, "two 64 KB stages");
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+struct F8Map {
+    uint32_t vo[kF8PerWave];
+    uint32_t fr[4];
+};
+
+template <class RowOf>
+__device__ __forceinline__ void f8_map(F8Map& m, uint32_t ld, int frag_row0, int nfrag, RowOf src_row) {
+    const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < kF8PerWave; ++j) {
+        const int row = (j * kWaves + w) * 8 + (L >> 3);
+        const int chunk = (L & 7) ^ ((row >> 1) & 7);
+        m.vo[j] = static_cast<uint32_t>(src_row(row)) * ld + chunk * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m.fr[i] = i < nfrag ? k64_off(frag_row0 + i * 32 + (L & 31), 2 * (L >> 5)) : 0;
+}
+
+__device__ __forceinline__ i32x8_t f8_frag(const uint8_t* tile, uint32_t fr, int b) {
+    const uint32_t o = fr ^ static_cast<uint32_t>(b << 6);
+    const uint4 lo = *reinterpret_cast<const uint4*>(tile + o);
+    const uint4 hi = *reinterpret_cast<const uint4*>(tile + (o ^ 16u));
+    i32x8_t v;
+    v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+    v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+    return v;
+}
+
+template <int MODE, int EPI, int YF, int XF>
+__global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
+    __shared__ __align__(1024) uint8_t lds[kF8LdsBytes];
+    Tile t;
+    if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
+    t.g = __builtin_amdgcn_readfirstlane(t.g);
+    t.x0 = __builtin_amdgcn_readfirstlane(t.x0);
+    t.x_lim = __builtin_amdgcn_readfirstlane(t.x_lim);
+    t.y0 = __builtin_amdgcn_readfirstlane(t.y0);
+    t.y_lim = __builtin_amdgcn_readfirstlane(t.y_lim);
+    t.row0 = __builtin_amdgcn_readfirstlane(static_cast<int>(t.row0));
+    t.k_begin = __builtin_amdgcn_readfirstlane(t.k_begin);
+    t.k_end = __builtin_amdgcn_readfirstlane(t.k_end);
+    const int g = t.g;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wx = wave & 1, wy = wave >> 1;
+
+    Rsrc rx, ry;
+    F8Map mx, my;
+    const int y_last = t.y_lim - 1;
+    if (MODE == kWgrad) {
+        const uint32_t ld = static_cast<uint32_t>(t.k_end);   // R_g
+        const uint8_t* Y = static_cast<const uint8_t*>(p.a[0]) + static_cast<int64_t>(p.Mo) * t.row0;
+        const uint8_t* X = static_cast<const uint8_t*>(p.b[0]) + static_cast<int64_t>(p.N) * t.row0;
+        ry = make_dma_rsrc(Y + static_cast<int64_t>(t.y0) * ld, static_cast<int64_t>(t.y_lim) * ld);
+        rx = make_dma_rsrc(X, static_cast<int64_t>(p.N) * ld);
+        f8_map(my, ld, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
+        f8_map(mx, ld, wx * 128, 4, [&](int r) {
+            const int n = t.x0 + r;
+            return n < p.N ? n : 0;
+        });
+    } else {
+        const uint8_t* Y = static_cast<const uint8_t*>(p.a[g]);
+        const uint8_t* X = static_cast<const uint8_t*>(p.b[g]);
+        const uint32_t lda = static_cast<uint32_t>(p.lda), ldb = static_cast<uint32_t>(p.ldb);
+        ry = make_dma_rsrc(Y + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda);
+        rx = make_dma_rsrc(X, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb);
+        f8_map(my, lda, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
+        f8_map(mx, ldb, wx * 128, 4, [&](int r) {
+            if (EPI == kEpiSwigluFwd) {
+                // 256 weight rows = [gate 64 | up 64] for each half of 128 activation columns.
+                const int half = r >> 7, qq = r & 127;
+                int col = t.x0 + half * 64 + (qq & 63);
+                col = col < p.f ? col : 0;
+                return qq < 64 ? col : p.f + col;
+            }
+            const int n = t.x0 + r;
+            return n < p.N ? n : 0;
+        });
+    }
+
+    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+    auto issue = [&](int step, int stage) {
+        const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kF8K);
+        const uint32_t base = lds0 + stage * kF8StageBytes + wave * 1024;
+#pragma unroll
+        for (int j = 0; j < kF8PerWave; ++j) {
+            const uint32_t at = base + j * kWaves * 1024;
+            dma16(rx, mx.vo[j], k0, at);
+            dma16(ry, my.vo[j], k0, at + kF8TileBytes);
+        }
+    };
+
+    f32x16_t acc[4][kFragY];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < kFragY; ++j) acc[i][j] = f32x16_t{};
+
+    typedef i32x8_t FragSet[4 + kFragY];
+    auto read_frags = [&](FragSet& f, int stage, int b) {
+        const uint8_t* xt = lds + stage * kF8StageBytes;
+        const uint8_t* yt = xt + kF8TileBytes;
+#pragma unroll
+        for (int j = 0; j < kFragY; ++j) f[4 + j] = f8_frag(yt, my.fr[j], b);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[i] = f8_frag(xt, mx.fr[i], b);
+    };
+    auto mfmas = [&](const FragSet& f) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < kFragY; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[i], f[4 + j], acc[i][j], XF, YF, 0, 127,
+                                                                           0, 127);
+    };
+    constexpr int kReads = 2 * (4 + kFragY);
+
+    const int nk = (t.k_end - t.k_begin + kF8K - 1) / kF8K;
+    const bool idle = wy * kWaveY >= t.y_lim;
+    FragSet fa, fb;
+    if (nk > 0) {
+        issue(0, 0);
+        wait_loads_all();
+        __syncthreads();
+        if (!idle) read_frags(fa, 0, 0);
+    }
+    if (idle) {
+        for (int kt = 0; kt < nk; ++kt) {
+            if (kt + 1 < nk) issue(kt + 1, (kt & 1) ^ 1);
+            wait_loads_all();
+            __syncthreads();
+        }
+    }
+    for (int kt = 0; kt < (idle ? 0 : nk); ++kt) {
+        const int st = kt & 1;
+        if (kt + 1 < nk) issue(kt + 1, st ^ 1);
+        read_frags(fb, st, 1);
+        mfmas(fa);
+        interleave_reads<0, 4 * kFragY, kReads>();
+        // The loads of step kt + 1 have landed in every wave's share and no wave
+        // still reads stage st (its block-1 reads complete before the barrier).
+        wait_loads_all();
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        read_frags(fa, st ^ 1, 0);
+        mfmas(fb);
+        interleave_reads<0, 4 * kFragY, kReads>();
+    }
+    const float mul = p.scale_inv_y[0] * p.scale_inv_x[g * p.scale_x_stride];
+    epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane, mul);
+}
+
+template <int MODE, int EPI, int YF, int XF>
+void launch_fp8(const Params& p, unsigned nb, hipStream_t s) {
+    hipLaunchKernelGGL((gg_fp8_kernel<MODE, EPI, YF, XF>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+}
+
+// The (mode, epilogue, formats) combinations the expert layer uses.
+bool launch_fp8_any(int mode, int epi, int yf, int xf, const Params& p, unsigned nb, hipStream_t s) {
+    if (xf != kFmtE4m3) return false;
+    const int key = (mode * 8 + epi) * 2 + yf;
+    switch (key) {
+        case (kFwd * 8 + kEpiSwigluFwd) * 2 + kFmtE4m3: launch_fp8<kFwd, kEpiSwigluFwd, kFmtE4m3, kFmtE4m3>(p, nb, s); return true;
+        case (kFwd * 8 + kEpiGeluFwd) * 2 + kFmtE4m3: launch_fp8<kFwd, kEpiGeluFwd, kFmtE4m3, kFmtE4m3>(p, nb, s); return true;
+        case (kFwd * 8 + kEpiStore) * 2 + kFmtE4m3: launch_fp8<kFwd, kEpiStore, kFmtE4m3, kFmtE4m3>(p, nb, s); return true;
+        case (kFwd * 8 + kEpiStore) * 2 + kFmtE5m2: launch_fp8<kFwd, kEpiStore, kFmtE5m2, kFmtE4m3>(p, nb, s); return true;
+        case (kFwd * 8 + kEpiSwigluBwd) * 2 + kFmtE5m2: launch_fp8<kFwd, kEpiSwigluBwd, kFmtE5m2, kFmtE4m3>(p, nb, s); return true;
+        case (kFwd * 8 + kEpiGeluBwd) * 2 + kFmtE5m2: launch_fp8<kFwd, kEpiGeluBwd, kFmtE5m2, kFmtE4m3>(p, nb, s); return true;
+        case (kWgrad * 8 + kEpiStore) * 2 + kFmtE5m2: launch_fp8<kWgrad, kEpiStore, kFmtE5m2, kFmtE4m3>(p, nb, s); return true;
+        default: return false;
+    }
+}
+
+int fp8_fmt(int dtype) { return dtype == RHP_E4M3 ? kFmtE4m3 : dtype == RHP_E5M2 ? kFmtE5m2 : -1; }
+
+}  // namespace
+}  // namespace rhp
+
+using namespace rhp;
+
+extern "C" int rhp_fp8_padded_offsets(const int32_t* offsets, int G, int align, int32_t* poff, hipStream_t stream) {
+    clear_error();
+    RHP_REQUIRE(offsets && poff, "rhp_fp8_padded_offsets: null pointer");
+    RHP_REQUIRE(G >= 1 && align >= 128 && align % 128 == 0,
+                "rhp_fp8_padded_offsets: need G >= 1 and an alignment that is a multiple of 128 (the fp8 K step)");
+    hipLaunchKernelGGL(fp8_pad_offsets_kernel, dim3(1), dim3(64), 0, stream, offsets, G, align, poff);
+    return check_launch("rhp_fp8_padded_offsets");
+}
+
+extern "C" int rhp_fp8_cast(const void* x, int x_dtype, int64_t ldx, int cols, int G, const int32_t* offsets,
+                            const int32_t* poff, int64_t rows_cap, const float* history, int hist_len, int fmt,
+                            int margin, uint32_t* amax_bits, float* scale_inv, void* q, void* qt,
+                            hipStream_t stream) {
+    clear_error();
+    RHP_REQUIRE(x_dtype == RHP_BF16, "rhp_fp8_cast: input must be bfloat16");
+    const int f8 = fp8_fmt(fmt);
+    RHP_REQUIRE(f8 >= 0, "rhp_fp8_cast: format must be RHP_E4M3 or RHP_E5M2");
+    RHP_REQUIRE(x && offsets && poff && history && amax_bits && scale_inv, "rhp_fp8_cast: null pointer");
+    RHP_REQUIRE(q || qt, "rhp_fp8_cast: nothing to write");
+    RHP_REQUIRE(G >= 1 && hist_len >= 1 && margin >= 0 && margin < 64, "rhp_fp8_cast: bad G, history or margin");
+    RHP_REQUIRE(cols > 0 && cols % kCastTile == 0, "rhp_fp8_cast: cols must be a positive multiple of 64");
+    RHP_REQUIRE(ldx >= cols && ldx % 8 == 0 && aligned16(x), "rhp_fp8_cast: x rows must be 16-byte aligned");
+    RHP_REQUIRE(rows_cap >= 0 && rows_cap < (int64_t(1) << 31), "rhp_fp8_cast: rows_cap out of range");
+    RHP_REQUIRE((!q || aligned16(q)) && (!qt || aligned16(qt)), "rhp_fp8_cast: outputs must be 16-byte aligned");
+    CastParams c{};
+    c.x = static_cast<const uint16_t*>(x);
+    c.ldx = ldx;
+    c.cols = cols;
+    c.G = G;
+    c.offsets = offsets;
+    c.poff = poff;
+    c.hist = history;
+    c.L = hist_len;
+    c.margin = margin;
+    c.amax_bits = amax_bits;
+    c.scale_inv = scale_inv;
+    c.q = static_cast<uint8_t*>(q);
+    c.qt = static_cast<uint8_t*>(qt);
+    // rows_cap bounds the padded rows: sum_g roundup(n_g, 128) <= rows_cap + 127 G.
+    const int64_t row_tiles = (rows_cap + 127 * static_cast<int64_t>(G)) / kCastTile + G;
+    const int64_t blocks = row_tiles * (cols / kCastTile);
+    RHP_REQUIRE(blocks < (int64_t(1) << 31), "rhp_fp8_cast: too many tiles");
+    if (blocks == 0) return 0;
+    if (f8 == kFmtE4m3)
+        hipLaunchKernelGGL(fp8_cast_kernel<kFmtE4m3>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, c);
+    else
+        hipLaunchKernelGGL(fp8_cast_kernel<kFmtE5m2>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, c);
+    return check_launch("rhp_fp8_cast");
+}
+
+extern "C" int rhp_fp8_amax_roll(float* history, uint32_t* amax_bits, int n, int hist_len, hipStream_t stream) {
+    clear_error();
+    RHP_REQUIRE(history && amax_bits, "rhp_fp8_amax_roll: null pointer");
+    RHP_REQUIRE(n >= 1 && hist_len >= 1, "rhp_fp8_amax_roll: need n >= 1 and hist_len >= 1");
+    hipLaunchKernelGGL(fp8_roll_kernel, dim3((n + 63) / 64), dim3(64), 0, stream, history, amax_bits, n, hist_len);
+    return check_launch("rhp_fp8_amax_roll");
+}
+
+extern "C" int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt,
+                            int x_fmt, int N, int K, int Mo, int f, const void* const* y, int64_t ldy,
+                            const void* const* x, int64_t ldx, void* const* c, int64_t ldc, void* const* c2,
+                            int64_t ldc2, const void* const* aux, int64_t ldaux, const float* y_scale_inv,
+                            const float* x_scale_inv, int x_scale_stride, hipStream_t stream) {
+    clear_error();
+    const int yf = fp8_fmt(y_fmt), xf = fp8_fmt(x_fmt);
+    RHP_REQUIRE(yf >= 0 && xf >= 0, "rhp_fp8_gemm: operand formats must be RHP_E4M3 or RHP_E5M2");
+    RHP_REQUIRE(G >= 1 && G <= RHP_MAX_GROUPS_PER_LAUNCH, "rhp_fp8_gemm: 1 to 64 groups per call");
+    RHP_REQUIRE(offsets && y && x && c && y_scale_inv && x_scale_inv, "rhp_fp8_gemm: null pointer");
+    RHP_REQUIRE(x_scale_stride == 0 || x_scale_stride == 1, "rhp_fp8_gemm: x scale stride must be 0 or 1");
+    RHP_REQUIRE(N > 0 && N % 64 == 0, "rhp_fp8_gemm: N must be a positive multiple of 64");
+    RHP_REQUIRE(rows_cap >= 0 && rows_cap < (int64_t(1) << 31), "rhp_fp8_gemm: rows_cap out of range");
+    RHP_REQUIRE(ldc > 0 && ldc < (int64_t(1) << 31), "rhp_fp8_gemm: bad ldc");
+    const int mode = kgroups ? kWgrad : kFwd;
+    Params p{};
+    const int ng = kgroups ? 1 : G;
+    for (int g = 0; g < ng; ++g) {
+        RHP_REQUIRE(y[g] && x[g] && aligned16(y[g]) && aligned16(x[g]), "rhp_fp8_gemm: operands must be 16-byte aligned");
+        p.a[g] = y[g];
+        p.b[g] = x[g];
+    }
+    for (int g = 0; g < G; ++g) {
+        RHP_REQUIRE(c[g] != nullptr, "rhp_fp8_gemm: null output");
+        p.c[g] = c[g];
+        p.c2[g] = c2 ? c2[g] : nullptr;
+        p.aux[g] = aux ? aux[g] : nullptr;
+    }
+    if (kgroups) {
+        RHP_REQUIRE(epi == kEpiStore, "rhp_fp8_gemm: K-grouped products store plain outputs");
+        RHP_REQUIRE(Mo > 0 && Mo % 64 == 0, "rhp_fp8_gemm: Mo must be a positive multiple of 64");
+        RHP_REQUIRE((int64_t(Mo) + N) * (rows_cap + 128 * int64_t(G)) < (int64_t(1) << 31),
+                    "rhp_fp8_gemm: transposed operands must stay below 2 GiB");
+    } else {
+        RHP_REQUIRE(K > 0 && K % kF8K == 0, "rhp_fp8_gemm: K must be a positive multiple of 128");
+        RHP_REQUIRE(ldy >= K && ldy % 16 == 0 && ldx >= K && ldx % 16 == 0, "rhp_fp8_gemm: bad row pitches");
+        const int64_t xrows = epi == kEpiSwigluFwd ? 2 * int64_t(f) : N;
+        RHP_REQUIRE(rows_cap * ldy < (int64_t(1) << 31) && xrows * ldx < (int64_t(1) << 31),
+                    "rhp_fp8_gemm: operands must stay below 2 GiB");
+        if (epi == kEpiSwigluFwd || epi == kEpiGeluFwd) RHP_REQUIRE(c2 != nullptr, "rhp_fp8_gemm: activation output missing");
+        if (epi == kEpiSwigluBwd || epi == kEpiGeluBwd) RHP_REQUIRE(aux != nullptr, "rhp_fp8_gemm: pre-activation input missing");
+        if (epi == kEpiSwigluFwd || epi == kEpiSwigluBwd) RHP_REQUIRE(f == N && f % 64 == 0, "rhp_fp8_gemm: SwiGLU needs N == f");
+    }
+    p.offsets = offsets;
+    p.G = G;
+    p.rows_from_offsets = 1;
+    p.N = N;
+    p.K = K;
+    p.Mo = Mo;
+    p.lda = static_cast<int>(ldy);
+    p.ldb = static_cast<int>(ldx);
+    p.ldc = static_cast<int>(ldc);
+    p.ldc2 = static_cast<int>(ldc2);
+    p.ldaux = static_cast<int>(ldaux);
+    p.f = f;
+    p.rows_cap = static_cast<int>(kgroups ? rows_cap + 128 * int64_t(G) : rows_cap);
+    p.scale_inv_y = y_scale_inv;
+    p.scale_inv_x = x_scale_inv;
+    p.scale_x_stride = x_scale_stride;
+    const int64_t xt = (N + (epi == kEpiSwigluFwd ? 127 : 255)) / (epi == kEpiSwigluFwd ? 128 : 256);
+    const int64_t nb = kgroups ? G * xt * ((Mo + kTile - 1) / kTile) : ((rows_cap + kTile - 1) / kTile + G) * xt;
+    if (nb == 0) return 0;
+    RHP_REQUIRE(launch_fp8_any(mode, epi, yf, xf, p, static_cast<unsigned>(nb), stream),
+                "rhp_fp8_gemm: unsupported combination of product, epilogue and formats");
+    return check_launch("rhp_fp8_gemm");
+}

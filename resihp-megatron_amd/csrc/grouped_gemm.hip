@@ -22,350 +22,10 @@
 // Work unit: a 256 x 256 output tile.  Tiles are ordered group-major, then by
 // output column block, then by row block, and block ids are remapped so each
 // XCD runs a contiguous range of that order.
-#include <algorithm>
-
-#include "rhp_common.h"
+#include "gemm_common.h"
 
 namespace rhp {
 namespace {
-
-constexpr int kMaxG = RHP_MAX_GROUPS_PER_LAUNCH;
-
-enum Mode { kFwd = 0, kDgrad = 1, kWgrad = 2 };
-enum Epi { kEpiStore = 0, kEpiSwigluFwd = 1, kEpiGeluFwd = 2, kEpiSwigluBwd = 3, kEpiGeluBwd = 4 };
-
-struct Params {
-    const void* a[kMaxG];     // FWD/DGRAD: token rows A; WGRAD: gradient rows G
-    const void* b[kMaxG];     // FWD/DGRAD: weight W;     WGRAD: activation rows V
-    void* c[kMaxG];           // primary output (hpre / y / dhpre / dxp / dW)
-    void* c2[kMaxG];          // FWD activation output
-    const void* aux[kMaxG];   // backward epilogues: pre-activation hpre
-    const int32_t* offsets;   // [G + 1] cumulative row counts
-    int G;
-    int rows_from_offsets;
-    int N;                    // FWD/DGRAD: output columns (activation columns for SwiGLU FWD); WGRAD: Ni
-    int K;                    // FWD/DGRAD: reduction length
-    int Mo;                   // WGRAD: rows of dW
-    int lda, ldb, ldc, ldc2, ldaux;
-    int f;                    // SwiGLU: up rows / columns start at f
-    int rows_cap;             // rows of a shared row buffer (rows_from_offsets = 1)
-};
-
-// ------------------------------------------------------------------ activations
-
-// Single-precision forms use the hardware exp2 and reciprocal (about 1 ulp);
-// their results are rounded to bfloat16 or float32 storage right after.
-__device__ __forceinline__ float sigmoid_fast(float g) { return __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
-__device__ __forceinline__ float silu_f(float g) { return g * sigmoid_fast(g); }
-__device__ __forceinline__ double silu_f(double g) { return g / (1.0 + exp(-g)); }
-__device__ __forceinline__ float dsilu_f(float g) {
-    const float s = sigmoid_fast(g);
-    return s * (1.0f + g * (1.0f - s));
-}
-__device__ __forceinline__ double dsilu_f(double g) {
-    const double s = 1.0 / (1.0 + exp(-g));
-    return s * (1.0 + g * (1.0 - s));
-}
-__device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
-__device__ __forceinline__ double gelu_f(double v) { return 0.5 * v * (1.0 + erf(v * 0.70710678118654752440)); }
-__device__ __forceinline__ float dgelu_f(float v) {
-    return 0.5f * (1.0f + erff(v * 0.70710678118654752f)) + v * 0.39894228040143268f * __expf(-0.5f * v * v);
-}
-__device__ __forceinline__ double dgelu_f(double v) {
-    return 0.5 * (1.0 + erf(v * 0.70710678118654752440)) + v * 0.39894228040143267794 * exp(-0.5 * v * v);
-}
-
-// ------------------------------------------------------------------ tile scheduling
-
-constexpr int kTile = 256;   // output tile edge (X rows and Y rows)
-
-struct Tile {
-    int g;
-    int x0, x_lim;      // first X row (output column) of the tile and how many are valid
-    int y0, y_lim;      // first Y row relative to the group's row 0, valid count
-    int64_t row0;       // FWD/DGRAD: row of the group's first row in the row buffers
-    int k_begin, k_end; // reduction range (WGRAD: group rows)
-};
-
-// Finds this block's tile.  xt_cols output columns (X rows) and yt_rows output
-// rows (Y rows) per tile.  Blocks beyond the real tile count return false;
-// the others are remapped so that each XCD runs a contiguous range of tiles.
-template <int MODE>
-__device__ __forceinline__ bool find_tile(const Params& p, int xt_cols, int yt_rows, Tile* t) {
-    const int xt_n = (p.N + xt_cols - 1) / xt_cols;
-    if (MODE == kWgrad) {
-        const int yt_n = (p.Mo + yt_rows - 1) / yt_rows;
-        const uint32_t total = static_cast<uint32_t>(p.G) * xt_n * yt_n;
-        if (blockIdx.x >= total) return false;
-        const uint32_t L = xcd_remap(blockIdx.x, total);
-        const int per_group = xt_n * yt_n;
-        t->g = L / per_group;
-        const int rem = L % per_group;
-        const int yt = rem / xt_n, xt = rem % xt_n;
-        t->x0 = xt * xt_cols;
-        t->x_lim = p.N - t->x0;
-        t->y0 = yt * yt_rows;
-        t->y_lim = p.Mo - t->y0;
-        const int r0 = p.offsets[t->g], r1 = p.offsets[t->g + 1];
-        t->row0 = p.rows_from_offsets ? r0 : 0;
-        t->k_begin = 0;
-        t->k_end = r1 - r0;
-        // A shared row buffer holds rows_cap rows: never read past it.
-        if (p.rows_from_offsets) t->k_end = max(0, min(t->k_end, p.rows_cap - r0));
-        return true;
-    }
-    uint32_t total = 0;
-    for (int g = 0; g < p.G; ++g) {
-        const int M = p.offsets[g + 1] - p.offsets[g];
-        total += static_cast<uint32_t>((M + yt_rows - 1) / yt_rows) * xt_n;
-    }
-    if (blockIdx.x >= total) return false;
-    uint32_t L = xcd_remap(blockIdx.x, total);
-    for (int g = 0; g < p.G; ++g) {
-        const int M = p.offsets[g + 1] - p.offsets[g];
-        const int mt = (M + yt_rows - 1) / yt_rows;
-        const uint32_t n_tiles = static_cast<uint32_t>(mt) * xt_n;
-        if (L < n_tiles) {
-            const int xt = L / mt, yt = L % mt;
-            t->g = g;
-            t->x0 = xt * xt_cols;
-            t->x_lim = p.N - t->x0;
-            t->y0 = yt * yt_rows;
-            t->y_lim = M - t->y0;
-            t->row0 = p.rows_from_offsets ? p.offsets[g] : 0;
-            t->k_begin = 0;
-            t->k_end = p.K;
-            // A shared row buffer holds rows_cap rows: never touch rows past it.
-            if (p.rows_from_offsets) t->y_lim = min(t->y_lim, p.rows_cap - static_cast<int>(t->row0) - t->y0);
-            return t->y_lim > 0;
-        }
-        L -= n_tiles;
-    }
-    return false;
-}
-
-// X columns covered by one MFMA tile: SwiGLU FWD tiles cover 128 activation
-// columns (their 256 weight rows are 128 gate + 128 up rows).
-template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI == kEpiSwigluFwd ? 128 : 256; }
-
-// ------------------------------------------------------------------ MFMA kernels (bf16)
-//
-// A 256 x 256 output tile per workgroup of 8 waves (two per SIMD).  Wave w
-// owns X rows [128 (w % 2), +128) and Y rows [64 (w / 2), +64): 4 x 2
-// accumulators of v_mfma_f32_32x32x16_bf16 (128 registers).
-//
-// Operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds:
-// no staging registers and no LDS stores.  One such load moves 64 lanes x 16
-// bytes into 1 KB of LDS at M0 + 16 * lane, so a stage is built from 1 KB
-// blocks whose lanes pick the global chunk that belongs at their position.
-//   K-major tiles (K contiguous in HBM: FWD both operands, DGRAD token rows)
-//     keep rows of K-step elements with the 16-byte chunks XOR-swizzled by
-//     row, so the 16 rows of one ds_read_b128 hit 16 distinct bank slots.
-//   MN-major tiles (K is the slow dimension: DGRAD weights, both WGRAD
-//     operands) keep 512-byte k rows with chunk c at position c ^ 4 (k & 3)
-//     and are read with gfx950's ds_read_b64_tr_b16, which transposes 4 x 16
-//     blocks across each 16-lane group; two such reads give one fragment.
-// No transposed copy of any operand is made in HBM.
-//
-// The loads are inline assembly so that the compiler, which does not see them,
-// does not make every LDS read wait for all of them; each kernel counts them
-// itself (s_waitcnt vmcnt) before its barriers.  Fragments are double-buffered
-// in registers: the reads of the next k16 block are interleaved with the
-// MFMAs of the current one.
-//
-// FWD runs gg_bf16_k64_kernel (K step 64: each row of a stage is a whole
-// 128-byte line, so L2 sees half the requests); DGRAD and WGRAD run
-// gg_bf16_k32_kernel (K step 32, four stages, loads two steps ahead), which
-// measured faster for the transposed operands.
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-constexpr int kWaves = 8;
-constexpr int kThreadsMfma = 64 * kWaves;
-constexpr int kWaveY = kTile / (kWaves / 2);               // Y rows per wave
-constexpr int kFragY = kWaveY / 32;                        // Y fragments per wave
-
-__device__ __forceinline__ int mnmaj_off(int k, int mn) {
-    return k * 512 + (((mn >> 3) ^ ((k & 3) << 2)) << 4) + ((mn & 7) << 1);
-}
-
-// Two transposed reads, k rows kb .. kb + 3 and kb + 4 .. kb + 7 (512 B apart per k row).
-__device__ __forceinline__ bf16x8_t frag_mnmaj(const uint8_t* tile, uint32_t fr, int kk) {
-    typedef s16x4_t __attribute__((address_space(3))) * lds_v4;
-    const uint8_t* p = tile + fr + kk * 16 * 512;
-    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(p)));
-    const s16x4_t hi =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(p + 4 * 512)));
-    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
-__device__ __forceinline__ void store_bf16x4(uint16_t* p, float a, float b, float c, float d) {
-    uint2 v;
-    v.x = pack_bf16x2(a, b);
-    v.y = pack_bf16x2(c, d);
-    *reinterpret_cast<uint2*>(p) = v;
-}
-__device__ __forceinline__ void load_bf16x4(const uint16_t* p, float* o) {
-    const uint2 v = *reinterpret_cast<const uint2*>(p);
-    o[0] = __uint_as_float(v.x << 16);
-    o[1] = __uint_as_float(v.x & 0xffff0000u);
-    o[2] = __uint_as_float(v.y << 16);
-    o[3] = __uint_as_float(v.y & 0xffff0000u);
-}
-
-// Epilogue staging: half a tile of fp32 accumulators, rows padded by 16 bytes
-// so that the 16 lanes of a ds_write_b128 (16 consecutive rows) hit distinct
-// bank groups.
-constexpr int kEpRows = 128;
-constexpr int kEpPitchF = 256 + 4;   // floats per staged row
-constexpr int kEpBytes = kEpRows * kEpPitchF * 4;
-
-__device__ __forceinline__ float4 lds_f4(const float* ep, int r, int x) {
-    return *reinterpret_cast<const float4*>(ep + r * kEpPitchF + x);
-}
-
-// Rows [r0, r0 + 128) of the tile, staged in ep.  Thread t handles 4-column
-// pieces t, t + 512, ...; a wave covers one row (or two rows of 128 columns).
-template <int MODE, int EPI>
-__device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, const float* ep, int r0) {
-    const int g = t.g;
-    if (EPI == kEpiSwigluFwd) {
-        // X columns of the tile are [gate 64 | up 64] for each half of 128
-        // activation columns; piece a covers activation columns 4a .. 4a + 3.
-        uint16_t* hpre = static_cast<uint16_t*>(p.c[g]);
-        uint16_t* act = static_cast<uint16_t*>(p.c2[g]);
-#pragma unroll 4
-        for (int idx = threadIdx.x; idx < kEpRows * 32; idx += kThreadsMfma) {
-            const int r = idx >> 5, a = (idx & 31) * 4;
-            const int yr = r0 + r, col = t.x0 + a;
-            if (yr >= t.y_lim || col >= p.N) continue;
-            const int xg = (a >> 6) * 128 + (a & 63);
-            const float4 gv = lds_f4(ep, r, xg), uv = lds_f4(ep, r, xg + 64);
-            const int64_t row = t.row0 + t.y0 + yr;
-            store_bf16x4(hpre + row * p.ldc + col, gv.x, gv.y, gv.z, gv.w);
-            store_bf16x4(hpre + row * p.ldc + p.f + col, uv.x, uv.y, uv.z, uv.w);
-            store_bf16x4(act + row * p.ldc2 + col, silu_f(gv.x) * uv.x, silu_f(gv.y) * uv.y, silu_f(gv.z) * uv.z,
-                         silu_f(gv.w) * uv.w);
-        }
-        return;
-    }
-    uint16_t* out = static_cast<uint16_t*>(p.c[g]);
-#pragma unroll 4
-    for (int idx = threadIdx.x; idx < kEpRows * 64; idx += kThreadsMfma) {
-        const int r = idx >> 6, x = (idx & 63) * 4;
-        const int yr = r0 + r;
-        if (yr >= t.y_lim || x >= t.x_lim) continue;
-        const int col = t.x0 + x;
-        const float4 v = lds_f4(ep, r, x);
-        if (MODE == kWgrad) {
-            store_bf16x4(out + static_cast<int64_t>(t.y0 + yr) * p.ldc + col, v.x, v.y, v.z, v.w);
-            continue;
-        }
-        const int64_t row = t.row0 + t.y0 + yr;
-        if (EPI == kEpiStore) {
-            store_bf16x4(out + row * p.ldc + col, v.x, v.y, v.z, v.w);
-        } else if (EPI == kEpiGeluFwd) {
-            uint16_t* act = static_cast<uint16_t*>(p.c2[g]);
-            store_bf16x4(out + row * p.ldc + col, v.x, v.y, v.z, v.w);
-            store_bf16x4(act + row * p.ldc2 + col, gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w));
-        } else if (EPI == kEpiGeluBwd) {
-            const uint16_t* hp = static_cast<const uint16_t*>(p.aux[g]);
-            float hv[4];
-            load_bf16x4(hp + row * p.ldaux + col, hv);
-            store_bf16x4(out + row * p.ldc + col, v.x * dgelu_f(hv[0]), v.y * dgelu_f(hv[1]), v.z * dgelu_f(hv[2]),
-                         v.w * dgelu_f(hv[3]));
-        } else if (EPI == kEpiSwigluBwd) {
-            const uint16_t* hp = static_cast<const uint16_t*>(p.aux[g]);
-            float gv[4], uv[4];
-            load_bf16x4(hp + row * p.ldaux + col, gv);
-            load_bf16x4(hp + row * p.ldaux + p.f + col, uv);
-            const float dv[4] = {v.x, v.y, v.z, v.w};
-            float dg[4], du[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                dg[e] = dv[e] * uv[e] * dsilu_f(gv[e]);
-                du[e] = dv[e] * silu_f(gv[e]);
-            }
-            store_bf16x4(out + row * p.ldc + col, dg[0], dg[1], dg[2], dg[3]);
-            store_bf16x4(out + row * p.ldc + p.f + col, du[0], du[1], du[2], du[3]);
-        }
-    }
-}
-
-// Epilogue, in two halves of 128 Y rows.  The waves owning a half write
-// their fp32 accumulators to LDS ([128 rows][256 X] at kEpPitchF floats per
-// row); then every thread takes 4-column pieces, so each wave instruction
-// reads or writes whole contiguous row segments in HBM.  For MFMA tile (i, j)
-// a lane holds Y row wy * kWaveY + 32 j + (lane & 31) and X columns
-// wx * 128 + 32 i + 8 q + 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller
-// guarantees that no wave still reads or writes the LDS buffer.
-template <int MODE, int EPI>
-__device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][kFragY],
-                                         int wx, int wy, int lane) {
-    float* ep = reinterpret_cast<float*>(lds);
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        __syncthreads();
-        if ((wy * kWaveY) / kEpRows == half) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < kFragY; ++j) {
-                    const int y = wy * kWaveY + j * 32 + (lane & 31) - half * kEpRows;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int x = wx * 128 + i * 32 + q * 8 + 4 * (lane >> 5);
-                        float4 v;
-                        v.x = acc[i][j][4 * q + 0];
-                        v.y = acc[i][j][4 * q + 1];
-                        v.z = acc[i][j][4 * q + 2];
-                        v.w = acc[i][j][4 * q + 3];
-                        *reinterpret_cast<float4*>(ep + y * kEpPitchF + x) = v;
-                    }
-                }
-        }
-        __syncthreads();
-        epilogue_half<MODE, EPI>(p, t, ep, half * kEpRows);
-    }
-}
-
-// Scheduling hint: MF MFMAs with RD LDS reads spread evenly between them.
-template <int Q, int MF, int RD>
-__device__ __forceinline__ void interleave_reads() {
-    if constexpr (Q < MF) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        constexpr int n = RD * (Q + 1) / MF - RD * Q / MF;
-        if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
-        interleave_reads<Q + 1, MF, RD>();
-    }
-}
-
-constexpr uint32_t kOutOfRange = 0x80000000u;             // a buffer offset past every view: reads zero
-
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-struct Rsrc {
-    i32x4_t d;
-};
-__device__ __forceinline__ Rsrc make_dma_rsrc(const void* base, int64_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    Rsrc r;
-    r.d[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a));
-    r.d[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));
-    r.d[2] = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes > 0x7ffffff0 ? 0x7ffffff0 : bytes));
-    r.d[3] = 0x00020000;
-    return r;
-}
-// 16 bytes per lane from the buffer at voff + soff into LDS at lds + 16 * lane.
-__device__ __forceinline__ void dma16(const Rsrc& r, uint32_t voff, uint32_t soff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-                 :
-                 : "v"(voff), "s"(r.d), "s"(__builtin_amdgcn_readfirstlane(soff)),
-                   "s"(__builtin_amdgcn_readfirstlane(lds))
-                 : "memory");
-}
 
 // ------------------------------------------------------------------ K step 32, four stages
 //
@@ -617,9 +277,6 @@ constexpr int kLds64Bytes = 2 * kS64Bytes > kEpBytes ? 2 * kS64Bytes : kEpBytes;
 static_assert(kLds64Bytes <= 163840, "two 64 KB stages");
 static_assert((kT64Bytes / 1024) % kWaves == 0, "whole loads per wave");
 
-__device__ __forceinline__ uint32_t k64_off(int row, int chunk) {
-    return static_cast<uint32_t>(row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4));
-}
 
 struct Dma64Map {
     uint32_t vo[kD64PerWave];
@@ -756,14 +413,14 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k64_kernel(Params p) {
     FragSet fa, fb;
     if (nk > 0) {
         issue(0, 0);
-        wait_dma_steps(0);
+        wait_loads_all();
         __syncthreads();
         if (!idle) read_frags(fa, 0, 0);
     }
     if (idle) {
         for (int kt = 0; kt < nk; ++kt) {
             if (kt + 1 < nk) issue(kt + 1, (kt & 1) ^ 1);
-            wait_dma_steps(0);
+            wait_loads_all();
             __syncthreads();
         }
     }
@@ -783,7 +440,7 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k64_kernel(Params p) {
         interleave_reads<0, 4 * kFragY, kReads>();
         // The loads of step kt + 1 have landed in every wave's share and no wave
         // still reads stage st (its block-3 reads complete before the barrier).
-        wait_dma_steps(0);
+        wait_loads_all();
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
         read_frags(fa, st ^ 1, 0);

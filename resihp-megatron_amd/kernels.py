@@ -347,3 +347,101 @@ def expert_fc1_bwd(dhpre: list[torch.Tensor], xs: list[torch.Tensor], offsets: t
         _check_groups("dx", dxs, G, dt, h, rows)
     _call("rhp_expert_fc1_bwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w1[0]),
           act_code(act), h, f, _arr(dhpre), _arr(xs), _arr(w1), _arr(dxs) if dxs else None, _arr(dw1))
+
+
+# ----------------------------------------------------------------------------- fp8 experts
+
+FP8_FORMATS = {"e4m3": (C.E4M3, torch.float8_e4m3fn, 448.0), "e5m2": (C.E5M2, torch.float8_e5m2, 57344.0)}
+FP8_ALIGN = 128   # rows of each expert in the transposed copies are padded to this (the fp8 K step)
+EPI_CODES = {"store": 0, "swiglu_fwd": 1, "gelu_fwd": 2, "swiglu_bwd": 3, "gelu_bwd": 4}
+
+
+def fp8_padded_offsets(offsets: torch.Tensor) -> torch.Tensor:
+    """poff[g+1] = poff[g] + roundup(rows of expert g, 128): where each expert starts in a transposed copy."""
+    dev = _need_cuda(offsets)
+    _expect(offsets.dtype == torch.int32 and offsets.dim() == 1 and offsets.numel() >= 2, "offsets must be int32 [G+1]")
+    G = offsets.numel() - 1
+    poff = torch.empty(G + 1, dtype=torch.int32, device=dev)
+    _call("rhp_fp8_padded_offsets", dev, _ptr(offsets), G, FP8_ALIGN, _ptr(poff))
+    return poff
+
+
+def fp8_transposed_numel(cols: int, rows_cap: int, G: int) -> int:
+    """Elements of a buffer that holds every expert's transposed, row-padded copy."""
+    return cols * (rows_cap + (FP8_ALIGN - 1) * G)
+
+
+def fp8_cast(x: torch.Tensor, offsets: torch.Tensor, poff: torch.Tensor, rows_cap: int, history: torch.Tensor,
+             fmt: str, amax_bits: torch.Tensor, scale_inv: torch.Tensor, q: torch.Tensor | None = None,
+             qt: torch.Tensor | None = None, margin: int = 0) -> None:
+    """Delayed-scaling cast of bf16 rows to fp8 (row-major ``q`` and/or per-expert transposed ``qt``).
+
+    ``amax_bits`` (int32 holding float bits) is raised to max |x|; ``scale_inv`` (float32 [1]) receives 1/scale.
+    """
+    dev = _need_cuda(x, offsets, poff, history, amax_bits, scale_inv, q, qt)
+    code, fdt, _ = FP8_FORMATS[fmt]
+    G = offsets.numel() - 1
+    _expect(x.dtype == torch.bfloat16 and x.dim() == 2, "x must be bf16 [rows, cols]")
+    rows, cols = x.shape
+    _expect(cols % 64 == 0, "cols must be a multiple of 64")
+    _expect(rows_cap <= rows, "rows_cap exceeds the rows of x")
+    _expect(poff.dtype == torch.int32 and poff.numel() == G + 1, "poff must be int32 [G+1]")
+    _expect(history.dtype == torch.float32 and history.dim() == 1, "history must be float32 [L]")
+    _expect(amax_bits.dtype == torch.int32 and amax_bits.numel() == 1, "amax_bits must be int32 [1]")
+    _expect(scale_inv.dtype == torch.float32 and scale_inv.numel() == 1, "scale_inv must be float32 [1]")
+    _expect(q is not None or qt is not None, "nothing to write")
+    if q is not None:
+        _expect(q.dtype == fdt and tuple(q.shape) == (rows, cols), f"q must be {fdt} [{rows}, {cols}]")
+    if qt is not None:
+        _expect(qt.dtype == fdt and qt.numel() >= fp8_transposed_numel(cols, rows_cap, G), "qt is too small")
+    _call("rhp_fp8_cast", dev, _ptr(x), C.BF16, cols, cols, G, _ptr(offsets), _ptr(poff), rows_cap, _ptr(history),
+          history.numel(), code, margin, _ptr(amax_bits), _ptr(scale_inv), _ptr(q), _ptr(qt))
+
+
+def fp8_amax_roll(history: torch.Tensor, amax_bits: torch.Tensor) -> None:
+    """End of iteration: every history gets its pending amax prepended (newest first); the amax resets."""
+    dev = _need_cuda(history, amax_bits)
+    _expect(history.dtype == torch.float32 and history.dim() == 2, "history must be float32 [n, L]")
+    _expect(amax_bits.dtype == torch.int32 and amax_bits.numel() == history.shape[0], "amax_bits must be int32 [n]")
+    _call("rhp_fp8_amax_roll", dev, _ptr(history), _ptr(amax_bits), history.shape[0], history.shape[1])
+
+
+def fp8_gemm(kgroups: bool, epi: str, offsets: torch.Tensor, rows_cap: int, ys: list[torch.Tensor], y_fmt: str,
+             xs: list[torch.Tensor], x_fmt: str, N: int, K: int, Mo: int, f: int, cs: list[torch.Tensor],
+             y_scale_inv: torch.Tensor, x_scale_inv: torch.Tensor, c2s: list[torch.Tensor] | None = None,
+             auxs: list[torch.Tensor] | None = None) -> None:
+    """Grouped fp8 product with bf16 outputs (see rhp_fp8_gemm in include/resihp_moe.h)."""
+    G = offsets.numel() - 1
+    dev = _need_cuda(offsets, *ys, *xs, *cs, *(c2s or []), *(auxs or []), y_scale_inv, x_scale_inv)
+    ycode, ydt, _ = FP8_FORMATS[y_fmt]
+    xcode, xdt, _ = FP8_FORMATS[x_fmt]
+    _expect(len(cs) == G, f"expected {G} outputs")
+    for t in ys:
+        _expect(t.dtype == ydt, f"y operands must be {ydt}")
+    for t in xs:
+        _expect(t.dtype == xdt, f"x operands must be {xdt}")
+    for t in cs + (c2s or []) + (auxs or []):
+        _expect(t.dtype == torch.bfloat16 and t.dim() == 2, "outputs and pre-activations must be bf16 matrices")
+    _expect(x_scale_inv.dtype == torch.float32 and x_scale_inv.numel() in (1, G), "x_scale_inv must be float32 [1] or [G]")
+    _expect(y_scale_inv.dtype == torch.float32 and y_scale_inv.numel() == 1, "y_scale_inv must be float32 [1]")
+    if kgroups:
+        _expect(len(ys) == 1 and len(xs) == 1, "K-grouped products take one transposed buffer per operand")
+        _expect(ys[0].numel() >= fp8_transposed_numel(Mo, rows_cap, G), "y is too small")
+        _expect(xs[0].numel() >= fp8_transposed_numel(N, rows_cap, G), "x is too small")
+        for t in cs:
+            _expect(tuple(t.shape) == (Mo, N), f"outputs must be [{Mo}, {N}]")
+        ldy = ldx = 0
+    else:
+        _expect(len(ys) == G and len(xs) == G, f"expected {G} operands per side")
+        for t in ys:
+            _expect(t.dim() == 2 and t.shape[1] == K and t.shape[0] >= rows_cap, f"y must be [>= {rows_cap}, {K}]")
+        xrows = 2 * f if epi == "swiglu_fwd" else N
+        for t in xs:
+            _expect(tuple(t.shape) == (xrows, K), f"x must be [{xrows}, {K}]")
+        ldy = ldx = K
+    c2p = _arr(c2s) if c2s else None
+    auxp = _arr(auxs) if auxs else None
+    _call("rhp_fp8_gemm", dev, int(kgroups), EPI_CODES[epi], G, _ptr(offsets), rows_cap, ycode, xcode, N, K, Mo, f,
+          _arr(ys), ldy, _arr(xs), ldx, _arr(cs), cs[0].shape[1], c2p, c2s[0].shape[1] if c2s else 0, auxp,
+          auxs[0].shape[1] if auxs else 0, _ptr(y_scale_inv), _ptr(x_scale_inv),
+          0 if x_scale_inv.numel() == 1 else 1)

@@ -1,0 +1,179 @@
+"""FP8 experts on the GPU: delayed-scaling casts bit for bit against the oracle, and every fp8
+product against float64 on the dequantised operands.
+
+The cast must reproduce oracle/moe_ref.py's recipe exactly (scale from the
+amax history, saturating round-to-nearest-even to OCP e4m3 / e5m2), including
+the per-expert transposed copies with zero padding, the running amax and the
+history roll.  The products consume exactly the codes the cast wrote, so the
+float64 reference (codes / scale) differs from the kernel only by fp32
+accumulation and the bf16 rounding of the outputs.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _helpers import DEV, rel_err, say, seeded
+from oracle import moe_ref as M
+from resihp_megatron_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+BAR = 1e-2   # bf16 output rounding of products of exact fp8 codes
+
+
+def _offsets(counts):
+    return torch.tensor([0] + torch.tensor(counts).cumsum(0).tolist(), dtype=torch.int32)
+
+
+def _history(seed, L=16, scale=3.0):
+    return (torch.rand(L, generator=torch.Generator().manual_seed(seed), dtype=torch.float32) * scale + 0.1)
+
+
+def _cast(x, counts, hist, fmt, q=True, qt=True, margin=0):
+    """GPU cast of bf16 rows x (host) split into experts of `counts`."""
+    offs = _offsets(counts).to(DEV)
+    poff = K.fp8_padded_offsets(offs)
+    rows, cols = x.shape
+    _, fdt, _ = K.FP8_FORMATS[fmt]
+    amax = torch.zeros(1, dtype=torch.int32, device=DEV)
+    sinv = torch.zeros(1, dtype=torch.float32, device=DEV)
+    qd = torch.empty(rows, cols, dtype=fdt, device=DEV) if q else None
+    qtd = torch.zeros(K.fp8_transposed_numel(cols, rows, len(counts)), dtype=fdt, device=DEV) if qt else None
+    K.fp8_cast(x.to(DEV), offs, poff, rows, hist.to(DEV), fmt, amax, sinv, qd, qtd, margin)
+    return offs, poff, qd, qtd, amax, sinv
+
+
+def _codes(t):
+    return t.detach().cpu().view(torch.uint8)
+
+
+@pytest.mark.parametrize("fmt,margin", [("e4m3", 0), ("e5m2", 0), ("e4m3", 1)])
+def test_cast_matches_oracle_bits(fmt, margin):
+    counts = [300, 0, 17, 129]
+    cols = 192
+    x = seeded((sum(counts), cols), 11, 2.0, torch.bfloat16)
+    x[5, 7] = 900.0                      # saturates in e4m3 at scale > 0.5
+    hist = _history(3)
+    say(f"fp8 cast {fmt} margin={margin}")
+    offs, poff, q, qt, amax, sinv = _cast(x, counts, hist, fmt, margin=margin)
+    torch.cuda.synchronize()
+    scale = M.fp8_scale(hist.double(), fmt, margin)
+    ref = M.quantize(x.double(), scale, fmt).to(K.FP8_FORMATS[fmt][1])
+    assert torch.equal(_codes(q), ref.view(torch.uint8)), "row-major codes differ"
+    # transposed copies: expert g at cols * poff[g], [cols, R_g], zero past its rows
+    po = poff.cpu().tolist()
+    assert po == [0, 384, 384, 512, 768]
+    qt_h = _codes(qt)
+    o = _offsets(counts).tolist()
+    for g, n in enumerate(counts):
+        Rg = po[g + 1] - po[g]
+        blk = qt_h[cols * po[g]: cols * po[g + 1]].reshape(cols, Rg)
+        assert torch.equal(blk[:, :n], ref.view(torch.uint8)[o[g]:o[g + 1]].t()), f"expert {g} transposed codes differ"
+        assert not blk[:, n:].any(), f"expert {g} padding is not zero"
+    assert torch.equal(amax.cpu().view(torch.float32), x.float().abs().max().reshape(1))
+    assert sinv.item() == (torch.tensor(1.0) / torch.tensor(scale, dtype=torch.float32)).item()
+
+
+def test_cast_scale_falls_back_to_one():
+    x = seeded((64, 64), 12, 1.0, torch.bfloat16)
+    for hist in (torch.zeros(4), torch.tensor([1.0, float("nan"), 2.0, 3.0]), torch.tensor([float("inf"), 1.0])):
+        say(f"fp8 cast history {hist.tolist()}")
+        _, _, q, _, _, sinv = _cast(x, [64], hist, "e4m3", qt=False)
+        torch.cuda.synchronize()
+        assert M.fp8_scale(hist.double(), "e4m3") == 1.0
+        assert sinv.item() == 1.0
+        assert torch.equal(_codes(q), M.quantize(x.double(), 1.0, "e4m3").to(torch.float8_e4m3fn).view(torch.uint8))
+
+
+def test_amax_roll_newest_first():
+    hist = torch.tensor([[4.0, 3.0, 2.0, 1.0], [1.0, 1.0, 1.0, 1.0], [0.5, 0.25, 0.0, 0.0]])
+    amax = torch.tensor([9.0, 0.0, 7.5]).view(torch.int32)
+    h, a = hist.to(DEV), amax.to(DEV)
+    say("fp8 amax roll")
+    K.fp8_amax_roll(h, a)
+    torch.cuda.synchronize()
+    for i in range(3):
+        assert torch.equal(h[i].cpu(), M.amax_roll(hist[i], amax.view(torch.float32)[i]).float())
+    assert not a.cpu().any()
+
+
+def _deq(q, sinv):
+    return q.detach().cpu().to(torch.float64) * float(sinv.item())
+
+
+def _swiglu_bwd(da, hp, f):
+    g, u = hp[:, :f], hp[:, f:]
+    s = torch.sigmoid(g)
+    return torch.cat([da * u * s * (1 + g * (1 - s)), da * g * s], 1)
+
+
+GEMM_CASES = [
+    # (name, h, f, counts)
+    ("ragged", 256, 384, [200, 0, 300]),
+    ("one-expert-multi-tile", 512, 256, [700]),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=[c[0] for c in GEMM_CASES])
+def test_fp8_expert_products(case):
+    name, h, f, counts = case
+    G, P = len(counts), sum(counts)
+    o = _offsets(counts).tolist()
+    say(f"fp8 products {name}: h={h} f={f} counts={counts}")
+    x = seeded((P, h), 21, 1.0, torch.bfloat16)
+    w1 = [seeded((2 * f, h), 30 + g, 0.05, torch.bfloat16) for g in range(G)]
+    w2 = [seeded((h, f), 40 + g, 0.05, torch.bfloat16) for g in range(G)]
+    a = seeded((P, f), 22, 0.5, torch.bfloat16)
+    dy = seeded((P, h), 23, 0.01, torch.bfloat16)
+    dh = seeded((P, 2 * f), 24, 0.01, torch.bfloat16)
+    hist = _history(5)
+
+    offs, poff, xq, xqt, _, sx = _cast(x, counts, hist, "e4m3")
+    _, _, aq, aqt, _, sa = _cast(a, counts, hist, "e4m3")
+    _, _, dyq, dyqt, _, sdy = _cast(dy, counts, _history(6, scale=0.05), "e5m2")
+    _, _, dhq, dhqt, _, sdh = _cast(dh, counts, _history(7, scale=0.05), "e5m2")
+    w1q, w1qt, w2q, w2qt = [], [], [], []
+    sw1 = torch.empty(G, dtype=torch.float32, device=DEV)
+    sw2 = torch.empty(G, dtype=torch.float32, device=DEV)
+    for g in range(G):
+        hw = _history(50 + g, scale=0.2)
+        _, _, q1, t1, _, s1 = _cast(w1[g], [2 * f], hw, "e4m3")
+        _, _, q2, t2, _, s2 = _cast(w2[g], [h], hw, "e4m3")
+        w1q.append(q1); w1qt.append(t1[: 2 * f * h].view(h, 2 * f)); sw1[g:g + 1].copy_(s1)
+        w2q.append(q2); w2qt.append(t2[: h * f].view(f, h)); sw2[g:g + 1].copy_(s2)
+
+    hpre = torch.empty(P, 2 * f, dtype=torch.bfloat16, device=DEV)
+    act = torch.empty(P, f, dtype=torch.bfloat16, device=DEV)
+    y = torch.empty(P, h, dtype=torch.bfloat16, device=DEV)
+    dhpre = torch.empty(P, 2 * f, dtype=torch.bfloat16, device=DEV)
+    dxp = torch.empty(P, h, dtype=torch.bfloat16, device=DEV)
+    dw2 = [torch.empty(h, f, dtype=torch.bfloat16, device=DEV) for _ in range(G)]
+    dw1 = [torch.empty(2 * f, h, dtype=torch.bfloat16, device=DEV) for _ in range(G)]
+    hp_in = seeded((P, 2 * f), 25, 1.0, torch.bfloat16).to(DEV)
+
+    K.fp8_gemm(False, "swiglu_fwd", offs, P, [xq] * G, "e4m3", w1q, "e4m3", f, h, 0, f, [hpre] * G, sx, sw1,
+               c2s=[act] * G)
+    K.fp8_gemm(False, "store", offs, P, [aq] * G, "e4m3", w2q, "e4m3", h, f, 0, f, [y] * G, sa, sw2)
+    K.fp8_gemm(False, "swiglu_bwd", offs, P, [dyq] * G, "e5m2", w2qt, "e4m3", f, h, 0, f, [dhpre] * G, sdy, sw2,
+               auxs=[hp_in] * G)
+    K.fp8_gemm(False, "store", offs, P, [dhq] * G, "e5m2", w1qt, "e4m3", h, 2 * f, 0, f, [dxp] * G, sdh, sw1)
+    K.fp8_gemm(True, "store", poff, P, [dyqt], "e5m2", [aqt], "e4m3", f, 0, h, f, dw2, sdy, sa)
+    K.fp8_gemm(True, "store", poff, P, [dhqt], "e5m2", [xqt], "e4m3", h, 0, 2 * f, f, dw1, sdh, sx)
+    torch.cuda.synchronize()
+
+    xd, ad, dyd, dhd = _deq(xq, sx), _deq(aq, sa), _deq(dyq, sdy), _deq(dhq, sdh)
+    hp64 = hp_in.cpu().double()
+    for g in range(G):
+        r = slice(o[g], o[g + 1])
+        w1d, w2d = _deq(w1q[g], sw1[g]), _deq(w2q[g], sw2[g])
+        ref_h = xd[r] @ w1d.t()
+        assert rel_err(hpre[r], ref_h) <= BAR, f"fc1 fwd expert {g}"
+        assert rel_err(act[r], F.silu(ref_h[:, :f]) * ref_h[:, f:]) <= BAR, f"SwiGLU expert {g}"
+        assert rel_err(y[r], ad[r] @ w2d.t()) <= BAR, f"fc2 fwd expert {g}"
+        assert rel_err(dhpre[r], _swiglu_bwd(dyd[r] @ w2d, hp64[r], f)) <= BAR, f"fc2 dgrad expert {g}"
+        assert rel_err(dxp[r], dhd[r] @ w1d) <= BAR, f"fc1 dgrad expert {g}"
+        assert rel_err(dw2[g], dyd[r].t() @ ad[r]) <= BAR, f"fc2 wgrad expert {g}"
+        assert rel_err(dw1[g], dhd[r].t() @ xd[r]) <= BAR, f"fc1 wgrad expert {g}"
