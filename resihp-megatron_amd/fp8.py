@@ -1,0 +1,91 @@
+"""Delayed-scaling state of one MoE layer whose experts run in fp8.
+
+The reference keeps an FP8-style amax history per layer
+(resihp/runtime/reference_model.py:44-46, 204-207): a buffer of L entries, a
+pending amax raised during the iteration, and at the end of the iteration the
+amax prepended newest-first (:212-216).  Here every quantised tensor of the
+layer has such a history:
+
+    0  expert-input rows (fc1 input)          e4m3
+    1  SwiGLU / GELU output rows (fc2 input)  e4m3
+    2  gradient of the expert outputs         e5m2
+    3  gradient of the pre-activations        e5m2
+    4 + g        fc1 weight of local expert g   e4m3
+    4 + G + g    fc2 weight of local expert g   e4m3
+
+All of it lives on the device; casts raise the pending amax with atomics and
+``finish_iteration`` rolls every history in one kernel, so the layer never
+synchronises with the host for scaling.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import kernels as K
+
+X, ACT, DY, DH = 0, 1, 2, 3
+FORMATS = {X: "e4m3", ACT: "e4m3", DY: "e5m2", DH: "e5m2"}
+
+
+class Fp8State:
+    """Histories [n, L] (float32), pending amax [n] (float bits in int32) and 1/scale [n] (float32)."""
+
+    def __init__(self, num_local_experts: int, history_len: int = 16, margin: int = 0,
+                 device: torch.device | str = "cuda"):
+        if num_local_experts < 1 or history_len < 1 or margin < 0:
+            raise ValueError("need at least one expert, a positive history length and a margin >= 0")
+        self.G = num_local_experts
+        self.L = history_len
+        self.margin = margin
+        n = 4 + 2 * num_local_experts
+        self.history = torch.ones(n, history_len, dtype=torch.float32, device=device)   # reference init: ones
+        self.amax = torch.zeros(n, dtype=torch.int32, device=device)
+        self.scale_inv = torch.ones(n, dtype=torch.float32, device=device)
+        self._ranges: dict[tuple[int, str], tuple[torch.Tensor, torch.Tensor]] = {}
+
+    def w1(self, g: int) -> int:
+        return 4 + g
+
+    def w2(self, g: int) -> int:
+        return 4 + self.G + g
+
+    def seed_history(self, priors: dict[int, float], seed: int = 0, spread: float = 0.25) -> None:
+        """Prior amax values: history[i] = priors[i] * (1 + spread * u), u ~ U(-1, 1) from a seeded generator.
+
+        ``priors`` maps a tensor index (X, ACT, DY, DH, w1(g), w2(g)) to its nominal amax; indices not
+        given keep their history.
+        """
+        g = torch.Generator().manual_seed(seed)
+        h = self.history.cpu()
+        for i, a in priors.items():
+            u = torch.rand(self.L, generator=g, dtype=torch.float64) * 2 - 1
+            h[i] = (a * (1 + spread * u)).float()
+        self.history.copy_(h)
+
+    def finish_iteration(self) -> None:
+        """Prepend every pending amax to its history and reset it (reference_model.py:212-216)."""
+        K.fp8_amax_roll(self.history, self.amax)
+
+    def single_range(self, rows: int, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+        """Offsets [0, rows] and padded offsets of a one-group cast (a weight matrix), cached per size."""
+        key = (rows, str(device))
+        if key not in self._ranges:
+            if rows % K.FP8_ALIGN:
+                raise ValueError(f"fp8 weights need row counts that are multiples of {K.FP8_ALIGN}, got {rows}")
+            t = torch.tensor([0, rows], dtype=torch.int32, device=device)
+            self._ranges[key] = (t, t.clone())
+        return self._ranges[key]
+
+    def cast(self, i: int, x: torch.Tensor, offsets: torch.Tensor, poff: torch.Tensor, rows_cap: int,
+             row_major: bool = True, transposed: bool = True) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+        """Casts rows of ``x`` with tensor i's scale; returns (row-major fp8, per-expert transposed fp8)."""
+        fmt = FORMATS.get(i, "e4m3")
+        fdt = K.FP8_FORMATS[fmt][1]
+        rows, cols = x.shape
+        G = offsets.numel() - 1
+        q = torch.empty(rows, cols, dtype=fdt, device=x.device) if row_major else None
+        qt = torch.empty(K.fp8_transposed_numel(cols, rows_cap, G), dtype=fdt, device=x.device) if transposed else None
+        K.fp8_cast(x, offsets, poff, rows_cap, self.history[i], fmt, self.amax[i:i + 1], self.scale_inv[i:i + 1], q, qt,
+                   self.margin)
+        return q, qt

@@ -20,6 +20,7 @@ from dataclasses import dataclass
 import torch
 
 from . import kernels as K
+from .fp8 import ACT, DH, DY, X, Fp8State
 
 
 @dataclass(frozen=True)
@@ -50,9 +51,65 @@ def _fc1_rows(act: str, f: int) -> int:
     return 2 * f if act == "swiglu" else f
 
 
+def _fp8_forward(st: Fp8State, meta: LayerMeta, offsets, P, xp, fc1s, fc2s, hpre, act, y):
+    """Expert FFN forward in fp8; returns what the backward needs (codes and transposed copies)."""
+    G, f = st.G, meta.ffn
+    h = xp.shape[1]
+    dev = xp.device
+    w1q, w1qt, w2q, w2qt = [], [], [], []
+    for g, (w1, w2) in enumerate(zip(fc1s, fc2s)):
+        o1, p1 = st.single_range(w1.shape[0], dev)
+        q, qt = st.cast(st.w1(g), w1, o1, p1, w1.shape[0])
+        w1q.append(q)
+        w1qt.append(qt[:w1.numel()].view(w1.shape[1], w1.shape[0]))
+        o2, p2 = st.single_range(w2.shape[0], dev)
+        q, qt = st.cast(st.w2(g), w2, o2, p2, w2.shape[0])
+        w2q.append(q)
+        w2qt.append(qt[:w2.numel()].view(w2.shape[1], w2.shape[0]))
+    sw1 = st.scale_inv[st.w1(0):st.w1(0) + G]
+    sw2 = st.scale_inv[st.w2(0):st.w2(0) + G]
+    poff = K.fp8_padded_offsets(offsets)
+    xqt = aqt = None
+    if P > 0:
+        xq, xqt = st.cast(X, xp, offsets, poff, P)
+        epi = "swiglu_fwd" if meta.act == "swiglu" else "gelu_fwd"
+        K.fp8_gemm(False, epi, offsets, P, [xq] * G, "e4m3", w1q, "e4m3", f, h, 0, f, [hpre] * G,
+                   st.scale_inv[X:X + 1], sw1, c2s=[act] * G)
+        aq, aqt = st.cast(ACT, act, offsets, poff, P)
+        K.fp8_gemm(False, "store", offsets, P, [aq] * G, "e4m3", w2q, "e4m3", h, f, 0, f, [y] * G,
+                   st.scale_inv[ACT:ACT + 1], sw2)
+    return dict(poff=poff, xqt=xqt, aqt=aqt, w1qt=w1qt, w2qt=w2qt, sw1=sw1, sw2=sw2)
+
+
+def _fp8_backward(st: Fp8State, q8: dict, meta: LayerMeta, offsets, P, dy, hpre, dxp, dw1, dw2):
+    """Expert FFN backward in fp8 (e5m2 gradients, e4m3 weights and activations)."""
+    G, f = st.G, meta.ffn
+    h = dy.shape[1]
+    F1 = _fc1_rows(meta.act, f)
+    if P == 0:
+        for w in (*dw1, *dw2):
+            w.zero_()
+        return
+    poff = q8["poff"]
+    s = st.scale_inv
+    dyq, dyqt = st.cast(DY, dy, offsets, poff, P)
+    dhpre = dy.new_empty(P, F1)
+    epi = "swiglu_bwd" if meta.act == "swiglu" else "gelu_bwd"
+    K.fp8_gemm(False, epi, offsets, P, [dyq] * G, "e5m2", q8["w2qt"], "e4m3", f, h, 0, f, [dhpre] * G,
+               s[DY:DY + 1], q8["sw2"], auxs=[hpre] * G)
+    K.fp8_gemm(True, "store", poff, P, [dyqt], "e5m2", [q8["aqt"]], "e4m3", f, 0, h, f, list(dw2), s[DY:DY + 1],
+               s[ACT:ACT + 1])
+    dhq, dhqt = st.cast(DH, dhpre, offsets, poff, P)
+    if dxp is not None:
+        K.fp8_gemm(False, "store", offsets, P, [dhq] * G, "e5m2", q8["w1qt"], "e4m3", h, F1, 0, f, [dxp] * G,
+                   s[DH:DH + 1], q8["sw1"])
+    K.fp8_gemm(True, "store", poff, P, [dhqt], "e5m2", [q8["xqt"]], "e4m3", h, 0, F1, f, list(dw1), s[DH:DH + 1],
+               s[X:X + 1])
+
+
 class _MoELayerFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, meta: LayerMeta, x, router_w, bias, *weights):
+    def forward(ctx, meta: LayerMeta, fp8, x, router_w, bias, *weights):
         e0, e1 = meta.window
         G = e1 - e0
         S = meta.num_shared
@@ -70,7 +127,10 @@ class _MoELayerFn(torch.autograd.Function):
         hpre = x.new_empty(P, F1)
         act = x.new_empty(P, f)
         y = x.new_empty(P, h)
-        if P > 0:
+        q8 = None
+        if fp8 is not None:
+            q8 = _fp8_forward(fp8, meta, plan.offsets, P, xp, fc1s, fc2s, hpre, act, y)
+        elif P > 0:
             K.expert_fc1_fwd([xp] * G, plan.offsets, True, P, fc1s, f, meta.act, [hpre] * G, [act] * G)
             K.expert_fc2_fwd([act] * G, plan.offsets, True, P, fc2s, [y] * G)
         shared_off = shared_h = shared_a = shared_y = None
@@ -85,6 +145,7 @@ class _MoELayerFn(torch.autograd.Function):
                 K.expert_fc2_fwd(shared_a, shared_off, False, T, sfc2s, shared_y)
         out = K.combine(y, x, gates, topi, plan.pair_row, shared_y or [])
         ctx.meta = meta
+        ctx.fp8 = (fp8, q8)
         ctx.dims = (T, h, P, G, S)
         ctx.save_for_backward(x, router_w, logits, topi, gates, plan.perm, plan.offsets, plan.pair_row, xp, hpre,
                               act, y, *fc1s, *fc2s, *sfc1s, *sfc2s)
@@ -102,12 +163,15 @@ class _MoELayerFn(torch.autograd.Function):
         shared_off, shared_h, shared_a = ctx.shared
         f = meta.ffn
         dout = dout.contiguous()
-        need_x = ctx.needs_input_grad[1]
+        need_x = ctx.needs_input_grad[2]
         dy, dgates = K.combine_bwd(dout, y, gates, pair_row, P)
         dw2 = [torch.empty_like(w) for w in fc2s]
         dw1 = [torch.empty_like(w) for w in fc1s]
         dxp = x.new_empty(P, h) if need_x else None
-        if P > 0:
+        fp8, q8 = ctx.fp8
+        if fp8 is not None:
+            _fp8_backward(fp8, q8, meta, offsets, P, dy, hpre, dxp, dw1, dw2)
+        elif P > 0:
             dhpre = x.new_empty(P, _fc1_rows(meta.act, f))
             K.expert_fc2_bwd([dy] * G, [act] * G, [hpre] * G, offsets, True, P, fc2s, meta.act, [dhpre] * G, dw2)
             K.expert_fc1_bwd([dhpre] * G, [xp] * G, offsets, True, P, fc1s, f, meta.act,
@@ -127,25 +191,37 @@ class _MoELayerFn(torch.autograd.Function):
         dl = K.route_bwd(dgates, gates, logits, topi, meta.score, meta.normalize, meta.gate_scale)
         dx = K.token_bwd(dout, dxp, pair_row, dl, topi, router_w, shared_dx) if need_x else None
         dwr = None
-        if ctx.needs_input_grad[2]:
+        if ctx.needs_input_grad[3]:
             if meta.full:
                 rperm, roff = perm, offsets
             else:
                 full_plan = K.dispatch(topi, meta.num_experts)
                 rperm, roff = full_plan.perm, full_plan.offsets
             dwr = K.router_wgrad(dl, rperm, roff, x, meta.num_experts, router_w.dtype)
-        return (None, dx, dwr, None, *dw1, *dw2, *sdw1, *sdw2)
+        return (None, None, dx, dwr, None, *dw1, *dw2, *sdw1, *sdw2)
 
 
 def moe_layer(meta: LayerMeta, x: torch.Tensor, router_w: torch.Tensor, bias: torch.Tensor | None,
               fc1s: list[torch.Tensor], fc2s: list[torch.Tensor], shared_fc1s: list[torch.Tensor] = (),
-              shared_fc2s: list[torch.Tensor] = ()) -> tuple[torch.Tensor, torch.Tensor]:
-    """Layer output and the int32 per-expert counts (``counts[E]`` counts invalid ids)."""
+              shared_fc2s: list[torch.Tensor] = (), fp8: Fp8State | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Layer output and the int32 per-expert counts (``counts[E]`` counts invalid ids).
+
+    With ``fp8`` the routed experts run in fp8 (e4m3 weights and activations, e5m2 gradients) with the
+    delayed scaling of that state; the caller ends each iteration with ``fp8.finish_iteration()``.
+    """
     e0, e1 = meta.window
+    if fp8 is not None:
+        if fp8.G != e1 - e0:
+            raise ValueError(f"the fp8 state holds {fp8.G} experts, the window {e1 - e0}")
+        if meta.num_shared:
+            raise ValueError("fp8 experts: shared experts are not supported")
+        h, F1 = fc1s[0].shape[1], _fc1_rows(meta.act, meta.ffn)
+        if x.dtype != torch.bfloat16 or h % K.FP8_ALIGN or meta.ffn % K.FP8_ALIGN:
+            raise ValueError(f"fp8 experts need bf16 tokens and hidden/ffn sizes that are multiples of {K.FP8_ALIGN}")
     if len(fc1s) != e1 - e0 or len(fc2s) != e1 - e0:
         raise ValueError(f"need one fc1 and one fc2 weight per local expert ({e1 - e0})")
     if len(shared_fc1s) != meta.num_shared or len(shared_fc2s) != meta.num_shared:
         raise ValueError(f"need {meta.num_shared} shared expert weight pairs")
-    return _MoELayerFn.apply(meta, x.contiguous(), router_w.contiguous(),
+    return _MoELayerFn.apply(meta, fp8, x.contiguous(), router_w.contiguous(),
                              None if bias is None else bias.detach().contiguous(),
                              *fc1s, *fc2s, *shared_fc1s, *shared_fc2s)

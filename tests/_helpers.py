@@ -30,6 +30,14 @@ def rel_err(a: torch.Tensor, b: torch.Tensor) -> float:
     return (a - b).abs().max().item() / denom
 
 
+def frob_err(a: torch.Tensor, b: torch.Tensor) -> float:
+    """||a - b|| / ||b|| (Frobenius), the usual accuracy measure of fp8 training."""
+    a = a.detach().to("cpu", torch.float64)
+    b = b.detach().to("cpu", torch.float64)
+    nb = b.norm().item()
+    return (a - b).norm().item() / nb if nb else a.norm().item()
+
+
 def bf16_bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 

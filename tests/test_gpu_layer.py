@@ -18,19 +18,28 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import DEV, TOL, rel_err, say, seeded, zipf_prior
+from _helpers import DEV, TOL, frob_err, rel_err, say, seeded, zipf_prior
 from oracle import moe_ref as M
 from oracle import route_c as R
 from resihp_megatron_amd import kernels as K
 from resihp_megatron_amd import moe, placement
+from resihp_megatron_amd.fp8 import Fp8State
 from resihp_megatron_amd.layer import LayerMeta, moe_layer
 
 pytestmark = pytest.mark.gpu
 
+# fp8 experts (e4m3 forward, e5m2 gradients, per-tensor delayed scaling) against the unquantised
+# float64 layer.  Exact quantisation alone already moves a random-data layer this far (a float64
+# emulation of the recipe: output 7e-2 max-relative, weight gradients 8e-2 to 1.3e-1 max-relative and
+# 8e-2 to 9e-2 in norm): e4m3 keeps 3 mantissa bits, e5m2 2.  Output and input gradient are held to
+# max-relative bars, weight gradients to a norm-relative bar, because with few rows per expert one
+# product dominates a weight-gradient element and the max-relative statistic then measures a single
+# rounding.  test_gpu_fp8.py checks the kernels against that exact emulation.
+FP8_TOL = {"out": 1e-1, "dx": 1.5e-1, "grad_norm": 1.5e-1}
 GOLD = np.load(pathlib.Path(__file__).resolve().parent / "golden" / "reference_moe.npz")
 
 
-def _run(name, cfg: moe.MoEConfig, window=None, n_src=1, bias=None, check_route=False):
+def _run(name, cfg: moe.MoEConfig, window=None, n_src=1, bias=None, check_route=False, fp8=False):
     E = cfg.num_experts
     e0, e1 = window or (0, E)
     specs = moe.moe_specs(cfg)
@@ -47,8 +56,19 @@ def _run(name, cfg: moe.MoEConfig, window=None, n_src=1, bias=None, check_route=
     s2 = [params[f"shared_experts.{s}.fc2.weight"] for s in range(cfg.num_shared)]
     bias_d = None if bias is None else bias.to(DEV, moe.router_dtype(cfg))
     say(f"layer {name}: T={cfg.tokens} h={cfg.hidden} f={cfg.ffn} E={E} k={cfg.top_k} window=[{e0},{e1})")
-    out, counts = moe_layer(meta, x, params["router.weight"], bias_d, fc1s, fc2s, s1, s2)
-    dout = seeded(out.shape, 77, 1.0, out.dtype).to(DEV)
+    dout = seeded((cfg.tokens, cfg.hidden), 77, 1.0, x.dtype).to(DEV)
+    st = None
+    if fp8:
+        # Delayed scaling: one calibration iteration records every tensor's amax, which then seeds
+        # the 16-step histories (prior values spread by +-25%) of the measured iteration.
+        st = Fp8State(e1 - e0, 16, device=DEV)
+        out0, _ = moe_layer(meta, x, params["router.weight"], bias_d, fc1s, fc2s, s1, s2, fp8=st)
+        out0.backward(dout)
+        st.finish_iteration()
+        st.seed_history({i: float(a) for i, a in enumerate(st.history[:, 0].tolist())}, seed=5)
+        for t in (x, *params.values()):
+            t.grad = None
+    out, counts = moe_layer(meta, x, params["router.weight"], bias_d, fc1s, fc2s, s1, s2, fp8=st)
     out.backward(dout)
     _, topi, _ = K.route(x.detach(), params["router.weight"].detach(), bias_d, cfg.top_k, cfg.score,
                          cfg.normalize, cfg.gate_scale)
@@ -71,6 +91,15 @@ def _run(name, cfg: moe.MoEConfig, window=None, n_src=1, bias=None, check_route=
     x64 = x.detach().cpu().double().requires_grad_(True)
     ref = M.layer_forward(ocfg, p64, x64, topi=topi.long(), local=(e0, e1))
     ref.backward(dout.cpu().double())
+    if fp8:
+        errs = {"out": rel_err(out, ref), "dx": rel_err(x.grad, x64.grad)}
+        gerr = {k: frob_err(params[k].grad, p64[k].grad if p64[k].grad is not None else torch.zeros_like(p64[k]))
+                for k in params}
+        say(f"  out {errs['out']:.3e} dx {errs['dx']:.3e} gradient norm errors "
+            + " ".join(f"{k.replace('experts.', 'e').replace('.weight', '')}={e:.2e}" for k, e in gerr.items()))
+        assert errs["out"] <= FP8_TOL["out"] and errs["dx"] <= FP8_TOL["dx"], errs
+        assert max(gerr.values()) <= FP8_TOL["grad_norm"], gerr
+        return plan
     tol = TOL[cfg.dtype]
     errs = {"out": rel_err(out, ref), "dx": rel_err(x.grad, x64.grad)}
     for k in params:
@@ -113,6 +142,52 @@ def test_config4_ep_share_zipf(window):
     assert plan["src_counts"].shape == (8, 16)
     if window[0] == 112:
         assert (plan["counts"][112:128] == 0).any(), "the Zipf tail share should hold empty experts"
+
+
+def test_config5_fp8_mixtral_shape():
+    _run("c5-fp8-mixtral", moe.MoEConfig(hidden=4096, ffn=14336, num_experts=8, top_k=2, tokens=64, act="swiglu",
+                                         dtype=torch.bfloat16, init_std=0.02, device=DEV), fp8=True)
+
+
+def test_config5_fp8_gelu_ragged():
+    _run("c5-fp8-gelu", moe.MoEConfig(hidden=256, ffn=384, num_experts=8, top_k=2, tokens=300, act="gelu",
+                                      dtype=torch.bfloat16, init_std=0.05, device=DEV), fp8=True)
+
+
+def test_config5_fp8_full_size_against_bf16():
+    """Config 5 at its full size (16384 tokens, Mixtral shape): the fp8 layer against the bf16 layer
+    (itself within 2e-2 of float64), output and every gradient within the fp8 bars."""
+    T, h, f, E, k = 16384, 4096, 14336, 8, 2
+    g = torch.Generator(device=DEV).manual_seed(9)
+    rnd = lambda *s, std=1.0, dt=torch.bfloat16: (torch.randn(*s, generator=g, device=DEV) * std).to(dt)
+    x = rnd(T, h).requires_grad_(True)
+    router = rnd(E, h, std=0.02, dt=torch.float32).requires_grad_(True)
+    fc1 = [rnd(2 * f, h, std=0.02).requires_grad_(True) for _ in range(E)]
+    fc2 = [rnd(h, f, std=0.02).requires_grad_(True) for _ in range(E)]
+    dout = rnd(T, h)
+    meta = LayerMeta(num_experts=E, top_k=k, ffn=f, act="swiglu")
+    say("layer c5-fp8 full size: bf16 pass")
+    out, _ = moe_layer(meta, x, router, None, fc1, fc2)
+    out.backward(dout)
+    ref = [out.detach().clone(), x.grad.clone(), router.grad.clone()] + [w.grad.clone() for w in fc1 + fc2]
+    st = Fp8State(E, 16, device=DEV)
+    for it in range(2):   # the first iteration calibrates the histories
+        for t in (x, router, *fc1, *fc2):
+            t.grad = None
+        say(f"layer c5-fp8 full size: fp8 iteration {it}")
+        out, _ = moe_layer(meta, x, router, None, fc1, fc2, fp8=st)
+        out.backward(dout)
+        st.finish_iteration()
+        if it == 0:
+            st.seed_history({i: float(a) for i, a in enumerate(st.history[:, 0].tolist())}, seed=6)
+    got = [out.detach(), x.grad, router.grad] + [w.grad for w in fc1 + fc2]
+    torch.cuda.synchronize()
+    e_out, e_dx = rel_err(got[0], ref[0]), rel_err(got[1], ref[1])
+    gerr = [frob_err(a, b) for a, b in zip(got[2:], ref[2:])]
+    say(f"  out {e_out:.3e} dx {e_dx:.3e} gradient norm errors (router, fc1s, fc2s) "
+        + " ".join(f"{e:.2e}" for e in gerr))
+    assert e_out <= FP8_TOL["out"] and e_dx <= FP8_TOL["dx"], (e_out, e_dx)
+    assert max(gerr) <= FP8_TOL["grad_norm"], gerr
 
 
 def test_reference_default_gelu_fp64():
