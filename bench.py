@@ -1,12 +1,19 @@
 """MoE-layer throughput benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload mixtral|...] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload mixtral|dsv2lite|ep128-share|mixtral-fp8]
+                    [--no-cpu-baseline]
 
 One step is one forward + backward of the MoE layer over one batch of
-synthetic tokens at the Mixtral-8x7B layer shape (hidden 4096, 8 experts,
-ffn 14336 SwiGLU, top-2 softmax router in float32, 8192 tokens, bfloat16),
-with inputs and weights already resident in HBM.  Weights are random
-N(0, 0.02) of that architecture, drawn on the device; tokens are N(0, 1).
+synthetic tokens, with inputs and weights already resident in HBM.  The
+default workload is the Mixtral-8x7B layer shape (hidden 4096, 8 experts,
+ffn 14336 SwiGLU, top-2 softmax router in float32, 8192 tokens, bfloat16).
+Weights are random N(0, 0.02) of the architecture, drawn on the device;
+tokens are N(0, 1).  The other workloads are the fine-grained layer with
+shared experts and a sigmoid router with selection bias (dsv2lite), one
+GPU's 16-expert share of a 128-expert top-8 layer under a Zipf(1.1)
+selection prior (ep128-share), and the Mixtral shape with 16384 tokens and
+fp8 experts under delayed scaling (mixtral-fp8; its step includes the end of
+iteration amax-history roll).
 
 Prints one JSON line: whole-job tokens/s, the grouped-GEMM roofline fraction
 (algorithmic FLOPs / the GEMM kernels' HIP-event time / dense bf16 peak),
@@ -32,12 +39,15 @@ PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0        # MI355X HBM3E
 
 WORKLOADS = {
-    # name: (tokens, hidden, ffn, experts, top_k, score, num_shared)
-    "mixtral": (8192, 4096, 14336, 8, 2, "softmax", 0),
-    "dsv2lite": (16384, 2048, 1408, 64, 6, "sigmoid", 2),
+    # name: (tokens, hidden, ffn, experts, top_k, score, num_shared, window, n_src, selection bias, fp8)
+    "mixtral": (8192, 4096, 14336, 8, 2, "softmax", 0, None, 1, None, False),
+    "dsv2lite": (16384, 2048, 1408, 64, 6, "sigmoid", 2, None, 1, "normal", False),
+    "ep128-share": (32768, 2048, 768, 128, 8, "softmax", 0, (0, 16), 8, "zipf", False),
+    "mixtral-fp8": (16384, 4096, 14336, 8, 2, "softmax", 0, None, 1, None, True),
 }
 
-GEMM_CALLS = ("rhp_expert_fc1_fwd", "rhp_expert_fc2_fwd", "rhp_expert_fc2_bwd", "rhp_expert_fc1_bwd")
+GEMM_CALLS = ("rhp_expert_fc1_fwd", "rhp_expert_fc2_fwd", "rhp_expert_fc2_bwd", "rhp_expert_fc1_bwd", "rhp_fp8_gemm")
+PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 
 
 def _package():
@@ -79,29 +89,44 @@ class EventTimer:
 
 
 def build_workload(name: str, dev: torch.device):
-    T, h, f, E, k, score, S = WORKLOADS[name]
+    T, h, f, E, k, score, S, window, n_src, bias_kind, fp8 = WORKLOADS[name]
+    e0, e1 = window or (0, E)
     g = torch.Generator(device=dev).manual_seed(1234)
 
     def randn(*shape, std=1.0, dtype=torch.bfloat16):
         return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * std).to(dtype)
 
     router = randn(E, h, std=0.02, dtype=torch.float32).requires_grad_(True)
-    fc1 = [randn(2 * f, h, std=0.02).requires_grad_(True) for _ in range(E)]
-    fc2 = [randn(h, f, std=0.02).requires_grad_(True) for _ in range(E)]
+    fc1 = [randn(2 * f, h, std=0.02).requires_grad_(True) for _ in range(e1 - e0)]
+    fc2 = [randn(h, f, std=0.02).requires_grad_(True) for _ in range(e1 - e0)]
     s1 = [randn(2 * f, h, std=0.02).requires_grad_(True) for _ in range(S)]
     s2 = [randn(h, f, std=0.02).requires_grad_(True) for _ in range(S)]
-    bias = randn(E, std=0.1, dtype=torch.float32) if score == "sigmoid" else None
+    if bias_kind == "normal":
+        bias = randn(E, std=0.1, dtype=torch.float32)
+    elif bias_kind == "zipf":   # selection prior of a Zipf(1.1) expert popularity: -1.1 ln(e + 1)
+        bias = (-1.1 * torch.log(torch.arange(1, E + 1, dtype=torch.float64))).float().to(dev)
+    else:
+        bias = None
     x = randn(T, h).requires_grad_(True)
     dout = randn(T, h)
-    return dict(T=T, h=h, f=f, E=E, k=k, score=score, S=S, router=router, fc1=fc1, fc2=fc2, s1=s1, s2=s2,
-                bias=bias, x=x, dout=dout)
+    st = None
+    if fp8:
+        _package()
+        from resihp_megatron_amd.fp8 import Fp8State
+        st = Fp8State(e1 - e0, 16, device=dev)
+    return dict(T=T, h=h, f=f, E=E, k=k, score=score, S=S, e0=e0, e1=e1, n_src=n_src, router=router, fc1=fc1,
+                fc2=fc2, s1=s1, s2=s2, bias=bias, x=x, dout=dout, fp8=st)
 
 
 def gpu_step(pkg, w, meta):
     for p in (w["x"], w["router"], *w["fc1"], *w["fc2"], *w["s1"], *w["s2"]):
         p.grad = None
-    out, _ = pkg.layer.moe_layer(meta, w["x"], w["router"], w["bias"], w["fc1"], w["fc2"], w["s1"], w["s2"])
+    out, counts = pkg.layer.moe_layer(meta, w["x"], w["router"], w["bias"], w["fc1"], w["fc2"], w["s1"], w["s2"],
+                                      fp8=w["fp8"])
     out.backward(w["dout"])
+    if w["fp8"] is not None:
+        w["fp8"].finish_iteration()
+    return counts
 
 
 def cpu_baseline(name: str, sample_tokens: int, reps: int = 3) -> dict:
@@ -110,7 +135,7 @@ def cpu_baseline(name: str, sample_tokens: int, reps: int = 3) -> dict:
         sys.path.insert(0, str(ROOT))
     from oracle import moe_ref as M
 
-    T, h, f, E, k, score, S = WORKLOADS[name]
+    T, h, f, E, k, score, S = WORKLOADS[name][:7]
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     cfg = M.OracleConfig(hidden=h, ffn=f, num_experts=E, top_k=k, tokens=sample_tokens, act="swiglu", score=score,
@@ -158,10 +183,14 @@ def main() -> int:
     w = build_workload(args.workload, dev)
     T, h, f, E, k = w["T"], w["h"], w["f"], w["E"], w["k"]
     meta = pkg.layer.LayerMeta(num_experts=E, top_k=k, ffn=f, act="swiglu", score=w["score"],
-                               num_shared=w["S"], shared_ffn=f if w["S"] else 0)
+                               num_shared=w["S"], shared_ffn=f if w["S"] else 0, e0=w["e0"], e1=w["e1"],
+                               n_src=w["n_src"])
+    counts = None
     for _ in range(args.warmup):
-        gpu_step(pkg, w, meta)
+        counts = gpu_step(pkg, w, meta)
     torch.cuda.synchronize()
+    # Routed pairs on this GPU (the routing is the same every step: same tokens and router).
+    P = int(counts[w["e0"]:w["e1"]].sum().item()) if counts is not None else T * k
 
     timer = EventTimer()
     kernels.set_timer(timer)
@@ -174,8 +203,9 @@ def main() -> int:
     kernels.set_timer(None)
 
     per = {name: (ms / args.steps, n // args.steps) for name, (ms, n) in timer.totals_ms().items()}
-    P = T * k
     S = w["S"]
+    fp8 = w["fp8"] is not None
+    peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
     gemm_flops = 18.0 * (P + S * T) * h * f          # SwiGLU: fwd 6 P h f + bwd 12 P h f
     gemm_ms = sum(per.get(n, (0.0, 0))[0] for n in GEMM_CALLS)
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
@@ -201,15 +231,17 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8 (e4m3 fwd, e5m2 grads) with bf16 outputs" if fp8 else "bf16",
         "data": "synthetic (N(0,1) tokens, random N(0,0.02) weights of the layer shape, drawn on device)",
         "config": {"workload": f"{args.workload} MoE layer: tokens={T}, hidden={h}, ffn={f} SwiGLU, experts={E}, "
-                               f"top_k={k} {w['score']} router (fp32), shared experts={S}, bf16, fwd+bwd",
-                   "tokens": T, "hidden": h, "ffn": f, "experts": E, "top_k": k, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": gemm_tflops / PEAK_BF16_TFLOPS, "traffic": None,
+                               f"local experts [{w['e0']}, {w['e1']}), top_k={k} {w['score']} router (fp32), "
+                               f"shared experts={S}, {'fp8 experts' if fp8 else 'bf16'}, fwd+bwd",
+                   "tokens": T, "hidden": h, "ffn": f, "experts": E, "top_k": k, "local_experts": w["e1"] - w["e0"],
+                   "routed_pairs": P, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": peak, "unit": "TFLOP/s",
+                     "frac": gemm_tflops / peak, "traffic": None,
                      "kernel": "grouped expert GEMMs (fc1/fc2 fwd, dgrad, wgrad)",
-                     "algorithmic": f"18*P*h*f = {gemm_flops:.4g} FLOP per step, P = {P} routed pairs"},
+                     "algorithmic": f"18*(P + S*T)*h*f = {gemm_flops:.4g} FLOP per step, P = {P} routed pairs"},
         "rows_roofline": {"bound": "hbm", "achieved": row_gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                           "frac": (row_gbps / PEAK_HBM_GBPS) if row_gbps else None,
                           "kernel": "permute + combine + combine_bwd + token_bwd"},
