@@ -77,11 +77,29 @@ struct CastParams {
 
 constexpr int kCastTile = 64;
 
-// One block: 64 rows x 64 columns of one expert; thread t covers row t / 4 and
-// 16 columns.  Rows past the expert's count quantise to zero (qt padding).
+// 4 x 4 byte transpose: word j holds bytes (row j, cols 0..3); word i of the
+// result holds bytes (rows 0..3, col i).
+__device__ __forceinline__ void transpose4x4(const uint32_t a[4], uint32_t b[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(a[1], a[0], 0x05010400u);   // a0.0 a1.0 a0.1 a1.1
+    const uint32_t t1 = __builtin_amdgcn_perm(a[1], a[0], 0x07030602u);   // a0.2 a1.2 a0.3 a1.3
+    const uint32_t t2 = __builtin_amdgcn_perm(a[3], a[2], 0x05010400u);   // a2.0 a3.0 a2.1 a3.1
+    const uint32_t t3 = __builtin_amdgcn_perm(a[3], a[2], 0x07030602u);   // a2.2 a3.2 a2.3 a3.3
+    b[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    b[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    b[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    b[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+
+// One block: 64 rows x 64 columns of one expert; thread t quantises row t / 4,
+// columns 16 (t % 4) .. +15.  Rows past the expert's count quantise to zero
+// (qt padding).  The transposed copy goes through LDS as words (rows padded to
+// 17 words, so the column reads below hit 64 distinct banks); thread t then
+// transposes the 4 x 4 byte block (rows 4 (t % 16) .., columns 4 (t / 16) ..)
+// in registers and writes 4 bytes to each of 4 output rows, 16 lanes covering
+// 64 contiguous bytes of one output row.
 template <int FMT>
 __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
-    __shared__ uint8_t tr[kCastTile][kCastTile + 16];
+    __shared__ uint32_t tw[kCastTile][kCastTile / 4 + 1];
     __shared__ float wave_max[4];
     const int ct_n = c.cols / kCastTile;
     uint32_t b = blockIdx.x;
@@ -143,24 +161,27 @@ __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
     if ((t & 63) == 0) wave_max[t >> 6] = m;
     if (c.qt) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) tr[cs + i][r] = static_cast<uint8_t>(packed[i >> 2] >> (8 * (i & 3)));
+        for (int i = 0; i < 4; ++i) tw[r][cs / 4 + i] = packed[i];
     }
     __syncthreads();
     if (t == 0) {
+        // The running maximum only grows, so a block whose maximum does not exceed the value it
+        // reads (possibly stale, never larger than the true one) has nothing to add: most blocks
+        // skip the atomic, which would otherwise serialise every block on one address.
         const float bm = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
-        if (bm > 0.0f) atomicMax(c.amax_bits, __float_as_uint(bm));
+        const uint32_t seen = __hip_atomic_load(c.amax_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (bm > 0.0f && __float_as_uint(bm) > seen) atomicMax(c.amax_bits, __float_as_uint(bm));
     }
     if (c.qt) {
-        const int cc = t >> 2, rs = (t & 3) * 16;
-        uint32_t w[4];
+        const int rg = t & 15, cg = t >> 4;
+        uint32_t a[4], b[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            w[i] = static_cast<uint32_t>(tr[cc][rs + 4 * i]) | (static_cast<uint32_t>(tr[cc][rs + 4 * i + 1]) << 8) |
-                   (static_cast<uint32_t>(tr[cc][rs + 4 * i + 2]) << 16) |
-                   (static_cast<uint32_t>(tr[cc][rs + 4 * i + 3]) << 24);
+        for (int j = 0; j < 4; ++j) a[j] = tw[4 * rg + j][cg];
+        transpose4x4(a, b);
         uint8_t* dst = c.qt + static_cast<int64_t>(c.cols) * c.poff[g] +
-                       static_cast<int64_t>(ct * kCastTile + cc) * rpad + rt * kCastTile + rs;
-        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+                       static_cast<int64_t>(ct * kCastTile + 4 * cg) * rpad + rt * kCastTile + 4 * rg;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint32_t*>(dst + static_cast<int64_t>(i) * rpad) = b[i];
     }
 }
 
