@@ -24,11 +24,24 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kMaxShared = 8;
 constexpr int kChunksPerIter = 4;   // 8-element chunks each lane keeps in flight
 
+// Every row is touched once per kernel, so rows move with non-temporal loads and
+// stores (streaming cache policy): they do not evict what other kernels reuse.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 nt_load16(const void* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void nt_store16(void* p, uint4 q) {
+    u32x4_t v;
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(p));
+}
+
 // 8 consecutive elements of type S, held as compute type A.
 template <class S, class A> struct Vec8;
 template <> struct Vec8<bf16, float> {
     __device__ __forceinline__ static void load(const bf16* p, float* v) {
-        const uint4 q = *reinterpret_cast<const uint4*>(p);
+        const uint4 q = nt_load16(p);
         const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -42,7 +55,7 @@ template <> struct Vec8<bf16, float> {
         q.y = pack_bf16x2(v[2], v[3]);
         q.z = pack_bf16x2(v[4], v[5]);
         q.w = pack_bf16x2(v[6], v[7]);
-        *reinterpret_cast<uint4*>(p) = q;
+        nt_store16(p, q);
     }
 };
 template <> struct Vec8<float, float> {
@@ -76,11 +89,11 @@ template <class S> struct Raw8 {
     uint4 w[kWords];
     __device__ __forceinline__ void load(const S* p) {
 #pragma unroll
-        for (int i = 0; i < kWords; ++i) w[i] = reinterpret_cast<const uint4*>(p)[i];
+        for (int i = 0; i < kWords; ++i) w[i] = nt_load16(reinterpret_cast<const uint4*>(p) + i);
     }
     __device__ __forceinline__ void store(S* p) const {
 #pragma unroll
-        for (int i = 0; i < kWords; ++i) reinterpret_cast<uint4*>(p)[i] = w[i];
+        for (int i = 0; i < kWords; ++i) nt_store16(reinterpret_cast<uint4*>(p) + i, w[i]);
     }
 };
 
@@ -197,20 +210,28 @@ __global__ __launch_bounds__(kThreads) void combine_bwd_kernel(const S* __restri
         dot[j] = G(0);
     }
     const int nch = h / 8;
-    for (int c = lane; c < nch; c += 64) {
-        A dv[8];
-        Vec8<S, A>::load(dout + t * h + c * 8, dv);
+    for (int c0 = lane; c0 < nch; c0 += 64 * kChunksPerIter) {
+        A dv[kChunksPerIter][8];
+#pragma unroll
+        for (int u = 0; u < kChunksPerIter; ++u)
+            if (c0 + u * 64 < nch) Vec8<S, A>::load(dout + t * h + (c0 + u * 64) * 8, dv[u]);
         for (int j = 0; j < k; ++j) {
             if (rows[j] < 0) continue;
-            const int64_t off = static_cast<int64_t>(rows[j]) * h + c * 8;
-            A yv[8], o[8];
-            Vec8<S, A>::load(y + off, yv);
+            A yv[kChunksPerIter][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                o[i] = g[j] * dv[i];
-                dot[j] = dot[j] + static_cast<G>(dv[i]) * static_cast<G>(yv[i]);
+            for (int u = 0; u < kChunksPerIter; ++u)
+                if (c0 + u * 64 < nch) Vec8<S, A>::load(y + static_cast<int64_t>(rows[j]) * h + (c0 + u * 64) * 8, yv[u]);
+#pragma unroll
+            for (int u = 0; u < kChunksPerIter; ++u) {
+                if (c0 + u * 64 >= nch) continue;
+                A o[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    o[i] = g[j] * dv[u][i];
+                    dot[j] = dot[j] + static_cast<G>(dv[u][i]) * static_cast<G>(yv[u][i]);
+                }
+                Vec8<S, A>::store(dy + static_cast<int64_t>(rows[j]) * h + (c0 + u * 64) * 8, o);
             }
-            Vec8<S, A>::store(dy + off, o);
         }
     }
     // Lane partials -> one value per slot by a fixed butterfly.
@@ -242,32 +263,49 @@ __global__ __launch_bounds__(kThreads) void token_bwd_kernel(const S* __restrict
         d[j] = dl ? dl[t * k + j] : R(0);
     }
     const int nch = h / 8;
-    for (int c = lane; c < nch; c += 64) {
-        A acc[8];
-        Vec8<S, A>::load(dout + t * h + c * 8, acc);
+    for (int c0 = lane; c0 < nch; c0 += 64 * kChunksPerIter) {
+        A acc[kChunksPerIter][8];
+#pragma unroll
+        for (int u = 0; u < kChunksPerIter; ++u)
+            if (c0 + u * 64 < nch) Vec8<S, A>::load(dout + t * h + (c0 + u * 64) * 8, acc[u]);
         for (int j = 0; j < k; ++j) {
             if (rows[j] < 0) continue;
-            A v[8];
-            Vec8<S, A>::load(dxp + static_cast<int64_t>(rows[j]) * h + c * 8, v);
+            A v[kChunksPerIter][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+            for (int u = 0; u < kChunksPerIter; ++u)
+                if (c0 + u * 64 < nch) Vec8<S, A>::load(dxp + static_cast<int64_t>(rows[j]) * h + (c0 + u * 64) * 8, v[u]);
+#pragma unroll
+            for (int u = 0; u < kChunksPerIter; ++u)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[u][i] = acc[u][i] + v[u][i];
         }
         if (dl) {
             for (int j = 0; j < k; ++j) {
                 if (ex[j] < 0 || ex[j] >= E) continue;   // dropped id: no router row
-                R wv[8];
-                Vec8<R, R>::load(router_w + static_cast<int64_t>(ex[j]) * h + c * 8, wv);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc[i] = acc[i] + static_cast<A>(d[j] * wv[i]);
+                for (int u = 0; u < kChunksPerIter; ++u) {
+                    if (c0 + u * 64 >= nch) continue;
+                    R wv[8];
+                    Vec8<R, R>::load(router_w + static_cast<int64_t>(ex[j]) * h + (c0 + u * 64) * 8, wv);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[u][i] = acc[u][i] + static_cast<A>(d[j] * wv[i]);
+                }
             }
         }
         for (int s = 0; s < n_shared; ++s) {
-            A v[8];
-            Vec8<S, A>::load(static_cast<const S*>(shared.p[s]) + t * h + c * 8, v);
+            A v[kChunksPerIter][8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+            for (int u = 0; u < kChunksPerIter; ++u)
+                if (c0 + u * 64 < nch)
+                    Vec8<S, A>::load(static_cast<const S*>(shared.p[s]) + t * h + (c0 + u * 64) * 8, v[u]);
+#pragma unroll
+            for (int u = 0; u < kChunksPerIter; ++u)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[u][i] = acc[u][i] + v[u][i];
         }
-        Vec8<S, A>::store(dx + t * h + c * 8, acc);
+#pragma unroll
+        for (int u = 0; u < kChunksPerIter; ++u)
+            if (c0 + u * 64 < nch) Vec8<S, A>::store(dx + t * h + (c0 + u * 64) * 8, acc[u]);
     }
 }
 
