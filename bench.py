@@ -161,6 +161,27 @@ def cpu_baseline(name: str, sample_tokens: int, reps: int = 3) -> dict:
                       f"fwd+bwd, median of {reps} after 1 warm-up; torch {torch.__version__}"}
 
 
+def copy_probe(nbytes: int) -> int:
+    """A plain device copy of a known size: profiled with FETCH_SIZE / WRITE_SIZE, it converts those
+    counters into bytes (each copy reads and writes ``nbytes``)."""
+    a = torch.ones(nbytes // 2, dtype=torch.bfloat16, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": nbytes, "copies": 3}), flush=True)
+    return 0
+
+
+def gemm_traffic(workload: str) -> float | None:
+    """HBM bytes per step of the grouped GEMM launches, from profiles/gemm_traffic_<workload>.json
+    (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), when it was measured."""
+    path = ROOT / "profiles" / f"gemm_traffic_{workload}.json"
+    if not path.exists():
+        return None
+    return float(json.loads(path.read_text())["hbm_bytes_per_step"])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -169,7 +190,11 @@ def main() -> int:
     ap.add_argument("--workload", default="mixtral", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-sample", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only copy BYTES bytes on the device three times (calibrates HBM byte counters)")
     args = ap.parse_args()
+    if args.copy_probe:
+        return copy_probe(args.copy_probe)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs the MoE layer on one GPU; multi-GPU expert parallelism "
                                    "(the all-to-all dispatch) is not part of it", "n_gpus": args.gpus}))
@@ -239,7 +264,7 @@ def main() -> int:
                    "tokens": T, "hidden": h, "ffn": f, "experts": E, "top_k": k, "local_experts": w["e1"] - w["e0"],
                    "routed_pairs": P, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": peak, "unit": "TFLOP/s",
-                     "frac": gemm_tflops / peak, "traffic": None,
+                     "frac": gemm_tflops / peak, "traffic": gemm_traffic(args.workload),
                      "kernel": "grouped expert GEMMs (fc1/fc2 fwd, dgrad, wgrad)",
                      "algorithmic": f"18*(P + S*T)*h*f = {gemm_flops:.4g} FLOP per step, P = {P} routed pairs"},
         "rows_roofline": {"bound": "hbm", "achieved": row_gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
