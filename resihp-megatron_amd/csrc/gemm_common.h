@@ -159,11 +159,6 @@ template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI =
 // itself (s_waitcnt vmcnt) before its barriers.  Fragments are double-buffered
 // in registers: the reads of the next k16 block are interleaved with the
 // MFMAs of the current one.
-//
-// FWD runs gg_bf16_k64_kernel (K step 64: each row of a stage is a whole
-// 128-byte line, so L2 sees half the requests); DGRAD and WGRAD run
-// gg_bf16_k32_kernel (K step 32, four stages, loads two steps ahead), which
-// measured faster for the transposed operands.
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
@@ -213,9 +208,10 @@ __device__ __forceinline__ float4 lds_f4(const float* ep, int r, int x) {
     return *reinterpret_cast<const float4*>(ep + r * kEpPitchF + x);
 }
 
-// Rows [r0, r0 + 128) of the tile, staged in ep.  Thread t handles 4-column
-// pieces t, t + 512, ...; a wave covers one row (or two rows of 128 columns).
-template <int MODE, int EPI>
+// Rows [r0, r0 + 128) of the tile, staged in ep.  Thread t of NT handles
+// 4-column pieces t, t + NT, ...; a wave covers one row (or two rows of 128
+// columns).
+template <int MODE, int EPI, int NT>
 __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, const float* ep, int r0) {
     const int g = t.g;
     if (EPI == kEpiSwigluFwd) {
@@ -224,7 +220,7 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
         uint16_t* hpre = static_cast<uint16_t*>(p.c[g]);
         uint16_t* act = static_cast<uint16_t*>(p.c2[g]);
 #pragma unroll 4
-        for (int idx = threadIdx.x; idx < kEpRows * 32; idx += kThreadsMfma) {
+        for (int idx = threadIdx.x; idx < kEpRows * 32; idx += NT) {
             const int r = idx >> 5, a = (idx & 31) * 4;
             const int yr = r0 + r, col = t.x0 + a;
             if (yr >= t.y_lim || col >= p.N) continue;
@@ -240,7 +236,7 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
     }
     uint16_t* out = static_cast<uint16_t*>(p.c[g]);
 #pragma unroll 4
-    for (int idx = threadIdx.x; idx < kEpRows * 64; idx += kThreadsMfma) {
+    for (int idx = threadIdx.x; idx < kEpRows * 64; idx += NT) {
         const int r = idx >> 6, x = (idx & 63) * 4;
         const int yr = r0 + r;
         if (yr >= t.y_lim || x >= t.x_lim) continue;
@@ -284,23 +280,25 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
 // Epilogue, in two halves of 128 Y rows.  The waves owning a half write
 // their fp32 accumulators to LDS ([128 rows][256 X] at kEpPitchF floats per
 // row); then every thread takes 4-column pieces, so each wave instruction
-// reads or writes whole contiguous row segments in HBM.  For MFMA tile (i, j)
-// a lane holds Y row wy * kWaveY + 32 j + (lane & 31) and X columns
-// wx * 128 + 32 i + 8 q + 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller
-// guarantees that no wave still reads or writes the LDS buffer.
-template <int MODE, int EPI>
-__device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][kFragY],
+// reads or writes whole contiguous row segments in HBM.  A wave owns WY Y rows
+// (NT threads in the workgroup); for MFMA tile (i, j) a lane holds Y row
+// wy * WY + 32 j + (lane & 31) and X columns wx * 128 + 32 i + 8 q +
+// 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller guarantees that no wave
+// still reads or writes the LDS buffer.
+template <int MODE, int EPI, int NT = kThreadsMfma, int WY = kWaveY>
+__device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][WY / 32],
                                          int wx, int wy, int lane, float mul = 1.0f) {
+    static_assert(WY <= kEpRows && kEpRows % WY == 0, "a wave's rows lie in one half");
     float* ep = reinterpret_cast<float*>(lds);
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
         __syncthreads();
-        if ((wy * kWaveY) / kEpRows == half) {
+        if ((wy * WY) / kEpRows == half) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < kFragY; ++j) {
-                    const int y = wy * kWaveY + j * 32 + (lane & 31) - half * kEpRows;
+                for (int j = 0; j < WY / 32; ++j) {
+                    const int y = wy * WY + j * 32 + (lane & 31) - half * kEpRows;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int x = wx * 128 + i * 32 + q * 8 + 4 * (lane >> 5);
@@ -314,7 +312,7 @@ __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t
                 }
         }
         __syncthreads();
-        epilogue_half<MODE, EPI>(p, t, ep, half * kEpRows);
+        epilogue_half<MODE, EPI, NT>(p, t, ep, half * kEpRows);
     }
 }
 

@@ -22,273 +22,41 @@
 // Work unit: a 256 x 256 output tile.  Tiles are ordered group-major, then by
 // output column block, then by row block, and block ids are remapped so each
 // XCD runs a contiguous range of that order.
+#include <type_traits>
+
 #include "gemm_common.h"
 
 namespace rhp {
 namespace {
 
-// ------------------------------------------------------------------ K step 32, four stages
+// ------------------------------------------------------------------ operand tiles and their loads
 //
-// K-major tile [256 rows][32 k], 64-byte rows, chunk c of row r at position
-// c ^ ((r >> 2) & 3).  MN-major tile [32 k][256 mn].
-//
-// Pipeline (S = 4 stages): the loads of step kt + S - 1 are issued during step
-// kt, after the barrier that opens it.  That barrier also guarantees that the
-// stages of steps kt and kt + 1 are complete, so the fragments of step kt + 1's
-// first k16 block are read during step kt's second block and no wave waits on
-// LDS after a barrier.  Stage (kt - 1) mod S, which the new loads overwrite,
-// was last read before that barrier.
-
-constexpr int kDmaK = 32;
-constexpr int kDmaStages = 4;
-constexpr int kDmaTileBytes = kTile * kDmaK * 2;          // 16 KB per operand
-constexpr int kDmaStageBytes = 2 * kDmaTileBytes;         // X + Y
-constexpr int kDmaPerWave = kDmaTileBytes / 1024 / kWaves;   // loads per wave per operand per step
-constexpr int kDmaPerStep = 2 * kDmaPerWave;              // loads per wave per step
-constexpr int kDmaLdsBytes = kDmaStages * kDmaStageBytes > kEpBytes ? kDmaStages * kDmaStageBytes : kEpBytes;
-static_assert(kDmaLdsBytes <= 163840, "LDS per workgroup");
-static_assert(kDmaPerWave == 2, "one load pair per k16 block");
-
-// Wait until at most n steps' worth of this wave's loads are still in flight.
-__device__ __forceinline__ void wait_dma_steps(int n) {
-    static_assert(2 * kDmaPerStep < 64, "vmcnt field");
-    if (n >= 2) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * kDmaPerStep) & 15) | (((2 * kDmaPerStep) >> 4) << 14));
-    } else if (n == 1) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (kDmaPerStep & 15) | ((kDmaPerStep >> 4) << 14));
-    } else {
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-    }
-}
-
-__device__ __forceinline__ int dkmaj_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
-
-// Per-lane offsets of one operand.  vo[j]: global byte offset (at k = 0) of
-// this lane's chunk in load j of this wave; fr[i][b]: LDS offset of fragment
-// i at k16 block b of a stage (MN-major: block 1 adds a constant).
-struct DmaMap {
-    uint32_t vo[kDmaPerWave];
-    uint32_t fr[4][2];
-};
-
-template <class RowOf>
-__device__ __forceinline__ void dmap_kmaj(DmaMap& m, uint32_t ld, int frag_row0, int nfrag, RowOf src_row) {
-    const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) {
-        const int row = (j * kWaves + w) * 16 + (L >> 2);
-        const int chunk = (L & 3) ^ ((row >> 2) & 3);
-        m.vo[j] = (static_cast<uint32_t>(src_row(row)) * ld + chunk * 8) * 2u;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-            m.fr[i][b] = i < nfrag ? dkmaj_off(frag_row0 + i * 32 + (L & 31), 2 * b + (L >> 5)) : 0;
-}
-
-__device__ __forceinline__ void dmap_mnmaj(DmaMap& m, uint32_t ld, int mn0, int mn_lim, int frag_row0, int nfrag) {
-    const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int j = 0; j < kDmaPerWave; ++j) {
-        const int k = (j * kWaves + w) * 2 + (L >> 5);
-        const int chunk = (L & 31) ^ ((k & 3) << 2);
-        m.vo[j] = chunk * 8 < mn_lim ? (static_cast<uint32_t>(k) * ld + static_cast<uint32_t>(mn0 + chunk * 8)) * 2u
-                                     : kOutOfRange;
-    }
-    const int g = L >> 4, r = L & 15;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        m.fr[i][0] = i < nfrag ? mnmaj_off(8 * (g >> 1) + (r >> 2), frag_row0 + i * 32 + 16 * (g & 1) + 4 * (r & 3)) : 0;
-        m.fr[i][1] = m.fr[i][0] + 16 * 512;
-    }
-}
-
-template <int MODE, int EPI>
-__global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k32_kernel(Params p) {
-    __shared__ __align__(1024) uint8_t lds[kDmaLdsBytes];
-    Tile t;
-    if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
-    t.g = __builtin_amdgcn_readfirstlane(t.g);
-    t.x0 = __builtin_amdgcn_readfirstlane(t.x0);
-    t.x_lim = __builtin_amdgcn_readfirstlane(t.x_lim);
-    t.y0 = __builtin_amdgcn_readfirstlane(t.y0);
-    t.y_lim = __builtin_amdgcn_readfirstlane(t.y_lim);
-    t.row0 = __builtin_amdgcn_readfirstlane(static_cast<int>(t.row0));
-    t.k_begin = __builtin_amdgcn_readfirstlane(t.k_begin);
-    t.k_end = __builtin_amdgcn_readfirstlane(t.k_end);
-    const int g = t.g;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wx = wave & 1, wy = wave >> 1;
-    constexpr bool kXK = MODE == kFwd;
-    constexpr bool kYK = MODE != kWgrad;
-
-    const uint16_t* A = static_cast<const uint16_t*>(p.a[g]);
-    const uint16_t* B = static_cast<const uint16_t*>(p.b[g]);
-    const uint32_t ldb = static_cast<uint32_t>(p.ldb), lda = static_cast<uint32_t>(p.lda);
-    Rsrc rx, ry;
-    DmaMap mx, my;
-    if (MODE == kWgrad) {
-        const int64_t rows = t.k_end;   // group rows; reads past them return zero
-        rx = make_dma_rsrc(B + t.row0 * p.ldb, rows * p.ldb * 2);
-        ry = make_dma_rsrc(A + t.row0 * p.lda, rows * p.lda * 2);
-        dmap_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
-        dmap_mnmaj(my, lda, t.y0, t.y_lim, wy * kWaveY, kFragY);
-    } else {
-        ry = make_dma_rsrc(A + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda * 2);
-        const int y_last = t.y_lim - 1;
-        dmap_kmaj(my, lda, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
-        if (MODE == kFwd) {
-            rx = make_dma_rsrc(B, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb * 2);
-            dmap_kmaj(mx, ldb, wx * 128, 4, [&](int r) {
-                if (EPI == kEpiSwigluFwd) {
-                    // 256 weight rows = [gate 64 | up 64] for each half of 128 activation columns.
-                    const int half = r >> 7, qq = r & 127;
-                    int col = t.x0 + half * 64 + (qq & 63);
-                    col = col < p.f ? col : 0;
-                    return qq < 64 ? col : p.f + col;
-                }
-                const int n = t.x0 + r;
-                return n < p.N ? n : 0;
-            });
-        } else {
-            rx = make_dma_rsrc(B, static_cast<int64_t>(p.K) * p.ldb * 2);
-            dmap_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
-        }
-    }
-
-    const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-    // Load j of both operands of one step.
-    auto issue_part = [&](int step, int stage, int j) {
-        const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kDmaK);
-        const uint32_t at = lds0 + stage * kDmaStageBytes + wave * 1024 + j * kWaves * 1024;
-        if (kXK) dma16(rx, mx.vo[j], k0 * 2u, at);
-        else dma16(rx, mx.vo[j] + k0 * ldb * 2u, 0, at);
-        if (kYK) dma16(ry, my.vo[j], k0 * 2u, at + kDmaTileBytes);
-        else dma16(ry, my.vo[j] + k0 * lda * 2u, 0, at + kDmaTileBytes);
-    };
-    auto issue = [&](int step, int stage) {
-        issue_part(step, stage, 0);
-        issue_part(step, stage, 1);
-    };
-
-    f32x16_t acc[4][kFragY];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < kFragY; ++j) acc[i][j] = f32x16_t{};
-
-    typedef bf16x8_t FragSet[4 + kFragY];
-    auto read_frags = [&](FragSet& f, int stage, int b) {
-        const uint8_t* xt = lds + stage * kDmaStageBytes;
-        const uint8_t* yt = xt + kDmaTileBytes;
-#pragma unroll
-        for (int j = 0; j < kFragY; ++j)
-            f[4 + j] = kYK ? *reinterpret_cast<const bf16x8_t*>(yt + my.fr[j][b]) : frag_mnmaj(yt, my.fr[j][b], 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            f[i] = kXK ? *reinterpret_cast<const bf16x8_t*>(xt + mx.fr[i][b]) : frag_mnmaj(xt, mx.fr[i][b], 0);
-    };
-    auto mfmas = [&](const FragSet& f) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < kFragY; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[4 + j], acc[i][j], 0, 0, 0);
-    };
-    constexpr int kReads = (kXK ? 4 : 8) + (kYK ? kFragY : 2 * kFragY);
-    // All waves see every LDS write of the stages the wait covered; LDS
-    // accesses do not move across it.
-    auto barrier = [] {
-        __builtin_amdgcn_sched_barrier(0);   // this step's MFMAs (and their LDS waits) stay before it
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-    };
-
-    const int nk = (t.k_end - t.k_begin + kDmaK - 1) / kDmaK;
-    // A wave whose Y rows all lie past the tile's valid rows (the partial last
-    // tile of a group) only loads its share and joins the barriers; its SIMD
-    // then runs the other wave's MFMAs alone.
-    const bool idle = wy * kWaveY >= t.y_lim;
-    FragSet fa, fb;
-    if (nk > 0) {
-#pragma unroll
-        for (int s = 0; s < kDmaStages - 1; ++s)
-            if (s < nk) issue(s, s);
-        wait_dma_steps(min(kDmaStages - 2, nk - 1) - min(1, nk - 1));
-        barrier();
-        if (!idle) read_frags(fa, 0, 0);
-    }
-    int stage = 0, next = 1 % kDmaStages, fill = kDmaStages - 1;   // stages of steps kt, kt + 1, kt + S - 1
-    if (idle) {
-        for (int kt = 0; kt < nk; ++kt) {
-            if (kt + kDmaStages - 1 < nk) issue(kt + kDmaStages - 1, fill);
-            wait_dma_steps(min(kt + kDmaStages - 1, nk - 1) - min(kt + 2, nk - 1));
-            barrier();
-            fill = fill + 1 == kDmaStages ? 0 : fill + 1;
-        }
-    }
-    // The body is the same for every step (the last one reads a stale block
-    // it does not use), so the accumulators never need copies between paths.
-    for (int kt = 0; kt < (idle ? 0 : nk); ++kt) {
-        // The step's loads are spread over its two k16 blocks, so the memory
-        // pipeline never holds a wave's whole burst in front of its MFMAs.
-        const bool more_dma = kt + kDmaStages - 1 < nk;
-        if (more_dma) issue_part(kt + kDmaStages - 1, fill, 0);
-        read_frags(fb, stage, 1);
-        mfmas(fa);
-        interleave_reads<0, 4 * kFragY, kReads>();
-        __builtin_amdgcn_sched_barrier(0);
-        if (more_dma) issue_part(kt + kDmaStages - 1, fill, 1);
-        read_frags(fa, next, 0);
-        mfmas(fb);
-        interleave_reads<0, 4 * kFragY, kReads>();
-        // Steps up to min(kt + S - 1, nk - 1) are issued; step kt + 2 must be complete.
-        wait_dma_steps(min(kt + kDmaStages - 1, nk - 1) - min(kt + 2, nk - 1));
-        barrier();
-        stage = next;
-        next = next + 1 == kDmaStages ? 0 : next + 1;
-        fill = fill + 1 == kDmaStages ? 0 : fill + 1;
-    }
-    // Every load was waited for (the last barrier's wait covered all of them,
-    // or there was one step only and the prologue waited), and every wave has
-    // consumed its LDS reads, so the stage memory can hold the epilogue.
-    epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane);
-}
-
-// ------------------------------------------------------------------ K step 64, two stages
-//
-// K-major tile [256 rows][64 k], 128-byte rows, chunk c of row r at position
-// c ^ ((r >> 1) & 7): the 16 rows of one ds_read_b128 hit 16 distinct bank
-// slots, and a lane's offset for k16 block b is its block-0 offset XOR 32 b.
-// MN-major tile [64 k][256 mn].
-//
-// Pipeline: the loads of step kt + 1 are issued right after the barrier that
-// opens step kt and waited for before the barrier that closes it.  That
-// barrier comes before the MFMAs of the last k16 block, so those MFMAs cover
-// the LDS latency of the next stage's first block.
+// An operand tile is 256 rows (or mn columns) by 64 k, 32 KB:
+//   K-major [256 rows][64 k]: 128-byte rows, chunk c of row r at position
+//     c ^ ((r >> 1) & 7), so the 16 rows of one ds_read_b128 hit 16 distinct
+//     bank slots, and a lane's offset for k16 block b is its block-0 offset
+//     XOR 32 b.
+//   MN-major [64 k][256 mn]: 512-byte k rows, chunk c at c ^ 4 (k & 3).
+// One load moves 1 KB: 8 K-major rows or 2 MN-major k rows.
 
 constexpr int kK64 = 64;
-constexpr int kT64Bytes = kTile * kK64 * 2;                // 32 KB per operand
-constexpr int kS64Bytes = 2 * kT64Bytes;                   // X + Y
-constexpr int kD64PerWave = kT64Bytes / 1024 / kWaves;     // loads per wave per operand per step
-constexpr int kLds64Bytes = 2 * kS64Bytes > kEpBytes ? 2 * kS64Bytes : kEpBytes;
-static_assert(kLds64Bytes <= 163840, "two 64 KB stages");
+constexpr int kT64Bytes = kTile * kK64 * 2;                // 32 KB per operand tile
+constexpr int kD64PerWave = kT64Bytes / 1024 / kWaves;     // loads per wave per operand tile
 static_assert((kT64Bytes / 1024) % kWaves == 0, "whole loads per wave");
 
-
+template <int NW = kWaves>
 struct Dma64Map {
-    uint32_t vo[kD64PerWave];
+    uint32_t vo[kT64Bytes / 1024 / NW];
     uint32_t fr[4];   // K-major: block-0 offset (block b: XOR 32 b); MN-major: block-0 offset (block b: + 8192 b)
 };
 
-template <class RowOf>
-__device__ __forceinline__ void d64_kmaj(Dma64Map& m, uint32_t ld, int frag_row0, int nfrag, RowOf src_row) {
+// Load j of wave w fills 1 KB block j * NW + w of an operand's stage.
+template <int NW, class RowOf>
+__device__ __forceinline__ void d64_kmaj(Dma64Map<NW>& m, uint32_t ld, int frag_row0, int nfrag, RowOf src_row) {
     const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < kD64PerWave; ++j) {
-        const int row = (j * kWaves + w) * 8 + (L >> 3);
+    for (int j = 0; j < kT64Bytes / 1024 / NW; ++j) {
+        const int row = (j * NW + w) * 8 + (L >> 3);
         const int chunk = (L & 7) ^ ((row >> 1) & 7);
         m.vo[j] = (static_cast<uint32_t>(src_row(row)) * ld + chunk * 8) * 2u;
     }
@@ -296,11 +64,12 @@ __device__ __forceinline__ void d64_kmaj(Dma64Map& m, uint32_t ld, int frag_row0
     for (int i = 0; i < 4; ++i) m.fr[i] = i < nfrag ? k64_off(frag_row0 + i * 32 + (L & 31), L >> 5) : 0;
 }
 
-__device__ __forceinline__ void d64_mnmaj(Dma64Map& m, uint32_t ld, int mn0, int mn_lim, int frag_row0, int nfrag) {
+template <int NW>
+__device__ __forceinline__ void d64_mnmaj(Dma64Map<NW>& m, uint32_t ld, int mn0, int mn_lim, int frag_row0, int nfrag) {
     const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < kD64PerWave; ++j) {
-        const int k = (j * kWaves + w) * 2 + (L >> 5);
+    for (int j = 0; j < kT64Bytes / 1024 / NW; ++j) {
+        const int k = (j * NW + w) * 2 + (L >> 5);
         const int chunk = (L & 31) ^ ((k & 3) << 2);
         m.vo[j] = chunk * 8 < mn_lim ? (static_cast<uint32_t>(k) * ld + static_cast<uint32_t>(mn0 + chunk * 8)) * 2u
                                      : kOutOfRange;
@@ -311,9 +80,31 @@ __device__ __forceinline__ void d64_mnmaj(Dma64Map& m, uint32_t ld, int mn0, int
         m.fr[i] = i < nfrag ? mnmaj_off(8 * (g >> 1) + (r >> 2), frag_row0 + i * 32 + 16 * (g & 1) + 4 * (r & 3)) : 0;
 }
 
+// ------------------------------------------------------------------ the MFMA kernel: a ring of five operand slots
+//
+// LDS holds five operand tiles ("slots", 160 KB), filled in the order X0 Y0
+// X1 Y1 X2 Y2 ..., operand tile q (X of step q / 2 for even q, Y for odd q)
+// in slot q mod 5.  Each K step of 64 runs four k16 blocks; the fragments of
+// block b + 1 are read while the MFMAs of block b run.  The barrier that
+// closes step kt comes after the reads of its last block and needs steps up
+// to kt + 1 complete, so X of step kt + 2 stays in flight across it; right
+// after it the two slots of step kt are refilled with Y of step kt + 2 and X
+// of step kt + 3, and the MFMAs of the last block cover the LDS latency of the
+// next step's first fragments.  Loads are thus never drained to zero at a
+// barrier: with the latency of L2 and HBM under load near a microsecond, the
+// bytes in flight per CU set the rate at which tiles arrive.  Tiles past the
+// last step are loaded from an offset past the buffer view (they read zeros
+// without touching memory), so every step issues and waits for the same
+// counts.
+
+constexpr int kSlots = 5;
+constexpr int kLdsSlotsBytes = kSlots * kT64Bytes > kEpBytes ? kSlots * kT64Bytes : kEpBytes;
+static_assert(kLdsSlotsBytes <= 163840, "five 32 KB slots");
+constexpr uint32_t kPastView = 0x7ffffff0u;   // soffset that puts every lane past its buffer view
+
 template <int MODE, int EPI>
-__global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k64_kernel(Params p) {
-    __shared__ __align__(1024) uint8_t lds[kLds64Bytes];
+__global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
+    __shared__ __align__(1024) uint8_t lds[kLdsSlotsBytes];
     Tile t;
     if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
     t.g = __builtin_amdgcn_readfirstlane(t.g);
@@ -334,7 +125,7 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k64_kernel(Params p) {
     const uint16_t* B = static_cast<const uint16_t*>(p.b[g]);
     const uint32_t ldb = static_cast<uint32_t>(p.ldb), lda = static_cast<uint32_t>(p.lda);
     Rsrc rx, ry;
-    Dma64Map mx, my;
+    Dma64Map<> mx, my;
     if (MODE == kWgrad) {
         const int64_t rows = t.k_end;   // group rows; reads past them return zero
         rx = make_dma_rsrc(B + t.row0 * p.ldb, rows * p.ldb * 2);
@@ -363,19 +154,42 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k64_kernel(Params p) {
             d64_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
         }
     }
+    const int nk = (t.k_end - t.k_begin + kK64 - 1) / kK64;
 
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-    auto issue = [&](int step, int stage) {
+    // X (Y) tile of step `step` into slot `slot`; past the last step, zeros.
+    auto issue_x = [&](int step, int slot) {
         const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kK64);
-        const uint32_t base = lds0 + stage * kS64Bytes + wave * 1024;
+        const bool live = step < nk;
+        const uint32_t base = lds0 + slot * kT64Bytes + wave * 1024;
 #pragma unroll
         for (int j = 0; j < kD64PerWave; ++j) {
             const uint32_t at = base + j * kWaves * 1024;
-            if (kXK) dma16(rx, mx.vo[j], k0 * 2u, at);
-            else dma16(rx, mx.vo[j] + k0 * ldb * 2u, 0, at);
-            if (kYK) dma16(ry, my.vo[j], k0 * 2u, at + kT64Bytes);
-            else dma16(ry, my.vo[j] + k0 * lda * 2u, 0, at + kT64Bytes);
+            if (kXK) dma16(rx, mx.vo[j], live ? k0 * 2u : kPastView, at);
+            else dma16(rx, mx.vo[j] + (live ? k0 * ldb * 2u : 0u), live ? 0u : kPastView, at);
         }
+    };
+    auto issue_y = [&](int step, int slot) {
+        const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kK64);
+        const bool live = step < nk;
+        const uint32_t base = lds0 + slot * kT64Bytes + wave * 1024;
+#pragma unroll
+        for (int j = 0; j < kD64PerWave; ++j) {
+            const uint32_t at = base + j * kWaves * 1024;
+            if (kYK) dma16(ry, my.vo[j], live ? k0 * 2u : kPastView, at);
+            else dma16(ry, my.vo[j] + (live ? k0 * lda * 2u : 0u), live ? 0u : kPastView, at);
+        }
+    };
+    // vmcnt(n loads of this wave) lgkmcnt(0).
+    auto wait_lds = [](auto n_c) {
+        constexpr int n = decltype(n_c)::value;
+        __builtin_amdgcn_s_waitcnt(0x0070 | (n & 15) | ((n >> 4) << 14));
+    };
+    auto barrier = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     };
 
     f32x16_t acc[4][kFragY];
@@ -388,9 +202,11 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k64_kernel(Params p) {
     auto kfrag = [](const uint8_t* tile, uint32_t fr, int b) {
         return *reinterpret_cast<const bf16x8_t*>(tile + (fr ^ static_cast<uint32_t>(b << 5)));
     };
-    auto read_frags = [&](FragSet& f, int stage, int b) {
-        const uint8_t* xt = lds + stage * kS64Bytes;
-        const uint8_t* yt = xt + kT64Bytes;
+    // sx, sy: byte offsets of the slots, wave-uniform values the compiler
+    // cannot fold into per-slot address registers.
+    auto read_frags = [&](FragSet& f, uint32_t sx, uint32_t sy, int b) {
+        const uint8_t* xt = lds + sx;
+        const uint8_t* yt = lds + sy;
 #pragma unroll
         for (int j = 0; j < kFragY; ++j)
             f[4 + j] = kYK ? kfrag(yt, my.fr[j], b) : frag_mnmaj(yt, my.fr[j], b);
@@ -405,50 +221,63 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_k64_kernel(Params p) {
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[4 + j], acc[i][j], 0, 0, 0);
     };
     constexpr int kReads = (kXK ? 4 : 8) + (kYK ? kFragY : 2 * kFragY);
+    using Pending = std::integral_constant<int, kD64PerWave>;   // one operand tile stays in flight
+    using Prolog = std::integral_constant<int, 3 * kD64PerWave>;
 
-    const int nk = (t.k_end - t.k_begin + kK64 - 1) / kK64;
     // A wave whose Y rows all lie past the tile's valid rows only loads its
     // share and joins the barriers.
     const bool idle = wy * kWaveY >= t.y_lim;
     FragSet fa, fb;
     if (nk > 0) {
-        issue(0, 0);
-        wait_loads_all();
-        __syncthreads();
-        if (!idle) read_frags(fa, 0, 0);
-    }
-    if (idle) {
-        for (int kt = 0; kt < nk; ++kt) {
-            if (kt + 1 < nk) issue(kt + 1, (kt & 1) ^ 1);
-            wait_loads_all();
-            __syncthreads();
+        issue_x(0, 0);
+        issue_y(0, 1);
+        issue_x(1, 2);
+        issue_y(1, 3);
+        issue_x(2, 4);
+        wait_lds(Prolog{});   // step 0 complete
+        barrier();
+        if (idle) {
+            for (int kt = 0; kt < nk; ++kt) {
+                wait_lds(Pending{});
+                barrier();
+                const int sx = (2 * kt) % kSlots, sy = (2 * kt + 1) % kSlots;
+                issue_y(kt + 2, sx);
+                issue_x(kt + 3, sy);
+            }
+        } else {
+            read_frags(fa, 0, kT64Bytes, 0);
+            // Slots of X and Y of step kt (sx, sy) and of step kt + 1 (nx, ny).
+            int sx = 0, sy = 1, nx = 2, ny = 3;
+            for (int kt = 0; kt < nk; ++kt) {
+                const uint32_t ox = sx * kT64Bytes, oy = sy * kT64Bytes;
+                read_frags(fb, ox, oy, 1);
+                mfmas(fa);
+                interleave_reads<0, 4 * kFragY, kReads>();
+                read_frags(fa, ox, oy, 2);
+                mfmas(fb);
+                interleave_reads<0, 4 * kFragY, kReads>();
+                read_frags(fb, ox, oy, 3);
+                mfmas(fa);
+                interleave_reads<0, 4 * kFragY, kReads>();
+                // Steps up to kt + 1 complete, every read of slots sx and sy done.
+                wait_lds(Pending{});
+                barrier();
+                issue_y(kt + 2, sx);
+                issue_x(kt + 3, sy);
+                read_frags(fa, nx * kT64Bytes, ny * kT64Bytes, 0);
+                mfmas(fb);
+                interleave_reads<0, 4 * kFragY, kReads>();
+                sx = nx;
+                sy = ny;
+                nx = ny + 1 == kSlots ? 0 : ny + 1;
+                ny = nx + 1 == kSlots ? 0 : nx + 1;
+            }
         }
-    }
-    // Same body for every step (the last one reads a stale block it does not
-    // use), so the accumulators never need copies between paths.
-    for (int kt = 0; kt < (idle ? 0 : nk); ++kt) {
-        const int st = kt & 1;
-        if (kt + 1 < nk) issue(kt + 1, st ^ 1);
-        read_frags(fb, st, 1);
-        mfmas(fa);
-        interleave_reads<0, 4 * kFragY, kReads>();
-        read_frags(fa, st, 2);
-        mfmas(fb);
-        interleave_reads<0, 4 * kFragY, kReads>();
-        read_frags(fb, st, 3);
-        mfmas(fa);
-        interleave_reads<0, 4 * kFragY, kReads>();
-        // The loads of step kt + 1 have landed in every wave's share and no wave
-        // still reads stage st (its block-3 reads complete before the barrier).
-        wait_loads_all();
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-        read_frags(fa, st ^ 1, 0);
-        mfmas(fb);
-        interleave_reads<0, 4 * kFragY, kReads>();
+        wait_loads_all();   // the tiles past the last step
     }
     epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane);
 }
+
 // ------------------------------------------------------------------ generic kernel (any dtype)
 
 // One thread per 4 outputs of a 32 x 32 tile, reading operands straight from
@@ -547,10 +376,7 @@ void launch_one(const Job& j, const Params& p, hipStream_t s) {
     if (j.mfma) {
         const unsigned nb = mfma_blocks<MODE, EPI>(p, j.rows_cap);
         if (!nb) return;
-        if constexpr (MODE == kFwd)
-            hipLaunchKernelGGL((gg_bf16_k64_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
-        else
-            hipLaunchKernelGGL((gg_bf16_k32_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+        hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
         return;
     }
     const unsigned nb = simt_blocks<MODE>(p, j.rows_cap);
