@@ -208,11 +208,56 @@ __device__ __forceinline__ float4 lds_f4(const float* ep, int r, int x) {
     return *reinterpret_cast<const float4*>(ep + r * kEpPitchF + x);
 }
 
+// Barrier for the epilogue's LDS staging: this wave's LDS accesses are
+// complete, global stores may still be in flight (a full __syncthreads would
+// wait for them too).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// The pre-activation values a backward epilogue needs (GELU: hpre, SwiGLU:
+// gate and up), loaded for one half before its accumulators are staged.
+template <int EPI, int NT>
+struct AuxHalf {
+    static constexpr int kPieces = kEpRows * 64 / NT;     // 4-column pieces per thread
+    static constexpr int kParts = EPI == kEpiSwigluBwd ? 2 : EPI == kEpiGeluBwd ? 1 : 0;
+    uint2 v[kParts ? kPieces : 1][kParts ? kParts : 1];
+};
+
+template <int MODE, int EPI, int NT>
+__device__ __forceinline__ void load_aux_half(const Params& p, const Tile& t, int r0, AuxHalf<EPI, NT>& aux) {
+    if constexpr (AuxHalf<EPI, NT>::kParts > 0) {
+        const uint16_t* hp = static_cast<const uint16_t*>(p.aux[t.g]);
+#pragma unroll
+        for (int n = 0; n < AuxHalf<EPI, NT>::kPieces; ++n) {
+            const int idx = threadIdx.x + n * NT;
+            const int r = idx >> 6, x = (idx & 63) * 4;
+            const int yr = r0 + r;
+            if (yr >= t.y_lim || x >= t.x_lim) continue;
+            const int64_t row = t.row0 + t.y0 + yr;
+            const uint16_t* src = hp + row * p.ldaux + t.x0 + x;
+            aux.v[n][0] = *reinterpret_cast<const uint2*>(src);
+            if (EPI == kEpiSwigluBwd) aux.v[n][1] = *reinterpret_cast<const uint2*>(src + p.f);
+        }
+    }
+}
+
+__device__ __forceinline__ void unpack_bf16x4(uint2 v, float* o) {
+    o[0] = __uint_as_float(v.x << 16);
+    o[1] = __uint_as_float(v.x & 0xffff0000u);
+    o[2] = __uint_as_float(v.y << 16);
+    o[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+
 // Rows [r0, r0 + 128) of the tile, staged in ep.  Thread t of NT handles
 // 4-column pieces t, t + NT, ...; a wave covers one row (or two rows of 128
 // columns).
 template <int MODE, int EPI, int NT>
-__device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, const float* ep, int r0) {
+__device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, const float* ep, int r0,
+                                              const AuxHalf<EPI, NT>& aux) {
     const int g = t.g;
     if (EPI == kEpiSwigluFwd) {
         // X columns of the tile are [gate 64 | up 64] for each half of 128
@@ -235,8 +280,9 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
         return;
     }
     uint16_t* out = static_cast<uint16_t*>(p.c[g]);
-#pragma unroll 4
-    for (int idx = threadIdx.x; idx < kEpRows * 64; idx += NT) {
+#pragma unroll
+    for (int n = 0; n < kEpRows * 64 / NT; ++n) {
+        const int idx = threadIdx.x + n * NT;
         const int r = idx >> 6, x = (idx & 63) * 4;
         const int yr = r0 + r;
         if (yr >= t.y_lim || x >= t.x_lim) continue;
@@ -254,16 +300,14 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
             store_bf16x4(out + row * p.ldc + col, v.x, v.y, v.z, v.w);
             store_bf16x4(act + row * p.ldc2 + col, gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w));
         } else if (EPI == kEpiGeluBwd) {
-            const uint16_t* hp = static_cast<const uint16_t*>(p.aux[g]);
             float hv[4];
-            load_bf16x4(hp + row * p.ldaux + col, hv);
+            unpack_bf16x4(aux.v[n][0], hv);
             store_bf16x4(out + row * p.ldc + col, v.x * dgelu_f(hv[0]), v.y * dgelu_f(hv[1]), v.z * dgelu_f(hv[2]),
                          v.w * dgelu_f(hv[3]));
         } else if (EPI == kEpiSwigluBwd) {
-            const uint16_t* hp = static_cast<const uint16_t*>(p.aux[g]);
             float gv[4], uv[4];
-            load_bf16x4(hp + row * p.ldaux + col, gv);
-            load_bf16x4(hp + row * p.ldaux + p.f + col, uv);
+            unpack_bf16x4(aux.v[n][0], gv);
+            unpack_bf16x4(aux.v[n][EPI == kEpiSwigluBwd ? 1 : 0], uv);
             const float dv[4] = {v.x, v.y, v.z, v.w};
             float dg[4], du[4];
 #pragma unroll
@@ -277,14 +321,17 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
     }
 }
 
-// Epilogue, in two halves of 128 Y rows.  The waves owning a half write
-// their fp32 accumulators to LDS ([128 rows][256 X] at kEpPitchF floats per
-// row); then every thread takes 4-column pieces, so each wave instruction
-// reads or writes whole contiguous row segments in HBM.  A wave owns WY Y rows
+// Epilogue, in two halves of 128 Y rows.  The pre-activation values a
+// backward epilogue reads are loaded first, so their latency overlaps the
+// staging; then the waves owning the half write their fp32 accumulators to
+// LDS ([128 rows][256 X] at kEpPitchF floats per row), and every thread takes
+// 4-column pieces, so each wave instruction reads or writes whole contiguous
+// row segments in HBM.  Barriers here wait only for LDS accesses: the global
+// stores of one half drain while the next is staged.  A wave owns WY Y rows
 // (NT threads in the workgroup); for MFMA tile (i, j) a lane holds Y row
 // wy * WY + 32 j + (lane & 31) and X columns wx * 128 + 32 i + 8 q +
-// 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller guarantees that no wave
-// still reads or writes the LDS buffer.
+// 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller guarantees that every
+// load into the LDS buffer has completed.
 template <int MODE, int EPI, int NT = kThreadsMfma, int WY = kWaveY>
 __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][WY / 32],
                                          int wx, int wy, int lane, float mul = 1.0f) {
@@ -292,7 +339,9 @@ __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t
     float* ep = reinterpret_cast<float*>(lds);
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
-        __syncthreads();
+        AuxHalf<EPI, NT> aux;
+        load_aux_half<MODE, EPI, NT>(p, t, half * kEpRows, aux);
+        lds_barrier();
         if ((wy * WY) / kEpRows == half) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -311,8 +360,8 @@ __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t
                     }
                 }
         }
-        __syncthreads();
-        epilogue_half<MODE, EPI, NT>(p, t, ep, half * kEpRows);
+        lds_barrier();
+        epilogue_half<MODE, EPI, NT>(p, t, ep, half * kEpRows, aux);
     }
 }
 

@@ -102,8 +102,11 @@ constexpr int kLdsSlotsBytes = kSlots * kT64Bytes > kEpBytes ? kSlots * kT64Byte
 static_assert(kLdsSlotsBytes <= 163840, "five 32 KB slots");
 constexpr uint32_t kPastView = 0x7ffffff0u;   // soffset that puts every lane past its buffer view
 
-template <int MODE, int EPI>
-__global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
+template <int MODE, int EPI, int NW>
+__global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
+    // NW waves: wave w owns X rows [128 (w % 2), +128) and Y rows [WY (w / 2), +WY).
+    constexpr int WY = kTile / (NW / 2), FY = WY / 32;
+    constexpr int kPerWave = kT64Bytes / 1024 / NW;   // loads per wave per operand tile
     __shared__ __align__(1024) uint8_t lds[kLdsSlotsBytes];
     Tile t;
     if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
@@ -125,17 +128,17 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
     const uint16_t* B = static_cast<const uint16_t*>(p.b[g]);
     const uint32_t ldb = static_cast<uint32_t>(p.ldb), lda = static_cast<uint32_t>(p.lda);
     Rsrc rx, ry;
-    Dma64Map<> mx, my;
+    Dma64Map<NW> mx, my;
     if (MODE == kWgrad) {
         const int64_t rows = t.k_end;   // group rows; reads past them return zero
         rx = make_dma_rsrc(B + t.row0 * p.ldb, rows * p.ldb * 2);
         ry = make_dma_rsrc(A + t.row0 * p.lda, rows * p.lda * 2);
         d64_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
-        d64_mnmaj(my, lda, t.y0, t.y_lim, wy * kWaveY, kFragY);
+        d64_mnmaj(my, lda, t.y0, t.y_lim, wy * WY, FY);
     } else {
         ry = make_dma_rsrc(A + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda * 2);
         const int y_last = t.y_lim - 1;
-        d64_kmaj(my, lda, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
+        d64_kmaj(my, lda, wy * WY, FY, [&](int r) { return r < t.y_lim ? r : y_last; });
         if (MODE == kFwd) {
             rx = make_dma_rsrc(B, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb * 2);
             d64_kmaj(mx, ldb, wx * 128, 4, [&](int r) {
@@ -163,8 +166,8 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
         const bool live = step < nk;
         const uint32_t base = lds0 + slot * kT64Bytes + wave * 1024;
 #pragma unroll
-        for (int j = 0; j < kD64PerWave; ++j) {
-            const uint32_t at = base + j * kWaves * 1024;
+        for (int j = 0; j < kPerWave; ++j) {
+            const uint32_t at = base + j * NW * 1024;
             if (kXK) dma16(rx, mx.vo[j], live ? k0 * 2u : kPastView, at);
             else dma16(rx, mx.vo[j] + (live ? k0 * ldb * 2u : 0u), live ? 0u : kPastView, at);
         }
@@ -174,8 +177,8 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
         const bool live = step < nk;
         const uint32_t base = lds0 + slot * kT64Bytes + wave * 1024;
 #pragma unroll
-        for (int j = 0; j < kD64PerWave; ++j) {
-            const uint32_t at = base + j * kWaves * 1024;
+        for (int j = 0; j < kPerWave; ++j) {
+            const uint32_t at = base + j * NW * 1024;
             if (kYK) dma16(ry, my.vo[j], live ? k0 * 2u : kPastView, at);
             else dma16(ry, my.vo[j] + (live ? k0 * lda * 2u : 0u), live ? 0u : kPastView, at);
         }
@@ -192,13 +195,13 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
         asm volatile("" ::: "memory");
     };
 
-    f32x16_t acc[4][kFragY];
+    f32x16_t acc[4][FY];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < kFragY; ++j) acc[i][j] = f32x16_t{};
+        for (int j = 0; j < FY; ++j) acc[i][j] = f32x16_t{};
 
-    typedef bf16x8_t FragSet[4 + kFragY];
+    typedef bf16x8_t FragSet[4 + FY];
     auto kfrag = [](const uint8_t* tile, uint32_t fr, int b) {
         return *reinterpret_cast<const bf16x8_t*>(tile + (fr ^ static_cast<uint32_t>(b << 5)));
     };
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
         const uint8_t* xt = lds + sx;
         const uint8_t* yt = lds + sy;
 #pragma unroll
-        for (int j = 0; j < kFragY; ++j)
+        for (int j = 0; j < FY; ++j)
             f[4 + j] = kYK ? kfrag(yt, my.fr[j], b) : frag_mnmaj(yt, my.fr[j], b);
 #pragma unroll
         for (int i = 0; i < 4; ++i) f[i] = kXK ? kfrag(xt, mx.fr[i], b) : frag_mnmaj(xt, mx.fr[i], b);
@@ -217,16 +220,16 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < kFragY; ++j)
+            for (int j = 0; j < FY; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[4 + j], acc[i][j], 0, 0, 0);
     };
-    constexpr int kReads = (kXK ? 4 : 8) + (kYK ? kFragY : 2 * kFragY);
-    using Pending = std::integral_constant<int, kD64PerWave>;   // one operand tile stays in flight
-    using Prolog = std::integral_constant<int, 3 * kD64PerWave>;
+    constexpr int kReads = (kXK ? 4 : 8) + (kYK ? FY : 2 * FY);
+    using Pending = std::integral_constant<int, kPerWave>;   // one operand tile stays in flight
+    using Prolog = std::integral_constant<int, 3 * kPerWave>;
 
     // A wave whose Y rows all lie past the tile's valid rows only loads its
     // share and joins the barriers.
-    const bool idle = wy * kWaveY >= t.y_lim;
+    const bool idle = wy * WY >= t.y_lim;
     FragSet fa, fb;
     if (nk > 0) {
         issue_x(0, 0);
@@ -252,13 +255,13 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
                 const uint32_t ox = sx * kT64Bytes, oy = sy * kT64Bytes;
                 read_frags(fb, ox, oy, 1);
                 mfmas(fa);
-                interleave_reads<0, 4 * kFragY, kReads>();
+                interleave_reads<0, 4 * FY, kReads>();
                 read_frags(fa, ox, oy, 2);
                 mfmas(fb);
-                interleave_reads<0, 4 * kFragY, kReads>();
+                interleave_reads<0, 4 * FY, kReads>();
                 read_frags(fb, ox, oy, 3);
                 mfmas(fa);
-                interleave_reads<0, 4 * kFragY, kReads>();
+                interleave_reads<0, 4 * FY, kReads>();
                 // Steps up to kt + 1 complete, every read of slots sx and sy done.
                 wait_lds(Pending{});
                 barrier();
@@ -266,7 +269,7 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
                 issue_x(kt + 3, sy);
                 read_frags(fa, nx * kT64Bytes, ny * kT64Bytes, 0);
                 mfmas(fb);
-                interleave_reads<0, 4 * kFragY, kReads>();
+                interleave_reads<0, 4 * FY, kReads>();
                 sx = nx;
                 sy = ny;
                 nx = ny + 1 == kSlots ? 0 : ny + 1;
@@ -275,7 +278,7 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_bf16_kernel(Params p) {
         }
         wait_loads_all();   // the tiles past the last step
     }
-    epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane);
+    epilogue<MODE, EPI, 64 * NW, WY>(p, t, lds, acc, wx, wy, lane);
 }
 
 // ------------------------------------------------------------------ generic kernel (any dtype)
@@ -376,7 +379,7 @@ void launch_one(const Job& j, const Params& p, hipStream_t s) {
     if (j.mfma) {
         const unsigned nb = mfma_blocks<MODE, EPI>(p, j.rows_cap);
         if (!nb) return;
-        hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+        hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, kWaves>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
         return;
     }
     const unsigned nb = simt_blocks<MODE>(p, j.rows_cap);
