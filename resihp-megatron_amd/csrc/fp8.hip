@@ -21,6 +21,8 @@
 // The MFMA is v_mfma_scale_f32_32x32x64_f8f6f4 with unit block scales; the
 // per-tensor scales are divided out in the epilogue, which then runs the same
 // SwiGLU / GELU / store code as the bf16 kernels (bf16 outputs).
+#include <type_traits>
+
 #include "gemm_common.h"
 
 namespace rhp {
@@ -209,11 +211,14 @@ __global__ void fp8_roll_kernel(float* hist, uint32_t* amax_bits, int n, int L) 
 
 // ------------------------------------------------------------------ fp8 GEMM
 //
-// Tiles, waves and epilogue as the bf16 kernels; K step 128 (one 128-byte
-// line per operand row), two LDS stages filled by direct loads.  A k64 block
-// is one v_mfma_scale_f32_32x32x64_f8f6f4: lane L holds row L % 32 and 32
-// consecutive k bytes, 32 (L / 32) .. +31, of both operands (the same k
-// assignment on both sides, so any consistent choice is a valid product).
+// Tiles, waves, LDS slots and epilogue as the bf16 kernel; an operand tile is
+// 256 rows by 128 k (one 128-byte line per row, 32 KB), filled by direct
+// loads into a ring of five slots (X0 Y0 X1 Y1 X2 ..., tile q in slot q mod
+// 5), so that X of step kt + 2 stays in flight across the barrier that closes
+// step kt.  A k64 block is one v_mfma_scale_f32_32x32x64_f8f6f4: lane L holds
+// row L % 32 and 32 consecutive k bytes, 32 (L / 32) .. +31, of both operands
+// (the same k assignment on both sides, so any consistent choice is a valid
+// product).
 //
 // MODE kFwd: rows grouped by offsets, K fixed (fwd and dgrad).
 // MODE kWgrad: K grouped: expert g contributes K = R_g padded rows; Y rows
@@ -221,11 +226,12 @@ __global__ void fp8_roll_kernel(float* hist, uint32_t* amax_bits, int n, int L) 
 // a[0] + Mo * poff[g] and b[0] + N * poff[g], both with row pitch R_g.
 
 constexpr int kF8K = 128;
-constexpr int kF8TileBytes = kTile * kF8K;                  // 32 KB per operand
-constexpr int kF8StageBytes = 2 * kF8TileBytes;
-constexpr int kF8PerWave = kF8TileBytes / 1024 / kWaves;   // loads per wave per operand per step
-constexpr int kF8LdsBytes = 2 * kF8StageBytes > kEpBytes ? 2 * kF8StageBytes : kEpBytes;
-static_assert(kF8LdsBytes <= 163840, "two 64 KB stages");
+constexpr int kF8TileBytes = kTile * kF8K;                  // 32 KB per operand tile
+constexpr int kF8PerWave = kF8TileBytes / 1024 / kWaves;   // loads per wave per operand tile
+constexpr int kF8Slots = 5;
+constexpr int kF8LdsBytes = kF8Slots * kF8TileBytes > kEpBytes ? kF8Slots * kF8TileBytes : kEpBytes;
+static_assert(kF8LdsBytes <= 163840, "five 32 KB slots");
+constexpr uint32_t kF8PastView = 0x7ffffff0u;   // soffset that puts every lane past its buffer view
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
@@ -308,16 +314,31 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
         });
     }
 
+    const int nk = (t.k_end - t.k_begin + kF8K - 1) / kF8K;
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-    auto issue = [&](int step, int stage) {
-        const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kF8K);
-        const uint32_t base = lds0 + stage * kF8StageBytes + wave * 1024;
+    // X (Y) tile of step `step` into slot `slot`; past the last step, zeros.
+    auto issue_x = [&](int step, int slot) {
+        const uint32_t soff = step < nk ? static_cast<uint32_t>(t.k_begin + step * kF8K) : kF8PastView;
+        const uint32_t base = lds0 + slot * kF8TileBytes + wave * 1024;
 #pragma unroll
-        for (int j = 0; j < kF8PerWave; ++j) {
-            const uint32_t at = base + j * kWaves * 1024;
-            dma16(rx, mx.vo[j], k0, at);
-            dma16(ry, my.vo[j], k0, at + kF8TileBytes);
-        }
+        for (int j = 0; j < kF8PerWave; ++j) dma16(rx, mx.vo[j], soff, base + j * kWaves * 1024);
+    };
+    auto issue_y = [&](int step, int slot) {
+        const uint32_t soff = step < nk ? static_cast<uint32_t>(t.k_begin + step * kF8K) : kF8PastView;
+        const uint32_t base = lds0 + slot * kF8TileBytes + wave * 1024;
+#pragma unroll
+        for (int j = 0; j < kF8PerWave; ++j) dma16(ry, my.vo[j], soff, base + j * kWaves * 1024);
+    };
+    // vmcnt(n loads of this wave) lgkmcnt(0).
+    auto wait_lds = [](auto n_c) {
+        constexpr int n = decltype(n_c)::value;
+        __builtin_amdgcn_s_waitcnt(0x0070 | (n & 15) | ((n >> 4) << 14));
+    };
+    auto barrier = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
     };
 
     f32x16_t acc[4][kFragY];
@@ -327,9 +348,10 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
         for (int j = 0; j < kFragY; ++j) acc[i][j] = f32x16_t{};
 
     typedef i32x8_t FragSet[4 + kFragY];
-    auto read_frags = [&](FragSet& f, int stage, int b) {
-        const uint8_t* xt = lds + stage * kF8StageBytes;
-        const uint8_t* yt = xt + kF8TileBytes;
+    // sx, sy: byte offsets of the slots of the X and Y tiles.
+    auto read_frags = [&](FragSet& f, uint32_t sx, uint32_t sy, int b) {
+        const uint8_t* xt = lds + sx;
+        const uint8_t* yt = lds + sy;
 #pragma unroll
         for (int j = 0; j < kFragY; ++j) f[4 + j] = f8_frag(yt, my.fr[j], b);
 #pragma unroll
@@ -344,37 +366,49 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
                                                                            0, 127);
     };
     constexpr int kReads = 2 * (4 + kFragY);
+    using Pending = std::integral_constant<int, kF8PerWave>;   // one operand tile stays in flight
+    using Prolog = std::integral_constant<int, 3 * kF8PerWave>;
 
-    const int nk = (t.k_end - t.k_begin + kF8K - 1) / kF8K;
     const bool idle = wy * kWaveY >= t.y_lim;
     FragSet fa, fb;
     if (nk > 0) {
-        issue(0, 0);
-        wait_loads_all();
-        __syncthreads();
-        if (!idle) read_frags(fa, 0, 0);
-    }
-    if (idle) {
-        for (int kt = 0; kt < nk; ++kt) {
-            if (kt + 1 < nk) issue(kt + 1, (kt & 1) ^ 1);
-            wait_loads_all();
-            __syncthreads();
+        issue_x(0, 0);
+        issue_y(0, 1);
+        issue_x(1, 2);
+        issue_y(1, 3);
+        issue_x(2, 4);
+        wait_lds(Prolog{});   // step 0 complete
+        barrier();
+        if (idle) {
+            for (int kt = 0; kt < nk; ++kt) {
+                wait_lds(Pending{});
+                barrier();
+                issue_y(kt + 2, (2 * kt) % kF8Slots);
+                issue_x(kt + 3, (2 * kt + 1) % kF8Slots);
+            }
+        } else {
+            read_frags(fa, 0, kF8TileBytes, 0);
+            // Slots of X and Y of step kt (sx, sy) and of step kt + 1 (nx, ny).
+            int sx = 0, sy = 1, nx = 2, ny = 3;
+            for (int kt = 0; kt < nk; ++kt) {
+                read_frags(fb, sx * kF8TileBytes, sy * kF8TileBytes, 1);
+                mfmas(fa);
+                interleave_reads<0, 4 * kFragY, kReads>();
+                // Steps up to kt + 1 complete, every read of slots sx and sy done.
+                wait_lds(Pending{});
+                barrier();
+                issue_y(kt + 2, sx);
+                issue_x(kt + 3, sy);
+                read_frags(fa, nx * kF8TileBytes, ny * kF8TileBytes, 0);
+                mfmas(fb);
+                interleave_reads<0, 4 * kFragY, kReads>();
+                sx = nx;
+                sy = ny;
+                nx = ny + 1 == kF8Slots ? 0 : ny + 1;
+                ny = nx + 1 == kF8Slots ? 0 : nx + 1;
+            }
         }
-    }
-    for (int kt = 0; kt < (idle ? 0 : nk); ++kt) {
-        const int st = kt & 1;
-        if (kt + 1 < nk) issue(kt + 1, st ^ 1);
-        read_frags(fb, st, 1);
-        mfmas(fa);
-        interleave_reads<0, 4 * kFragY, kReads>();
-        // The loads of step kt + 1 have landed in every wave's share and no wave
-        // still reads stage st (its block-1 reads complete before the barrier).
-        wait_loads_all();
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-        read_frags(fa, st ^ 1, 0);
-        mfmas(fb);
-        interleave_reads<0, 4 * kFragY, kReads>();
+        wait_loads_all();   // the tiles past the last step
     }
     const float mul = p.scale_inv_y[0] * p.scale_inv_x[g * p.scale_x_stride];
     epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane, mul);

@@ -230,17 +230,22 @@ struct AuxHalf {
 template <int MODE, int EPI, int NT>
 __device__ __forceinline__ void load_aux_half(const Params& p, const Tile& t, int r0, AuxHalf<EPI, NT>& aux) {
     if constexpr (AuxHalf<EPI, NT>::kParts > 0) {
-        const uint16_t* hp = static_cast<const uint16_t*>(p.aux[t.g]);
+        // A buffer view of the tile's rows keeps one 32-bit offset per piece.
+        const uint16_t* hp = static_cast<const uint16_t*>(p.aux[t.g]) + (t.row0 + t.y0) * p.ldaux + t.x0;
+        const int64_t bytes = static_cast<int64_t>(t.y_lim) * p.ldaux * 2;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(hp), 0, static_cast<int>(bytes > 0x7ffffff0 ? 0x7ffffff0 : bytes), 0x00020000);
+        const int up = EPI == kEpiSwigluBwd ? p.f * 2 : 0;
 #pragma unroll
         for (int n = 0; n < AuxHalf<EPI, NT>::kPieces; ++n) {
             const int idx = threadIdx.x + n * NT;
             const int r = idx >> 6, x = (idx & 63) * 4;
             const int yr = r0 + r;
             if (yr >= t.y_lim || x >= t.x_lim) continue;
-            const int64_t row = t.row0 + t.y0 + yr;
-            const uint16_t* src = hp + row * p.ldaux + t.x0 + x;
-            aux.v[n][0] = *reinterpret_cast<const uint2*>(src);
-            if (EPI == kEpiSwigluBwd) aux.v[n][1] = *reinterpret_cast<const uint2*>(src + p.f);
+            const int off = (yr * p.ldaux + x) * 2;
+            aux.v[n][0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+            if (EPI == kEpiSwigluBwd)
+                aux.v[n][1] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, up, 0));
         }
     }
 }
