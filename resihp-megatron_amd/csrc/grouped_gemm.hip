@@ -41,7 +41,6 @@ namespace {
 
 constexpr int kK64 = 64;
 constexpr int kT64Bytes = kTile * kK64 * 2;                // 32 KB per operand tile
-constexpr int kD64PerWave = kT64Bytes / 1024 / kWaves;     // loads per wave per operand tile
 static_assert((kT64Bytes / 1024) % kWaves == 0, "whole loads per wave");
 
 template <int NW = kWaves>
@@ -160,24 +159,25 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
     const int nk = (t.k_end - t.k_begin + kK64 - 1) / kK64;
 
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-    // X (Y) tile of step `step` into slot `slot`; past the last step, zeros.
-    auto issue_x = [&](int step, int slot) {
+    // Loads [j0, j1) of the X (Y) tile of step `step` into slot `slot`; past
+    // the last step, zeros.
+    auto issue_x = [&](int step, int slot, int j0 = 0, int j1 = kT64Bytes / 1024 / NW) {
         const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kK64);
         const bool live = step < nk;
         const uint32_t base = lds0 + slot * kT64Bytes + wave * 1024;
 #pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
+        for (int j = j0; j < j1; ++j) {
             const uint32_t at = base + j * NW * 1024;
             if (kXK) dma16(rx, mx.vo[j], live ? k0 * 2u : kPastView, at);
             else dma16(rx, mx.vo[j] + (live ? k0 * ldb * 2u : 0u), live ? 0u : kPastView, at);
         }
     };
-    auto issue_y = [&](int step, int slot) {
+    auto issue_y = [&](int step, int slot, int j0 = 0, int j1 = kT64Bytes / 1024 / NW) {
         const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kK64);
         const bool live = step < nk;
         const uint32_t base = lds0 + slot * kT64Bytes + wave * 1024;
 #pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
+        for (int j = j0; j < j1; ++j) {
             const uint32_t at = base + j * NW * 1024;
             if (kYK) dma16(ry, my.vo[j], live ? k0 * 2u : kPastView, at);
             else dma16(ry, my.vo[j] + (live ? k0 * lda * 2u : 0u), live ? 0u : kPastView, at);
@@ -216,16 +216,44 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) f[i] = kXK ? kfrag(xt, mx.fr[i], b) : frag_mnmaj(xt, mx.fr[i], b);
     };
-    auto mfmas = [&](const FragSet& f) {
+    // MFMAs [m0, m1) of a block: accumulator (m / FY, m % FY).
+    auto mfma_range = [&](const FragSet& f, int m0, int m1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < FY; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[4 + j], acc[i][j], 0, 0, 0);
+        for (int m = m0; m < m1; ++m)
+            acc[m / FY][m % FY] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[m / FY], f[4 + m % FY], acc[m / FY][m % FY],
+                                                                        0, 0, 0);
     };
-    constexpr int kReads = (kXK ? 4 : 8) + (kYK ? FY : 2 * FY);
+    // One fragment of block b: Y fragment j (n = 4 + j) or X fragment i (n = i).
+    auto read_one = [&](FragSet& f, uint32_t sx, uint32_t sy, int b, int n) {
+        if (n >= 4) {
+            const uint8_t* yt = lds + sy;
+            f[n] = kYK ? kfrag(yt, my.fr[n - 4], b) : frag_mnmaj(yt, my.fr[n - 4], b);
+        } else {
+            const uint8_t* xt = lds + sx;
+            f[n] = kXK ? kfrag(xt, mx.fr[n], b) : frag_mnmaj(xt, mx.fr[n], b);
+        }
+    };
+    // The MFMAs of one block (fragments f) in four quarters, the fragment reads
+    // of the next block (into g, from slots sx, sy, block b) in the order its
+    // MFMAs use them, and n <= 4 loads, one after each of the first n quarters:
+    // the loads then reach the address unit at the rate it drains them,
+    // instead of every wave queueing a whole tile at once and stalling.
+    auto block = [&](const FragSet& f, FragSet& g, uint32_t sx, uint32_t sy, int b, auto load, int n) {
+        static_assert(FY == 2, "read order for two Y fragments");
+        constexpr int order[6] = {4, 0, 5, 1, 2, 3};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+                if (2 * q + r < 6) read_one(g, sx, sy, b, order[2 * q + r]);
+            mfma_range(f, 2 * q, 2 * q + 2);
+            if (q < n) load(q);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto no_load = [](int) {};
     using Pending = std::integral_constant<int, kPerWave>;   // one operand tile stays in flight
-    using Prolog = std::integral_constant<int, 3 * kPerWave>;
+    using Prolog = std::integral_constant<int, kPerWave + kPerWave / 2>;   // X1 and half of Y1 in flight
 
     // A wave whose Y rows all lie past the tile's valid rows only loads its
     // share and joins the barriers.
@@ -235,41 +263,37 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
         issue_x(0, 0);
         issue_y(0, 1);
         issue_x(1, 2);
-        issue_y(1, 3);
-        issue_x(2, 4);
+        issue_y(1, 3, 0, 2);
         wait_lds(Prolog{});   // step 0 complete
         barrier();
         if (idle) {
             for (int kt = 0; kt < nk; ++kt) {
+                issue_y(kt + 1, (2 * kt + 3) % kSlots, 2, 4);
+                issue_x(kt + 2, (2 * kt + 4) % kSlots);
                 wait_lds(Pending{});
                 barrier();
-                const int sx = (2 * kt) % kSlots, sy = (2 * kt + 1) % kSlots;
-                issue_y(kt + 2, sx);
-                issue_x(kt + 3, sy);
+                issue_y(kt + 2, (2 * kt) % kSlots, 0, 2);
             }
         } else {
             read_frags(fa, 0, kT64Bytes, 0);
-            // Slots of X and Y of step kt (sx, sy) and of step kt + 1 (nx, ny).
-            int sx = 0, sy = 1, nx = 2, ny = 3;
+            // Slots of X and Y of step kt (sx, sy), of step kt + 1 (nx, ny),
+            // and the slot that receives X of step kt + 2 (fx).  Two loads go
+            // with each block: the second half of Y of step kt + 1 (block 0),
+            // X of step kt + 2 (blocks 1 and 2), and after the barrier the
+            // first half of Y of step kt + 2 (block 3).
+            int sx = 0, sy = 1, nx = 2, ny = 3, fx = 4;
+            static_assert(kPerWave == 4, "two loads with each k16 block");
             for (int kt = 0; kt < nk; ++kt) {
                 const uint32_t ox = sx * kT64Bytes, oy = sy * kT64Bytes;
-                read_frags(fb, ox, oy, 1);
-                mfmas(fa);
-                interleave_reads<0, 4 * FY, kReads>();
-                read_frags(fa, ox, oy, 2);
-                mfmas(fb);
-                interleave_reads<0, 4 * FY, kReads>();
-                read_frags(fb, ox, oy, 3);
-                mfmas(fa);
-                interleave_reads<0, 4 * FY, kReads>();
-                // Steps up to kt + 1 complete, every read of slots sx and sy done.
+                block(fa, fb, ox, oy, 1, [&](int q) { issue_y(kt + 1, ny, q + 2, q + 3); }, 2);
+                block(fb, fa, ox, oy, 2, [&](int q) { issue_x(kt + 2, fx, q, q + 1); }, 2);
+                block(fa, fb, ox, oy, 3, [&](int q) { issue_x(kt + 2, fx, q + 2, q + 3); }, 2);
+                // Steps up to kt + 1 complete (X of step kt + 2 in flight),
+                // every read of slots sx and sy done.
                 wait_lds(Pending{});
                 barrier();
-                issue_y(kt + 2, sx);
-                issue_x(kt + 3, sy);
-                read_frags(fa, nx * kT64Bytes, ny * kT64Bytes, 0);
-                mfmas(fb);
-                interleave_reads<0, 4 * FY, kReads>();
+                block(fb, fa, nx * kT64Bytes, ny * kT64Bytes, 0, [&](int q) { issue_y(kt + 2, sx, q, q + 1); }, 2);
+                fx = sy;
                 sx = nx;
                 sy = ny;
                 nx = ny + 1 == kSlots ? 0 : ny + 1;
