@@ -244,7 +244,7 @@ __device__ __forceinline__ void load_aux_half(const Params& p, const Tile& t, in
             if (yr >= t.y_lim || x >= t.x_lim) continue;
             const int off = (yr * p.ldaux + x) * 2;
             aux.v[n][0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
-            if (EPI == kEpiSwigluBwd)
+            if constexpr (EPI == kEpiSwigluBwd)
                 aux.v[n][1] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, up, 0));
         }
     }

@@ -251,7 +251,6 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto no_load = [](int) {};
     using Pending = std::integral_constant<int, kPerWave>;   // one operand tile stays in flight
     using Prolog = std::integral_constant<int, kPerWave + kPerWave / 2>;   // X1 and half of Y1 in flight
 
