@@ -77,7 +77,8 @@ struct CastParams {
     uint8_t* qt;              // expert g: [cols][R_g] at qt + cols * poff[g], or null
 };
 
-constexpr int kCastTile = 64;
+constexpr int kCastRows = 128;   // rows of one block's tile (row tiles of an expert: padded rows / 128)
+constexpr int kCastCols = 128;   // columns of one block's tile (partial tiles mask 64-column segments)
 
 // 4 x 4 byte transpose: word j holds bytes (row j, cols 0..3); word i of the
 // result holds bytes (rows 0..3, col i).
@@ -92,25 +93,27 @@ __device__ __forceinline__ void transpose4x4(const uint32_t a[4], uint32_t b[4])
     b[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
-// One block: 64 rows x 64 columns of one expert; thread t quantises row t / 4,
-// columns 16 (t % 4) .. +15.  Rows past the expert's count quantise to zero
-// (qt padding).  The transposed copy goes through LDS as words (rows padded to
-// 17 words, so the column reads below hit 64 distinct banks); thread t then
-// transposes the 4 x 4 byte block (rows 4 (t % 16) .., columns 4 (t / 16) ..)
-// in registers and writes 4 bytes to each of 4 output rows, 16 lanes covering
-// 64 contiguous bytes of one output row.
+// One block: 128 rows x 128 columns of one expert.  Thread t quantises row
+// t / 2, columns 64 (t % 2) .. +63 (eight 16-byte loads, four 16-byte stores of
+// the row-major copy).  Rows past the expert's count quantise to zero (qt
+// padding).  The transposed copy goes through LDS as words (rows padded to 33
+// words, so both the row writes and the column reads below hit distinct
+// banks); thread t then takes the 16 x 4 byte block (rows 16 (t / 32) .., 4
+// columns from 4 (t % 32)), transposes its four 4 x 4 blocks in registers and
+// writes 16 bytes (16 rows) to each of 4 output rows: each output row gets a
+// whole 128-byte line from the block.
 template <int FMT>
 __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
-    __shared__ uint32_t tw[kCastTile][kCastTile / 4 + 1];
+    __shared__ uint32_t tw[kCastRows][kCastCols / 4 + 1];
     __shared__ float wave_max[4];
-    const int ct_n = c.cols / kCastTile;
+    const int ct_n = (c.cols + kCastCols - 1) / kCastCols;
     uint32_t b = blockIdx.x;
     int g = 0, rt = 0, ct = 0, count = 0, rpad = 0;
     bool found = false;
     for (; g < c.G; ++g) {
         count = c.offsets[g + 1] - c.offsets[g];
         rpad = c.poff[g + 1] - c.poff[g];
-        const uint32_t n = static_cast<uint32_t>(rpad / kCastTile) * ct_n;
+        const uint32_t n = static_cast<uint32_t>(rpad / kCastRows) * ct_n;
         if (b < n) {
             rt = b / ct_n;
             ct = b % ct_n;
@@ -123,48 +126,56 @@ __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
     if (blockIdx.x == 0 && threadIdx.x == 0) *c.scale_inv = 1.0f / scale;
     if (!found) return;
 
-    const int t = threadIdx.x, r = t >> 2, cs = (t & 3) * 16;
-    const int row = rt * kCastTile + r;                 // relative to the expert
-    const int col = ct * kCastTile + cs;
-    const bool valid = row < count;
-    float v[16];
-    if (valid) {
-        const uint4* src = reinterpret_cast<const uint4*>(c.x + (c.offsets[g] + row) * c.ldx + col);
-        const uint4 u0 = src[0], u1 = src[1];
-        const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            v[2 * i] = __uint_as_float(w[i] << 16);
-            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
-    }
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    const int t = threadIdx.x, r = t >> 1, seg = t & 1;
+    const int row = rt * kCastRows + r;                 // relative to the expert
+    const int col = ct * kCastCols + seg * 64;
+    const bool valid = row < count, col_ok = col < c.cols;
     const float lim = fp8_max(FMT);
-    uint32_t packed[4];
+    float m = 0.0f;
+    uint32_t packed[16];
+    if (col_ok) {
+        if (valid) {
+            const uint4* src = reinterpret_cast<const uint4*>(c.x + (c.offsets[g] + row) * c.ldx + col);
+            uint4 u[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float y[4];
+            for (int i = 0; i < 8; ++i) u[i] = src[i];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = fminf(fmaxf(v[4 * i + e] * scale, -lim), lim);
-        packed[i] = pack4<FMT>(y[0], y[1], y[2], y[3]);
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[2 * e] = __uint_as_float(w[e] << 16);
+                    v[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    m = fmaxf(m, fabsf(v[e]));
+                    v[e] = fminf(fmaxf(v[e] * scale, -lim), lim);
+                }
+                packed[2 * i] = pack4<FMT>(v[0], v[1], v[2], v[3]);
+                packed[2 * i + 1] = pack4<FMT>(v[4], v[5], v[6], v[7]);
+            }
+            if (c.q) {
+                uint4* dst = reinterpret_cast<uint4*>(c.q + (static_cast<int64_t>(c.offsets[g]) + row) * c.cols + col);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    dst[i] = make_uint4(packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) packed[i] = 0u;
+        }
+        if (c.qt) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tw[r][seg * 16 + i] = packed[i];
+        }
     }
-    if (valid && c.q)
-        *reinterpret_cast<uint4*>(c.q + (static_cast<int64_t>(c.offsets[g]) + row) * c.cols + col) =
-            make_uint4(packed[0], packed[1], packed[2], packed[3]);
 
     // amax: wave maximum, then one atomic per block (non-negative floats order like their bits)
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if ((t & 63) == 0) wave_max[t >> 6] = m;
-    if (c.qt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) tw[r][cs / 4 + i] = packed[i];
-    }
     __syncthreads();
     if (t == 0) {
         // The running maximum only grows, so a block whose maximum does not exceed the value it
@@ -175,15 +186,25 @@ __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
         if (bm > 0.0f && __float_as_uint(bm) > seen) atomicMax(c.amax_bits, __float_as_uint(bm));
     }
     if (c.qt) {
-        const int rg = t & 15, cg = t >> 4;
-        uint32_t a[4], b[4];
+        const int cg = t & 31, rg = t >> 5;
+        const int ccol = ct * kCastCols + 4 * cg;
+        if (ccol < c.cols) {
+            uint32_t a[16], o[4][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = tw[4 * rg + j][cg];
-        transpose4x4(a, b);
-        uint8_t* dst = c.qt + static_cast<int64_t>(c.cols) * c.poff[g] +
-                       static_cast<int64_t>(ct * kCastTile + 4 * cg) * rpad + rt * kCastTile + 4 * rg;
+            for (int j = 0; j < 16; ++j) a[j] = tw[16 * rg + j][cg];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<uint32_t*>(dst + static_cast<int64_t>(i) * rpad) = b[i];
+            for (int q = 0; q < 4; ++q) {
+                uint32_t bq[4];
+                transpose4x4(a + 4 * q, bq);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[i][q] = bq[i];
+            }
+            uint8_t* dst = c.qt + static_cast<int64_t>(c.cols) * c.poff[g] + static_cast<int64_t>(ccol) * rpad +
+                           rt * kCastRows + 16 * rg;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(i) * rpad) = make_uint4(o[i][0], o[i][1], o[i][2], o[i][3]);
+        }
     }
 }
 
@@ -462,7 +483,7 @@ extern "C" int rhp_fp8_cast(const void* x, int x_dtype, int64_t ldx, int cols, i
     RHP_REQUIRE(x && offsets && poff && history && amax_bits && scale_inv, "rhp_fp8_cast: null pointer");
     RHP_REQUIRE(q || qt, "rhp_fp8_cast: nothing to write");
     RHP_REQUIRE(G >= 1 && hist_len >= 1 && margin >= 0 && margin < 64, "rhp_fp8_cast: bad G, history or margin");
-    RHP_REQUIRE(cols > 0 && cols % kCastTile == 0, "rhp_fp8_cast: cols must be a positive multiple of 64");
+    RHP_REQUIRE(cols > 0 && cols % 64 == 0, "rhp_fp8_cast: cols must be a positive multiple of 64");
     RHP_REQUIRE(ldx >= cols && ldx % 8 == 0 && aligned16(x), "rhp_fp8_cast: x rows must be 16-byte aligned");
     RHP_REQUIRE(rows_cap >= 0 && rows_cap < (int64_t(1) << 31), "rhp_fp8_cast: rows_cap out of range");
     RHP_REQUIRE((!q || aligned16(q)) && (!qt || aligned16(qt)), "rhp_fp8_cast: outputs must be 16-byte aligned");
@@ -481,8 +502,8 @@ extern "C" int rhp_fp8_cast(const void* x, int x_dtype, int64_t ldx, int cols, i
     c.q = static_cast<uint8_t*>(q);
     c.qt = static_cast<uint8_t*>(qt);
     // rows_cap bounds the padded rows: sum_g roundup(n_g, 128) <= rows_cap + 127 G.
-    const int64_t row_tiles = (rows_cap + 127 * static_cast<int64_t>(G)) / kCastTile + G;
-    const int64_t blocks = row_tiles * (cols / kCastTile);
+    const int64_t row_tiles = (rows_cap + 127 * static_cast<int64_t>(G)) / kCastRows + G;
+    const int64_t blocks = row_tiles * ((cols + kCastCols - 1) / kCastCols);
     RHP_REQUIRE(blocks < (int64_t(1) << 31), "rhp_fp8_cast: too many tiles");
     if (blocks == 0) return 0;
     if (f8 == kFmtE4m3)
