@@ -93,15 +93,16 @@ __device__ __forceinline__ void transpose4x4(const uint32_t a[4], uint32_t b[4])
     b[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
-// One block: 128 rows x 128 columns of one expert.  Thread t quantises row
-// t / 2, columns 64 (t % 2) .. +63 (eight 16-byte loads, four 16-byte stores of
-// the row-major copy).  Rows past the expert's count quantise to zero (qt
-// padding).  The transposed copy goes through LDS as words (rows padded to 33
-// words, so both the row writes and the column reads below hit distinct
-// banks); thread t then takes the 16 x 4 byte block (rows 16 (t / 32) .., 4
-// columns from 4 (t % 32)), transposes its four 4 x 4 blocks in registers and
-// writes 16 bytes (16 rows) to each of 4 output rows: each output row gets a
-// whole 128-byte line from the block.
+// One block: 128 rows x 128 columns of one expert, wave w owning rows 32 w ..
+// +31.  Load i of lane l reads row 32 w + 4 i + l / 16, columns 8 (l % 16) ..
+// +7, so one load instruction covers four whole 256-byte row segments and one
+// 8-byte-a-lane store of the row-major copy four whole 128-byte lines.  Rows
+// past the expert's count load as zero and quantise to zero (the qt padding).
+// The transposed copy goes through LDS as words (rows padded to 33 words);
+// thread t then takes rows 16 (t % 8) .. +15 by columns 4 (t / 8) .. +3,
+// transposes its four 4 x 4 byte blocks in registers and stores 16 bytes to each
+// of 4 output rows: eight consecutive lanes fill one 128-byte line of an output
+// row, so a transposed store instruction covers eight whole lines.
 template <int FMT>
 __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
     __shared__ uint32_t tw[kCastRows][kCastCols / 4 + 1];
@@ -126,56 +127,60 @@ __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
     if (blockIdx.x == 0 && threadIdx.x == 0) *c.scale_inv = 1.0f / scale;
     if (!found) return;
 
-    const int t = threadIdx.x, r = t >> 1, seg = t & 1;
-    const int row = rt * kCastRows + r;                 // relative to the expert
-    const int col = ct * kCastCols + seg * 64;
-    const bool valid = row < count, col_ok = col < c.cols;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int col = ct * kCastCols + 8 * (lane & 15);
+    const bool col_ok = col < c.cols;
+    const int64_t first = c.offsets[g];                  // the expert's first row in x and q
+    const int r0 = 32 * w + (lane >> 4);                 // tile row of load 0; load i adds 4 i
     const float lim = fp8_max(FMT);
     float m = 0.0f;
-    uint32_t packed[16];
-    if (col_ok) {
-        if (valid) {
-            const uint4* src = reinterpret_cast<const uint4*>(c.x + (c.offsets[g] + row) * c.ldx + col);
-            uint4 u[8];
+    uint4 u[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) u[i] = src[i];
+    for (int i = 0; i < 8; ++i) {
+        const int row = rt * kCastRows + r0 + 4 * i;
+        u[i] = make_uint4(0u, 0u, 0u, 0u);
+        if (col_ok && row < count) u[i] = *reinterpret_cast<const uint4*>(c.x + (first + row) * c.ldx + col);
+    }
+    uint32_t pk[8][2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t wd[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = __uint_as_float(wd[e] << 16);
+            v[2 * e + 1] = __uint_as_float(wd[e] & 0xffff0000u);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            m = fmaxf(m, fabsf(v[e]));
+            v[e] = fminf(fmaxf(v[e] * scale, -lim), lim);
+        }
+        pk[i][0] = pack4<FMT>(v[0], v[1], v[2], v[3]);
+        pk[i][1] = pack4<FMT>(v[4], v[5], v[6], v[7]);
+    }
+    if (col_ok) {
+        if (c.q) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
-                float v[8];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[2 * e] = __uint_as_float(w[e] << 16);
-                    v[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-                }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    m = fmaxf(m, fabsf(v[e]));
-                    v[e] = fminf(fmaxf(v[e] * scale, -lim), lim);
-                }
-                packed[2 * i] = pack4<FMT>(v[0], v[1], v[2], v[3]);
-                packed[2 * i + 1] = pack4<FMT>(v[4], v[5], v[6], v[7]);
+                const int row = rt * kCastRows + r0 + 4 * i;
+                if (row < count)
+                    *reinterpret_cast<uint2*>(c.q + (first + row) * c.cols + col) = make_uint2(pk[i][0], pk[i][1]);
             }
-            if (c.q) {
-                uint4* dst = reinterpret_cast<uint4*>(c.q + (static_cast<int64_t>(c.offsets[g]) + row) * c.cols + col);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    dst[i] = make_uint4(packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) packed[i] = 0u;
         }
         if (c.qt) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) tw[r][seg * 16 + i] = packed[i];
+            for (int i = 0; i < 8; ++i) {
+                tw[r0 + 4 * i][2 * (lane & 15)] = pk[i][0];
+                tw[r0 + 4 * i][2 * (lane & 15) + 1] = pk[i][1];
+            }
         }
     }
 
     // amax: wave maximum, then one atomic per block (non-negative floats order like their bits)
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((t & 63) == 0) wave_max[t >> 6] = m;
+    if (lane == 0) wave_max[w] = m;
     __syncthreads();
     if (t == 0) {
         // The running maximum only grows, so a block whose maximum does not exceed the value it
@@ -186,12 +191,12 @@ __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
         if (bm > 0.0f && __float_as_uint(bm) > seen) atomicMax(c.amax_bits, __float_as_uint(bm));
     }
     if (c.qt) {
-        const int cg = t & 31, rg = t >> 5;
+        const int chunk = t & 7, cg = t >> 3;
         const int ccol = ct * kCastCols + 4 * cg;
         if (ccol < c.cols) {
             uint32_t a[16], o[4][4];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a[j] = tw[16 * rg + j][cg];
+            for (int j = 0; j < 16; ++j) a[j] = tw[16 * chunk + j][cg];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 uint32_t bq[4];
@@ -200,7 +205,7 @@ __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
                 for (int i = 0; i < 4; ++i) o[i][q] = bq[i];
             }
             uint8_t* dst = c.qt + static_cast<int64_t>(c.cols) * c.poff[g] + static_cast<int64_t>(ccol) * rpad +
-                           rt * kCastRows + 16 * rg;
+                           rt * kCastRows + 16 * chunk;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(i) * rpad) = make_uint4(o[i][0], o[i][1], o[i][2], o[i][3]);
