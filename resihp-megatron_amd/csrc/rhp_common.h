@@ -58,18 +58,20 @@ struct bf16 {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
-// Round-to-nearest-even float -> bfloat16 (quiet NaN preserved).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
-}
+// Round-to-nearest-even float -> bfloat16, NaN -> quiet NaN with the sign and
+// top payload bits kept: gfx950's v_cvt_pk_bf16_f32, one instruction per two
+// values.  It equals the integer form (u + 0x7fff + ((u >> 16) & 1)) >> 16,
+// with NaN as (u >> 16) | 0x40, on every one of the 2^32 float bit patterns
+// (checked exhaustively on the GPU).
+typedef __bf16 bf16x2_hw_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_hw_t __attribute__((ext_vector_type(2)));
 
 // Packs two floats into two bfloat16 halves of one dword (lo first).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+    const f32x2_hw_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_hw_t));
 }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return static_cast<uint16_t>(pack_bf16x2(f, 0.0f)); }
 
 // Typed element load/store with float/double compute types.
 template <class S> struct Elem;
