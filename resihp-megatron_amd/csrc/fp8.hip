@@ -540,6 +540,9 @@ extern "C" int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets,
     RHP_REQUIRE(N > 0 && N % 64 == 0, "rhp_fp8_gemm: N must be a positive multiple of 64");
     RHP_REQUIRE(rows_cap >= 0 && rows_cap < (int64_t(1) << 31), "rhp_fp8_gemm: rows_cap out of range");
     RHP_REQUIRE(ldc > 0 && ldc < (int64_t(1) << 31), "rhp_fp8_gemm: bad ldc");
+    // The epilogue writes (and reads aux) through views of kTile rows with 32-bit byte offsets.
+    RHP_REQUIRE(std::max({ldc, ldc2, ldaux}) * 2 * kTile < (int64_t(1) << 31),
+                "rhp_fp8_gemm: output, activation and pre-activation rows must be narrower than 2^22 elements");
     const int mode = kgroups ? kWgrad : kFwd;
     Params p{};
     const int ng = kgroups ? 1 : G;

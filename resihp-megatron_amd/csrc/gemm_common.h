@@ -197,6 +197,8 @@ __device__ __forceinline__ void load_bf16x4(const uint16_t* p, float* o) {
     o[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
+constexpr uint32_t kOutOfRange = 0x80000000u;   // a buffer offset past every view: loads read zero, stores drop
+
 // Epilogue staging: half a tile of fp32 accumulators, rows padded by 16 bytes
 // so that the 16 lanes of a ds_write_b128 (16 consecutive rows) hit distinct
 // bank groups.
@@ -218,8 +220,37 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// A buffer view of a tile's rows in an output or aux matrix: rows [0, rows)
+// (at most a tile's kTile) from matrix row `first`, starting at column x0.  Byte offsets below the view's
+// extent are the tile's valid rows; past it, loads read zero and stores are
+// dropped, so the pieces of rows past the tile's last valid row need no
+// branch.  Views and offsets stay below 2 GiB (the host admits no row wider than
+// 2^31 / (2 kTile) bytes).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_view(const void* base, int64_t first, int ld, int x0, int rows) {
+    const uint16_t* p = static_cast<const uint16_t*>(base) + first * ld + x0;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p), 0, min(rows, kTile) * ld * 2, 0x00020000);
+}
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void view_store_bf16x4(__amdgpu_buffer_rsrc_t v, uint32_t off, uint32_t soff, float a, float b,
+                                                  float c, float d) {
+    u32x2_t w;
+    w[0] = pack_bf16x2(a, b);
+    w[1] = pack_bf16x2(c, d);
+    __builtin_amdgcn_raw_buffer_store_b64(w, v, static_cast<int>(off), static_cast<int>(soff), 0);
+}
+__device__ __forceinline__ uint2 view_load_b64(__amdgpu_buffer_rsrc_t v, uint32_t off, uint32_t soff) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(v, static_cast<int>(off), static_cast<int>(soff), 0));
+}
+
+// Output (and aux) row of a tile's row 0: WGRAD writes dW rows, the others token rows.
+template <int MODE>
+__device__ __forceinline__ int64_t tile_first_row(const Tile& t) {
+    return MODE == kWgrad ? t.y0 : t.row0 + t.y0;
+}
+
 // The pre-activation values a backward epilogue needs (GELU: hpre, SwiGLU:
 // gate and up), loaded for one half before its accumulators are staged.
+// Thread t covers rows r0 + t / 64 + (NT / 64) n and columns 4 (t % 64) .. + 3.
 template <int EPI, int NT>
 struct AuxHalf {
     static constexpr int kPieces = kEpRows * 64 / NT;     // 4-column pieces per thread
@@ -230,22 +261,14 @@ struct AuxHalf {
 template <int MODE, int EPI, int NT>
 __device__ __forceinline__ void load_aux_half(const Params& p, const Tile& t, int r0, AuxHalf<EPI, NT>& aux) {
     if constexpr (AuxHalf<EPI, NT>::kParts > 0) {
-        // A buffer view of the tile's rows keeps one 32-bit offset per piece.
-        const uint16_t* hp = static_cast<const uint16_t*>(p.aux[t.g]) + (t.row0 + t.y0) * p.ldaux + t.x0;
-        const int64_t bytes = static_cast<int64_t>(t.y_lim) * p.ldaux * 2;
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t*>(hp), 0, static_cast<int>(bytes > 0x7ffffff0 ? 0x7ffffff0 : bytes), 0x00020000);
-        const int up = EPI == kEpiSwigluBwd ? p.f * 2 : 0;
+        const __amdgpu_buffer_rsrc_t view = tile_view(p.aux[t.g], tile_first_row<MODE>(t), p.ldaux, t.x0, t.y_lim);
+        const int x = (threadIdx.x & 63) * 4;
+        uint32_t off = x < t.x_lim ? static_cast<uint32_t>(((r0 + (threadIdx.x >> 6)) * p.ldaux + x) * 2) : kOutOfRange;
+        const uint32_t step = static_cast<uint32_t>((NT / 64) * p.ldaux * 2);
 #pragma unroll
-        for (int n = 0; n < AuxHalf<EPI, NT>::kPieces; ++n) {
-            const int idx = threadIdx.x + n * NT;
-            const int r = idx >> 6, x = (idx & 63) * 4;
-            const int yr = r0 + r;
-            if (yr >= t.y_lim || x >= t.x_lim) continue;
-            const int off = (yr * p.ldaux + x) * 2;
-            aux.v[n][0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
-            if constexpr (EPI == kEpiSwigluBwd)
-                aux.v[n][1] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, up, 0));
+        for (int n = 0; n < AuxHalf<EPI, NT>::kPieces; ++n, off += step) {
+            aux.v[n][0] = view_load_b64(view, off, 0);
+            if constexpr (EPI == kEpiSwigluBwd) aux.v[n][1] = view_load_b64(view, off, static_cast<uint32_t>(p.f * 2));
         }
     }
 }
@@ -259,56 +282,63 @@ __device__ __forceinline__ void unpack_bf16x4(uint2 v, float* o) {
 
 // Rows [r0, r0 + 128) of the tile, staged in ep.  Thread t of NT handles
 // 4-column pieces t, t + NT, ...; a wave covers one row (or two rows of 128
-// columns).
+// columns).  Stores go through views of the tile's valid rows, so that a
+// piece's address is one add from the previous one's and pieces of rows past
+// the tile drop out in the memory unit.
 template <int MODE, int EPI, int NT>
 __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, const float* ep, int r0,
                                               const AuxHalf<EPI, NT>& aux) {
     const int g = t.g;
+    const int64_t first = tile_first_row<MODE>(t);
     if (EPI == kEpiSwigluFwd) {
         // X columns of the tile are [gate 64 | up 64] for each half of 128
-        // activation columns; piece a covers activation columns 4a .. 4a + 3.
-        uint16_t* hpre = static_cast<uint16_t*>(p.c[g]);
-        uint16_t* act = static_cast<uint16_t*>(p.c2[g]);
-#pragma unroll 4
-        for (int idx = threadIdx.x; idx < kEpRows * 32; idx += NT) {
-            const int r = idx >> 5, a = (idx & 31) * 4;
-            const int yr = r0 + r, col = t.x0 + a;
-            if (yr >= t.y_lim || col >= p.N) continue;
-            const int xg = (a >> 6) * 128 + (a & 63);
+        // activation columns; thread t covers activation columns 4 (t % 32) ..
+        // + 3 of rows r0 + t / 32 + (NT / 32) n.
+        const __amdgpu_buffer_rsrc_t hv = tile_view(p.c[g], first, p.ldc, t.x0, t.y_lim);
+        const __amdgpu_buffer_rsrc_t av = tile_view(p.c2[g], first, p.ldc2, t.x0, t.y_lim);
+        const int rr = threadIdx.x >> 5, a = (threadIdx.x & 31) * 4;
+        const int xg = (a >> 6) * 128 + (a & 63);
+        const bool ok = a < t.x_lim;
+        uint32_t oh = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc + a) * 2) : kOutOfRange;
+        uint32_t oa = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc2 + a) * 2) : kOutOfRange;
+        const uint32_t sh = static_cast<uint32_t>((NT / 32) * p.ldc * 2), sa = static_cast<uint32_t>((NT / 32) * p.ldc2 * 2);
+        const uint32_t up = static_cast<uint32_t>(p.f * 2);
+#pragma unroll
+        for (int n = 0; n < kEpRows * 32 / NT; ++n, oh += sh, oa += sa) {
+            const int r = rr + n * (NT / 32);
             const float4 gv = lds_f4(ep, r, xg), uv = lds_f4(ep, r, xg + 64);
-            const int64_t row = t.row0 + t.y0 + yr;
-            store_bf16x4(hpre + row * p.ldc + col, gv.x, gv.y, gv.z, gv.w);
-            store_bf16x4(hpre + row * p.ldc + p.f + col, uv.x, uv.y, uv.z, uv.w);
-            store_bf16x4(act + row * p.ldc2 + col, silu_f(gv.x) * uv.x, silu_f(gv.y) * uv.y, silu_f(gv.z) * uv.z,
-                         silu_f(gv.w) * uv.w);
+            view_store_bf16x4(hv, oh, 0, gv.x, gv.y, gv.z, gv.w);
+            view_store_bf16x4(hv, oh, up, uv.x, uv.y, uv.z, uv.w);
+            view_store_bf16x4(av, oa, 0, silu_f(gv.x) * uv.x, silu_f(gv.y) * uv.y, silu_f(gv.z) * uv.z,
+                              silu_f(gv.w) * uv.w);
         }
         return;
     }
-    uint16_t* out = static_cast<uint16_t*>(p.c[g]);
+    const __amdgpu_buffer_rsrc_t ov = tile_view(p.c[g], first, p.ldc, t.x0, t.y_lim);
+    const int rr = threadIdx.x >> 6, x = (threadIdx.x & 63) * 4;
+    const bool ok = x < t.x_lim;
+    uint32_t off = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc + x) * 2) : kOutOfRange;
+    const uint32_t step = static_cast<uint32_t>((NT / 64) * p.ldc * 2);
+    uint32_t off2 = 0, step2 = 0;
+    __amdgpu_buffer_rsrc_t av = ov;
+    if (EPI == kEpiGeluFwd) {
+        av = tile_view(p.c2[g], first, p.ldc2, t.x0, t.y_lim);
+        off2 = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc2 + x) * 2) : kOutOfRange;
+        step2 = static_cast<uint32_t>((NT / 64) * p.ldc2 * 2);
+    }
 #pragma unroll
-    for (int n = 0; n < kEpRows * 64 / NT; ++n) {
-        const int idx = threadIdx.x + n * NT;
-        const int r = idx >> 6, x = (idx & 63) * 4;
-        const int yr = r0 + r;
-        if (yr >= t.y_lim || x >= t.x_lim) continue;
-        const int col = t.x0 + x;
-        const float4 v = lds_f4(ep, r, x);
-        if (MODE == kWgrad) {
-            store_bf16x4(out + static_cast<int64_t>(t.y0 + yr) * p.ldc + col, v.x, v.y, v.z, v.w);
-            continue;
-        }
-        const int64_t row = t.row0 + t.y0 + yr;
+    for (int n = 0; n < kEpRows * 64 / NT; ++n, off += step, off2 += step2) {
+        const float4 v = lds_f4(ep, rr + n * (NT / 64), x);
         if (EPI == kEpiStore) {
-            store_bf16x4(out + row * p.ldc + col, v.x, v.y, v.z, v.w);
+            view_store_bf16x4(ov, off, 0, v.x, v.y, v.z, v.w);
         } else if (EPI == kEpiGeluFwd) {
-            uint16_t* act = static_cast<uint16_t*>(p.c2[g]);
-            store_bf16x4(out + row * p.ldc + col, v.x, v.y, v.z, v.w);
-            store_bf16x4(act + row * p.ldc2 + col, gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w));
+            view_store_bf16x4(ov, off, 0, v.x, v.y, v.z, v.w);
+            view_store_bf16x4(av, off2, 0, gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w));
         } else if (EPI == kEpiGeluBwd) {
             float hv[4];
             unpack_bf16x4(aux.v[n][0], hv);
-            store_bf16x4(out + row * p.ldc + col, v.x * dgelu_f(hv[0]), v.y * dgelu_f(hv[1]), v.z * dgelu_f(hv[2]),
-                         v.w * dgelu_f(hv[3]));
+            view_store_bf16x4(ov, off, 0, v.x * dgelu_f(hv[0]), v.y * dgelu_f(hv[1]), v.z * dgelu_f(hv[2]),
+                              v.w * dgelu_f(hv[3]));
         } else if (EPI == kEpiSwigluBwd) {
             float gv[4], uv[4];
             unpack_bf16x4(aux.v[n][0], gv);
@@ -320,8 +350,8 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
                 dg[e] = dv[e] * uv[e] * dsilu_f(gv[e]);
                 du[e] = dv[e] * silu_f(gv[e]);
             }
-            store_bf16x4(out + row * p.ldc + col, dg[0], dg[1], dg[2], dg[3]);
-            store_bf16x4(out + row * p.ldc + p.f + col, du[0], du[1], du[2], du[3]);
+            view_store_bf16x4(ov, off, 0, dg[0], dg[1], dg[2], dg[3]);
+            view_store_bf16x4(ov, off, static_cast<uint32_t>(p.f * 2), du[0], du[1], du[2], du[3]);
         }
     }
 }
@@ -381,7 +411,6 @@ __device__ __forceinline__ void interleave_reads() {
     }
 }
 
-constexpr uint32_t kOutOfRange = 0x80000000u;             // a buffer offset past every view: reads zero
 
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 

@@ -484,13 +484,15 @@ int check_common(const char* fn, int G, const int32_t* offsets, int64_t rows_cap
     return 0;
 }
 
-// The MFMA kernel reads through buffer views whose byte extent is a 31-bit
-// number: every row buffer and weight must stay below 2 GiB.
+// The MFMA kernel reads and writes through buffer views whose byte extent is a
+// 31-bit number: every row buffer and weight must stay below 2 GiB, and so
+// must kTile rows of the widest matrix (an epilogue's view).
 bool mfma_ok(int dtype, int h, int f, int act, int64_t rows_cap) {
     const int64_t F1 = act == RHP_ACT_SWIGLU ? 2 * static_cast<int64_t>(f) : f;
     const int64_t widest = std::max<int64_t>(h, F1);
     const int64_t limit = int64_t(1) << 31;
-    return dtype == RHP_BF16 && h % 64 == 0 && f % 64 == 0 && rows_cap * widest * 2 < limit && F1 * h * 2 < limit;
+    return dtype == RHP_BF16 && h % 64 == 0 && f % 64 == 0 && rows_cap * widest * 2 < limit && F1 * h * 2 < limit &&
+           kTile * widest * 2 < limit;
 }
 
 }  // namespace
