@@ -303,7 +303,9 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
     t.k_begin = __builtin_amdgcn_readfirstlane(t.k_begin);
     t.k_end = __builtin_amdgcn_readfirstlane(t.k_end);
     const int g = t.g;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // The wave index is uniform: held in a scalar register, the LDS destination
+    // of each direct load is scalar arithmetic (no VALU -> SGPR move per load).
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wx = wave & 1, wy = wave >> 1;
 
     Rsrc rx, ry;

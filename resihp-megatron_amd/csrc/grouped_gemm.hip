@@ -118,7 +118,9 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
     t.k_begin = __builtin_amdgcn_readfirstlane(t.k_begin);
     t.k_end = __builtin_amdgcn_readfirstlane(t.k_end);
     const int g = t.g;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // The wave index is uniform: held in a scalar register, the LDS destination
+    // of each direct load is scalar arithmetic (no VALU -> SGPR move per load).
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wx = wave & 1, wy = wave >> 1;
     constexpr bool kXK = MODE == kFwd;
     constexpr bool kYK = MODE != kWgrad;
@@ -239,20 +241,24 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
     // the loads then reach the address unit at the rate it drains them,
     // instead of every wave queueing a whole tile at once and stalling.
     auto block = [&](const FragSet& f, FragSet& g, uint32_t sx, uint32_t sy, int b, auto load, int n) {
-        static_assert(FY == 2, "read order for two Y fragments");
-        constexpr int order[6] = {4, 0, 5, 1, 2, 3};
+        static_assert(FY == 2 || FY == 4, "read orders for two or four Y fragments");
+        // First the fragments the next block's first MFMAs use: Y 0 and X 0, then the other Y.
+        constexpr int order2[6] = {4, 0, 5, 1, 2, 3};
+        constexpr int order4[8] = {4, 0, 5, 6, 7, 1, 2, 3};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
 #pragma unroll
             for (int r = 0; r < 2; ++r)
-                if (2 * q + r < 6) read_one(g, sx, sy, b, order[2 * q + r]);
-            mfma_range(f, 2 * q, 2 * q + 2);
+                if (2 * q + r < 4 + FY) read_one(g, sx, sy, b, FY == 2 ? order2[2 * q + r] : order4[2 * q + r]);
+            mfma_range(f, FY * q, FY * q + FY);
             if (q < n) load(q);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
+    constexpr int H = kPerWave / 2;   // loads per wave issued with each k16 block
+    static_assert(H <= 4, "at most one load per quarter block");
     using Pending = std::integral_constant<int, kPerWave>;   // one operand tile stays in flight
-    using Prolog = std::integral_constant<int, kPerWave + kPerWave / 2>;   // X1 and half of Y1 in flight
+    using Prolog = std::integral_constant<int, kPerWave + H>;   // X1 and half of Y1 in flight
 
     // A wave whose Y rows all lie past the tile's valid rows only loads its
     // share and joins the barriers.
@@ -262,16 +268,16 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
         issue_x(0, 0);
         issue_y(0, 1);
         issue_x(1, 2);
-        issue_y(1, 3, 0, 2);
+        issue_y(1, 3, 0, H);
         wait_lds(Prolog{});   // step 0 complete
         barrier();
         if (idle) {
             for (int kt = 0; kt < nk; ++kt) {
-                issue_y(kt + 1, (2 * kt + 3) % kSlots, 2, 4);
+                issue_y(kt + 1, (2 * kt + 3) % kSlots, H, 2 * H);
                 issue_x(kt + 2, (2 * kt + 4) % kSlots);
                 wait_lds(Pending{});
                 barrier();
-                issue_y(kt + 2, (2 * kt) % kSlots, 0, 2);
+                issue_y(kt + 2, (2 * kt) % kSlots, 0, H);
             }
         } else {
             read_frags(fa, 0, kT64Bytes, 0);
@@ -281,17 +287,16 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
             // X of step kt + 2 (blocks 1 and 2), and after the barrier the
             // first half of Y of step kt + 2 (block 3).
             int sx = 0, sy = 1, nx = 2, ny = 3, fx = 4;
-            static_assert(kPerWave == 4, "two loads with each k16 block");
             for (int kt = 0; kt < nk; ++kt) {
                 const uint32_t ox = sx * kT64Bytes, oy = sy * kT64Bytes;
-                block(fa, fb, ox, oy, 1, [&](int q) { issue_y(kt + 1, ny, q + 2, q + 3); }, 2);
-                block(fb, fa, ox, oy, 2, [&](int q) { issue_x(kt + 2, fx, q, q + 1); }, 2);
-                block(fa, fb, ox, oy, 3, [&](int q) { issue_x(kt + 2, fx, q + 2, q + 3); }, 2);
+                block(fa, fb, ox, oy, 1, [&](int q) { issue_y(kt + 1, ny, q + H, q + H + 1); }, H);
+                block(fb, fa, ox, oy, 2, [&](int q) { issue_x(kt + 2, fx, q, q + 1); }, H);
+                block(fa, fb, ox, oy, 3, [&](int q) { issue_x(kt + 2, fx, q + H, q + H + 1); }, H);
                 // Steps up to kt + 1 complete (X of step kt + 2 in flight),
                 // every read of slots sx and sy done.
                 wait_lds(Pending{});
                 barrier();
-                block(fb, fa, nx * kT64Bytes, ny * kT64Bytes, 0, [&](int q) { issue_y(kt + 2, sx, q, q + 1); }, 2);
+                block(fb, fa, nx * kT64Bytes, ny * kT64Bytes, 0, [&](int q) { issue_y(kt + 2, sx, q, q + 1); }, H);
                 fx = sy;
                 sx = nx;
                 sy = ny;
