@@ -139,7 +139,13 @@ template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI =
 //
 // A 256 x 256 output tile per workgroup of 8 waves (two per SIMD).  Wave w
 // owns X rows [128 (w % 2), +128) and Y rows [64 (w / 2), +64): 4 x 2
-// accumulators of v_mfma_f32_32x32x16_bf16 (128 registers).
+// accumulators of v_mfma_f32_32x32x16_bf16 (128 registers).  The bf16
+// forward products run the same tile on 4 waves (one per SIMD), wave w owning
+// Y rows [128 (w / 2), +128) in 4 x 4 accumulators (256 registers): a third
+// fewer fragment reads per MFMA.  Under load the GPU runs at its power limit,
+// and LDS reads are a large share of the energy of a step, so the clock rises
+// by more than the single wave per SIMD loses in latency hiding; for the
+// backward products (DGRAD, and WGRAD's transposing reads) the two are even.
 //
 // Operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds:
 // no staging registers and no LDS stores.  One such load moves 64 lanes x 16

@@ -407,7 +407,8 @@ void launch_one(const Job& j, const Params& p, hipStream_t s) {
     if (j.mfma) {
         const unsigned nb = mfma_blocks<MODE, EPI>(p, j.rows_cap);
         if (!nb) return;
-        hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, kWaves>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+        constexpr int nw = MODE == kFwd ? 4 : kWaves;
+        hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, nw>), dim3(nb), dim3(64 * nw), 0, s, p);
         return;
     }
     const unsigned nb = simt_blocks<MODE>(p, j.rows_cap);
