@@ -24,17 +24,19 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kMaxShared = 8;
 constexpr int kChunksPerIter = 4;   // 8-element chunks each lane keeps in flight
 
-// Every row is touched once per kernel, so rows move with non-temporal loads and
-// stores (streaming cache policy): they do not evict what other kernels reuse.
+// Every input row is read once per kernel, so rows are loaded non-temporally
+// (streaming cache policy: they do not evict what other kernels reuse).
+// Results are stored with the default policy: the next kernel reads them
+// (the expert GEMMs read the permuted rows and the row gradients), and
+// measured at the Mixtral shape, default-policy stores of scattered expert
+// rows ran up to 14 % faster than streaming ones.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 nt_load16(const void* p) {
     const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
-__device__ __forceinline__ void nt_store16(void* p, uint4 q) {
-    u32x4_t v;
-    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
-    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(p));
+__device__ __forceinline__ void store16(void* p, uint4 q) {
+    *reinterpret_cast<uint4*>(p) = q;
 }
 
 // 8 consecutive elements of type S, held as compute type A.
@@ -55,7 +57,7 @@ template <> struct Vec8<bf16, float> {
         q.y = pack_bf16x2(v[2], v[3]);
         q.z = pack_bf16x2(v[4], v[5]);
         q.w = pack_bf16x2(v[6], v[7]);
-        nt_store16(p, q);
+        store16(p, q);
     }
 };
 template <> struct Vec8<float, float> {
@@ -93,7 +95,7 @@ template <class S> struct Raw8 {
     }
     __device__ __forceinline__ void store(S* p) const {
 #pragma unroll
-        for (int i = 0; i < kWords; ++i) nt_store16(reinterpret_cast<uint4*>(p) + i, w[i]);
+        for (int i = 0; i < kWords; ++i) store16(reinterpret_cast<uint4*>(p) + i, w[i]);
     }
 };
 
@@ -116,18 +118,20 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(const S* __restrict__
         any |= rows[j] >= 0;
     }
     if (!any) return;
+    // 128 bytes per lane per pass: a whole 4096-wide bf16 row in one pass.
+    constexpr int U = 128 / (8 * static_cast<int>(sizeof(S)));
     const int nch = h / 8;
     const S* src = x + t * h;
-    for (int c0 = lane; c0 < nch; c0 += 64 * kChunksPerIter) {
-        Raw8<S> v[kChunksPerIter];
+    for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+        Raw8<S> v[U];
 #pragma unroll
-        for (int u = 0; u < kChunksPerIter; ++u)
+        for (int u = 0; u < U; ++u)
             if (c0 + u * 64 < nch) v[u].load(src + (c0 + u * 64) * 8);
         for (int j = 0; j < k; ++j) {
             if (rows[j] < 0) continue;
             S* dst = xp + static_cast<int64_t>(rows[j]) * h;
 #pragma unroll
-            for (int u = 0; u < kChunksPerIter; ++u)
+            for (int u = 0; u < U; ++u)
                 if (c0 + u * 64 < nch) v[u].store(dst + (c0 + u * 64) * 8);
         }
     }
@@ -309,10 +313,302 @@ __global__ __launch_bounds__(kThreads) void token_bwd_kernel(const S* __restrict
     }
 }
 
+// ----------------------------------------------------------------------------- batched bf16 row kernels
+//
+// bfloat16 rows are the layer's production path.  A wave owns one token and
+// moves its rows in passes of U 16-byte chunks per lane; every load of a pass
+// (the token's own row, its k expert rows, its shared-expert rows) is issued
+// before the first of them is used, so a wave keeps rows x U KB in flight
+// rather than one row chunk per memory round trip.  KM and SM bound k and
+// the shared-expert count at compile time; slots past the runtime k (or S) are
+// skipped by wave-uniform branches, and every array is indexed by unrolled
+// loop counters, so nothing goes to scratch memory.  The arithmetic is that of
+// the generic kernels above, operation for operation and in the same order.
+
+__device__ __forceinline__ void unpack_bf16x8(uint4 q, float* v) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+__device__ __forceinline__ uint4 pack_bf16x8(const float* v) {
+    return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                      pack_bf16x2(v[6], v[7]));
+}
+
+// Rank of each slot in ascending expert id (ids of one token are distinct,
+// equal ids rank by slot), then the slot holding each rank, all by selects.
+template <int KM>
+__device__ __forceinline__ void ascending_slots_static(const int32_t* tk, int k, int* order) {
+    int rank[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        int r = 0;
+#pragma unroll
+        for (int i = 0; i < KM; ++i)
+            if (i < k) r += (tk[i] < tk[j]) || (tk[i] == tk[j] && i < j);
+        rank[j] = r;
+    }
+#pragma unroll
+    for (int r = 0; r < KM; ++r) {
+        int sel = 0;
+#pragma unroll
+        for (int j = 0; j < KM; ++j) sel = (j < k && rank[j] == r) ? j : sel;
+        order[r] = sel;
+    }
+}
+
+template <int KM, int SM, int U>
+__global__ __launch_bounds__(kThreads) void combine_bf16_kernel(const bf16* __restrict__ y, const bf16* __restrict__ x,
+                                                                const float* __restrict__ gates,
+                                                                const int32_t* __restrict__ topi,
+                                                                const int32_t* __restrict__ pair_row,
+                                                                SharedPtrs shared, int n_shared, int64_t T, int h,
+                                                                int k, bf16* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (t >= T) return;
+    int32_t tk[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) tk[j] = j < k ? topi[t * k + j] : 0;
+    int order[KM];
+    ascending_slots_static<KM>(tk, k, order);
+    int32_t row_of[KM];
+    float gate_of[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        row_of[j] = j < k ? pair_row[t * k + j] : -1;
+        gate_of[j] = j < k ? gates[t * k + j] : 0.0f;
+    }
+    // Rank r: the slot with the r-th smallest expert id.
+    int32_t rows[KM];
+    float g[KM];
+#pragma unroll
+    for (int r = 0; r < KM; ++r) {
+        int32_t rw = -1;
+        float gv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KM; ++j)
+            if (order[r] == j) {
+                rw = row_of[j];
+                gv = gate_of[j];
+            }
+        rows[r] = r < k ? rw : -1;
+        g[r] = gv;
+    }
+    const int nch = h / 8;
+    const bf16* xrow = x + t * h;
+    bf16* orow = out + t * h;
+    for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+        uint4 yv[KM][U], xv[U], sv[SM > 0 ? SM : 1][U];
+#pragma unroll
+        for (int r = 0; r < KM; ++r)
+            if (rows[r] >= 0) {
+                const bf16* src = y + static_cast<int64_t>(rows[r]) * h;
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (c0 + u * 64 < nch) yv[r][u] = nt_load16(src + (c0 + u * 64) * 8);
+            }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (c0 + u * 64 < nch) xv[u] = nt_load16(xrow + (c0 + u * 64) * 8);
+#pragma unroll
+        for (int s = 0; s < SM; ++s)
+            if (s < n_shared) {
+                const bf16* src = static_cast<const bf16*>(shared.p[s]) + t * h;
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (c0 + u * 64 < nch) sv[s][u] = nt_load16(src + (c0 + u * 64) * 8);
+            }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + u * 64 >= nch) continue;
+            float acc[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+            for (int r = 0; r < KM; ++r)
+                if (rows[r] >= 0) {
+                    float v[8];
+                    unpack_bf16x8(yv[r][u], v);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[i] = acc[i] + g[r] * v[i];
+                }
+            float o[8];
+            unpack_bf16x8(xv[u], o);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = o[i] + acc[i];
+#pragma unroll
+            for (int s = 0; s < SM; ++s)
+                if (s < n_shared) {
+                    float v[8];
+                    unpack_bf16x8(sv[s][u], v);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = o[i] + v[i];
+                }
+            store16(orow + (c0 + u * 64) * 8, pack_bf16x8(o));
+        }
+    }
+}
+
+template <int KM, int U>
+__global__ __launch_bounds__(kThreads) void combine_bwd_bf16_kernel(const bf16* __restrict__ dout,
+                                                                    const bf16* __restrict__ y,
+                                                                    const float* __restrict__ gates,
+                                                                    const int32_t* __restrict__ pair_row, int64_t T,
+                                                                    int h, int k, bf16* __restrict__ dy,
+                                                                    float* __restrict__ dgates) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (t >= T) return;
+    int32_t rows[KM];
+    float g[KM], dot[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        rows[j] = j < k ? pair_row[t * k + j] : -1;
+        g[j] = j < k ? gates[t * k + j] : 0.0f;
+        dot[j] = 0.0f;
+    }
+    const int nch = h / 8;
+    const bf16* drow = dout + t * h;
+    for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+        uint4 dv[U], yv[KM][U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (c0 + u * 64 < nch) dv[u] = nt_load16(drow + (c0 + u * 64) * 8);
+#pragma unroll
+        for (int j = 0; j < KM; ++j)
+            if (rows[j] >= 0) {
+                const bf16* src = y + static_cast<int64_t>(rows[j]) * h;
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (c0 + u * 64 < nch) yv[j][u] = nt_load16(src + (c0 + u * 64) * 8);
+            }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + u * 64 >= nch) continue;
+            float d[8];
+            unpack_bf16x8(dv[u], d);
+#pragma unroll
+            for (int j = 0; j < KM; ++j)
+                if (rows[j] >= 0) {
+                    float v[8], o[8];
+                    unpack_bf16x8(yv[j][u], v);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        o[i] = g[j] * d[i];
+                        dot[j] = dot[j] + d[i] * v[i];
+                    }
+                    store16(dy + static_cast<int64_t>(rows[j]) * h + (c0 + u * 64) * 8, pack_bf16x8(o));
+                }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        if (j >= k) continue;
+        float v = dot[j];
+        for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
+        if (lane == 0) dgates[t * k + j] = v;
+    }
+}
+
+template <int KM, int SM, int U>
+__global__ __launch_bounds__(kThreads) void token_bwd_bf16_kernel(const bf16* __restrict__ dout,
+                                                                  const bf16* __restrict__ dxp,
+                                                                  const int32_t* __restrict__ pair_row,
+                                                                  const float* __restrict__ dl,
+                                                                  const int32_t* __restrict__ topi,
+                                                                  const float* __restrict__ router_w,
+                                                                  SharedPtrs shared, int n_shared, int64_t T, int h,
+                                                                  int E, int k, bf16* __restrict__ dx) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (t >= T) return;
+    int32_t rows[KM], ex[KM];
+    float d[KM];
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+        rows[j] = j < k ? pair_row[t * k + j] : -1;
+        const int32_t e = j < k ? topi[t * k + j] : -1;
+        ex[j] = (dl != nullptr && e >= 0 && e < E) ? e : -1;   // -1: no router row (dropped id or no router term)
+        d[j] = (dl != nullptr && j < k) ? dl[t * k + j] : 0.0f;
+    }
+    const int nch = h / 8;
+    const bf16* drow = dout + t * h;
+    for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+        uint4 dv[U], xv[KM][U], sv[SM > 0 ? SM : 1][U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (c0 + u * 64 < nch) dv[u] = nt_load16(drow + (c0 + u * 64) * 8);
+#pragma unroll
+        for (int j = 0; j < KM; ++j)
+            if (rows[j] >= 0) {
+                const bf16* src = dxp + static_cast<int64_t>(rows[j]) * h;
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (c0 + u * 64 < nch) xv[j][u] = nt_load16(src + (c0 + u * 64) * 8);
+            }
+#pragma unroll
+        for (int s = 0; s < SM; ++s)
+            if (s < n_shared) {
+                const bf16* src = static_cast<const bf16*>(shared.p[s]) + t * h;
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (c0 + u * 64 < nch) sv[s][u] = nt_load16(src + (c0 + u * 64) * 8);
+            }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + u * 64 >= nch) continue;
+            const int c = c0 + u * 64;
+            float acc[8];
+            unpack_bf16x8(dv[u], acc);
+#pragma unroll
+            for (int j = 0; j < KM; ++j)
+                if (rows[j] >= 0) {
+                    float v[8];
+                    unpack_bf16x8(xv[j][u], v);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+                }
+            // Router rows are small and stay in L2: loaded here, per chunk.
+            float wv[KM][8];
+#pragma unroll
+            for (int j = 0; j < KM; ++j)
+                if (ex[j] >= 0) Vec8<float, float>::load(router_w + static_cast<int64_t>(ex[j]) * h + c * 8, wv[j]);
+#pragma unroll
+            for (int j = 0; j < KM; ++j)
+                if (ex[j] >= 0) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[i] = acc[i] + d[j] * wv[j][i];
+                }
+#pragma unroll
+            for (int s = 0; s < SM; ++s)
+                if (s < n_shared) {
+                    float v[8];
+                    unpack_bf16x8(sv[s][u], v);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+                }
+            store16(dx + t * h + c * 8, pack_bf16x8(acc));
+        }
+    }
+}
+
+// Batched bf16 variants by (k, shared experts); larger k or more shared
+// experts fall back to the generic kernels.  Variants without shared experts
+// hold no registers for them.
+enum class RowVariant { kSmall, kSmallShared, kWide, kWideShared, kGeneric };
+inline RowVariant row_variant(int k, int n_shared) {
+    if (k <= 2) return n_shared == 0 ? RowVariant::kSmall : n_shared <= 2 ? RowVariant::kSmallShared : RowVariant::kGeneric;
+    if (k <= 8) return n_shared == 0 ? RowVariant::kWide : n_shared <= 2 ? RowVariant::kWideShared : RowVariant::kGeneric;
+    return RowVariant::kGeneric;
+}
+
 // ----------------------------------------------------------------------------- router weight gradient
 
-constexpr int kWgradRows = 256;   // rows of one expert segment summed by one block
-constexpr int kWgradCols = 512;   // columns per block (64 lanes x 8)
+constexpr int kWgradRows = 64;   // rows of one expert segment summed by one wave
 
 __device__ __forceinline__ int pieces_of(int n) { return (n + kWgradRows - 1) / kWgradRows; }
 
@@ -332,50 +628,106 @@ __device__ __forceinline__ bool find_piece(const int32_t* offsets, int E, int b,
     return false;
 }
 
+// Raw chunk -> 8 values of the compute type.
+__device__ __forceinline__ void raw_to_acc(const Raw8<bf16>& q, float* v) {
+    const uint32_t w[4] = {q.w[0].x, q.w[0].y, q.w[0].z, q.w[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+__device__ __forceinline__ void raw_to_acc(const Raw8<float>& q, float* v) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        v[4 * i] = __uint_as_float(q.w[i].x);
+        v[4 * i + 1] = __uint_as_float(q.w[i].y);
+        v[4 * i + 2] = __uint_as_float(q.w[i].z);
+        v[4 * i + 3] = __uint_as_float(q.w[i].w);
+    }
+}
+__device__ __forceinline__ void raw_to_acc(const Raw8<double>& q, double* v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __hiloint2double(static_cast<int>(q.w[i].y), static_cast<int>(q.w[i].x));
+        v[2 * i + 1] = __hiloint2double(static_cast<int>(q.w[i].w), static_cast<int>(q.w[i].z));
+    }
+}
+
+// One wave sums the 64 rows of a piece for 512 columns (8 per lane), rows in
+// ascending order; the token rows of a batch of rows are all in flight before
+// the first is used (64 registers of raw row data per lane).
 template <class S, class R>
 __global__ __launch_bounds__(64) void router_wgrad_partial_kernel(const R* __restrict__ dl,
                                                                   const int32_t* __restrict__ perm,
                                                                   const int32_t* __restrict__ offsets,
                                                                   const S* __restrict__ x, int h, int E, int k,
                                                                   R* __restrict__ partial) {
+    constexpr int kBatch = 32 / static_cast<int>(sizeof(S));   // rows per batch: 16 bf16, 8 f32, 4 f64
+    using A = typename Elem<S>::acc;
     int e, r0, r1;
     if (!find_piece(offsets, E, blockIdx.x, &e, &r0, &r1)) return;
     const int c = blockIdx.y * 64 + threadIdx.x;   // 8-element column chunk
-    if (c * 8 >= h) return;
+    const bool live = c * 8 < h;
     R acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = R(0);
-    for (int r = r0; r < r1; ++r) {
-        const int p = perm[r];
-        const R d = dl[p];
-        typename Elem<S>::acc v[8];
-        Vec8<S, typename Elem<S>::acc>::load(x + static_cast<int64_t>(p / k) * h + c * 8, v);
+    for (int rb = r0; rb < r1; rb += kBatch) {
+        Raw8<S> v[kBatch];
+        R d[kBatch];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = acc[i] + d * static_cast<R>(v[i]);
+        for (int q = 0; q < kBatch; ++q) {
+            if (rb + q < r1) {
+                const int p = perm[rb + q];
+                d[q] = dl[p];
+                if (live) v[q].load(x + static_cast<int64_t>(p / k) * h + c * 8);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+            if (rb + q < r1) {
+                A a[8];
+                raw_to_acc(v[q], a);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[i] = acc[i] + d[q] * static_cast<R>(a[i]);
+            }
+        }
     }
-    Vec8<R, R>::store(partial + static_cast<int64_t>(blockIdx.x) * h + c * 8, acc);
+    if (live) Vec8<R, R>::store(partial + static_cast<int64_t>(blockIdx.x) * h + c * 8, acc);
 }
 
+// Sums an expert's pieces in ascending order; 4 columns per lane and 8 pieces
+// in flight.
 template <class R>
 __global__ __launch_bounds__(64) void router_wgrad_reduce_kernel(const R* __restrict__ partial,
                                                                  const int32_t* __restrict__ offsets, int h, int E,
                                                                  R* __restrict__ dw) {
+    constexpr int kBatch = 8;
     const int e = blockIdx.x;
-    const int c = blockIdx.y * 64 + threadIdx.x;
-    if (c * 8 >= h) return;
+    const int c = (blockIdx.y * 64 + threadIdx.x) * 4;
+    if (c >= h) return;
     int first = 0;
     for (int i = 0; i < e; ++i) first += pieces_of(offsets[i + 1] - offsets[i]);
     const int np = pieces_of(offsets[e + 1] - offsets[e]);
-    R acc[8];
+    R acc[4] = {R(0), R(0), R(0), R(0)};
+    for (int q0 = 0; q0 < np; q0 += kBatch) {
+        R v[kBatch][4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = R(0);
-    for (int q = 0; q < np; ++q) {
-        R v[8];
-        Vec8<R, R>::load(partial + static_cast<int64_t>(first + q) * h + c * 8, v);
+        for (int q = 0; q < kBatch; ++q)
+            if (q0 + q < np) {
+                const R* src = partial + static_cast<int64_t>(first + q0 + q) * h + c;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+                for (int i = 0; i < 4; ++i) v[q][i] = src[i];
+            }
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q)
+            if (q0 + q < np) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] = acc[i] + v[q][i];
+            }
     }
-    Vec8<R, R>::store(dw + static_cast<int64_t>(e) * h + c * 8, acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dw[static_cast<int64_t>(e) * h + c + i] = acc[i];
 }
 
 int64_t wgrad_pieces_bound(int64_t T, int k, int E) { return (T * k + kWgradRows - 1) / kWgradRows + E; }
@@ -437,11 +789,33 @@ extern "C" int rhp_combine(const void* y, const void* x, const void* gates, int 
                            n_shared, T, h, k, static_cast<double*>(out));
     } else {
         RHP_REQUIRE(g_dtype == RHP_F32, "rhp_combine: float32 / bfloat16 rows need float32 gates");
-        if (dtype == RHP_BF16)
-            hipLaunchKernelGGL((combine_kernel<bf16, float>), grid, block, 0, stream, static_cast<const bf16*>(y),
-                               static_cast<const bf16*>(x), static_cast<const float*>(gates), topi, pair_row, sp,
-                               n_shared, T, h, k, static_cast<bf16*>(out));
-        else
+        if (dtype == RHP_BF16) {
+            const bf16* yb = static_cast<const bf16*>(y);
+            const bf16* xb = static_cast<const bf16*>(x);
+            const float* gf = static_cast<const float*>(gates);
+            bf16* ob = static_cast<bf16*>(out);
+            switch (row_variant(k, n_shared)) {
+                case RowVariant::kSmall:
+                    hipLaunchKernelGGL((combine_bf16_kernel<2, 0, 8>), grid, block, 0, stream, yb, xb, gf, topi,
+                                       pair_row, sp, n_shared, T, h, k, ob);
+                    break;
+                case RowVariant::kSmallShared:
+                    hipLaunchKernelGGL((combine_bf16_kernel<2, 2, 4>), grid, block, 0, stream, yb, xb, gf, topi,
+                                       pair_row, sp, n_shared, T, h, k, ob);
+                    break;
+                case RowVariant::kWide:
+                    hipLaunchKernelGGL((combine_bf16_kernel<8, 0, 2>), grid, block, 0, stream, yb, xb, gf, topi,
+                                       pair_row, sp, n_shared, T, h, k, ob);
+                    break;
+                case RowVariant::kWideShared:
+                    hipLaunchKernelGGL((combine_bf16_kernel<8, 2, 2>), grid, block, 0, stream, yb, xb, gf, topi,
+                                       pair_row, sp, n_shared, T, h, k, ob);
+                    break;
+                default:
+                    hipLaunchKernelGGL((combine_kernel<bf16, float>), grid, block, 0, stream, yb, xb, gf, topi,
+                                       pair_row, sp, n_shared, T, h, k, ob);
+            }
+        } else
             hipLaunchKernelGGL((combine_kernel<float, float>), grid, block, 0, stream, static_cast<const float*>(y),
                                static_cast<const float*>(x), static_cast<const float*>(gates), topi, pair_row, sp,
                                n_shared, T, h, k, static_cast<float*>(out));
@@ -467,12 +841,26 @@ extern "C" int rhp_combine_bwd(const void* dout, const void* y, const void* gate
                            static_cast<double*>(dgates));
     } else {
         RHP_REQUIRE(g_dtype == RHP_F32, "rhp_combine_bwd: float32 / bfloat16 rows need float32 gates");
-        if (dtype == RHP_BF16)
-            hipLaunchKernelGGL((combine_bwd_kernel<bf16, float>), grid, block, 0, stream,
-                               static_cast<const bf16*>(dout), static_cast<const bf16*>(y),
-                               static_cast<const float*>(gates), pair_row, T, h, k, static_cast<bf16*>(dy),
-                               static_cast<float*>(dgates));
-        else
+        if (dtype == RHP_BF16) {
+            const bf16* db = static_cast<const bf16*>(dout);
+            const bf16* yb = static_cast<const bf16*>(y);
+            const float* gf = static_cast<const float*>(gates);
+            bf16* dyb = static_cast<bf16*>(dy);
+            float* dg = static_cast<float*>(dgates);
+            switch (row_variant(k, 0)) {
+                case RowVariant::kSmall:
+                    hipLaunchKernelGGL((combine_bwd_bf16_kernel<2, 8>), grid, block, 0, stream, db, yb, gf, pair_row,
+                                       T, h, k, dyb, dg);
+                    break;
+                case RowVariant::kWide:
+                    hipLaunchKernelGGL((combine_bwd_bf16_kernel<8, 2>), grid, block, 0, stream, db, yb, gf, pair_row,
+                                       T, h, k, dyb, dg);
+                    break;
+                default:
+                    hipLaunchKernelGGL((combine_bwd_kernel<bf16, float>), grid, block, 0, stream, db, yb, gf,
+                                       pair_row, T, h, k, dyb, dg);
+            }
+        } else
             hipLaunchKernelGGL((combine_bwd_kernel<float, float>), grid, block, 0, stream,
                                static_cast<const float*>(dout), static_cast<const float*>(y),
                                static_cast<const float*>(gates), pair_row, T, h, k, static_cast<float*>(dy),
@@ -506,11 +894,34 @@ extern "C" int rhp_token_bwd(const void* dout, const void* dxp, const int32_t* p
                            static_cast<const double*>(router_w), sp, n_shared, T, h, E, k, static_cast<double*>(dx));
     } else {
         RHP_REQUIRE(r_dtype == RHP_F32, "rhp_token_bwd: float32 / bfloat16 rows need a float32 router");
-        if (dtype == RHP_BF16)
-            hipLaunchKernelGGL((token_bwd_kernel<bf16, float>), grid, block, 0, stream, static_cast<const bf16*>(dout),
-                               static_cast<const bf16*>(dxp), pair_row, static_cast<const float*>(dlogits_sel), topi,
-                               static_cast<const float*>(router_w), sp, n_shared, T, h, E, k, static_cast<bf16*>(dx));
-        else
+        if (dtype == RHP_BF16) {
+            const bf16* db = static_cast<const bf16*>(dout);
+            const bf16* xb = static_cast<const bf16*>(dxp);
+            const float* dlf = static_cast<const float*>(dlogits_sel);
+            const float* wf = static_cast<const float*>(router_w);
+            bf16* dxb = static_cast<bf16*>(dx);
+            switch (row_variant(k, n_shared)) {
+                case RowVariant::kSmall:
+                    hipLaunchKernelGGL((token_bwd_bf16_kernel<2, 0, 4>), grid, block, 0, stream, db, xb, pair_row,
+                                       dlf, topi, wf, sp, n_shared, T, h, E, k, dxb);
+                    break;
+                case RowVariant::kSmallShared:
+                    hipLaunchKernelGGL((token_bwd_bf16_kernel<2, 2, 4>), grid, block, 0, stream, db, xb, pair_row,
+                                       dlf, topi, wf, sp, n_shared, T, h, E, k, dxb);
+                    break;
+                case RowVariant::kWide:
+                    hipLaunchKernelGGL((token_bwd_bf16_kernel<8, 0, 2>), grid, block, 0, stream, db, xb, pair_row,
+                                       dlf, topi, wf, sp, n_shared, T, h, E, k, dxb);
+                    break;
+                case RowVariant::kWideShared:
+                    hipLaunchKernelGGL((token_bwd_bf16_kernel<8, 2, 2>), grid, block, 0, stream, db, xb, pair_row,
+                                       dlf, topi, wf, sp, n_shared, T, h, E, k, dxb);
+                    break;
+                default:
+                    hipLaunchKernelGGL((token_bwd_kernel<bf16, float>), grid, block, 0, stream, db, xb, pair_row, dlf,
+                                       topi, wf, sp, n_shared, T, h, E, k, dxb);
+            }
+        } else
             hipLaunchKernelGGL((token_bwd_kernel<float, float>), grid, block, 0, stream,
                                static_cast<const float*>(dout), static_cast<const float*>(dxp), pair_row,
                                static_cast<const float*>(dlogits_sel), topi, static_cast<const float*>(router_w), sp,
@@ -536,14 +947,15 @@ extern "C" int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, co
                     (workspace == nullptr ? workspace_bytes == 0 : aligned16(workspace)),
                 "rhp_router_wgrad: null or unaligned pointer");
     const int64_t pieces = wgrad_pieces_bound(T, k, E);
-    const unsigned col_blocks = static_cast<unsigned>((h / 8 + 63) / 64);
+    const unsigned col_blocks = static_cast<unsigned>((h / 8 + 63) / 64);      // partial: 8 columns per lane
+    const unsigned red_blocks = static_cast<unsigned>((h / 4 + 63) / 64);      // reduce: 4 columns per lane
     if (x_dtype == RHP_F64) {
         RHP_REQUIRE(r_dtype == RHP_F64, "rhp_router_wgrad: float64 x needs a float64 router");
         hipLaunchKernelGGL((router_wgrad_partial_kernel<double, double>), dim3(pieces, col_blocks), dim3(64), 0, stream,
                            static_cast<const double*>(dlogits_sel), perm, offsets, static_cast<const double*>(x), h,
                            E, k, static_cast<double*>(workspace));
         if (int rc = check_launch("router_wgrad_partial_kernel")) return rc;
-        hipLaunchKernelGGL(router_wgrad_reduce_kernel<double>, dim3(E, col_blocks), dim3(64), 0, stream,
+        hipLaunchKernelGGL(router_wgrad_reduce_kernel<double>, dim3(E, red_blocks), dim3(64), 0, stream,
                            static_cast<const double*>(workspace), offsets, h, E, static_cast<double*>(dw));
     } else {
         RHP_REQUIRE(r_dtype == RHP_F32, "rhp_router_wgrad: float32 / bfloat16 x needs a float32 router");
@@ -556,7 +968,7 @@ extern "C" int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, co
                                stream, static_cast<const float*>(dlogits_sel), perm, offsets,
                                static_cast<const float*>(x), h, E, k, static_cast<float*>(workspace));
         if (int rc = check_launch("router_wgrad_partial_kernel")) return rc;
-        hipLaunchKernelGGL(router_wgrad_reduce_kernel<float>, dim3(E, col_blocks), dim3(64), 0, stream,
+        hipLaunchKernelGGL(router_wgrad_reduce_kernel<float>, dim3(E, red_blocks), dim3(64), 0, stream,
                            static_cast<const float*>(workspace), offsets, h, E, static_cast<float*>(dw));
     }
     return check_launch("router_wgrad_reduce_kernel");

@@ -70,6 +70,84 @@ template <class AT> __device__ __forceinline__ bool better(AT va, int ia, AT vb,
     return va > vb || (va == vb && ia < ib);
 }
 
+// Selection and gates of a block's tb tokens (first token t_block) from their
+// logits lg[tb][E] in LDS; sel[tb][k] is LDS scratch.  nthreads: block size.
+template <class AT>
+__device__ __forceinline__ void select_and_gate(const AT* lg, int* sel, int64_t t_block, int tb, int nthreads,
+                                                int64_t T, int E, int k, int score, int normalize, AT scale,
+                                                const AT* __restrict__ bias, int32_t* __restrict__ topi,
+                                                AT* __restrict__ gates) {
+    const int tid = threadIdx.x;
+    // Top-k by wavefront shuffles.  A group of lpt lanes handles one
+    // token; each lane owns experts lane_in_group + c * lpt.
+    int lpt = 1;
+    while (lpt < E && lpt < 64) lpt <<= 1;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int gl = lane & (lpt - 1);
+    const int groups_per_block = (nthreads / 64) * (64 / lpt);
+    const int my_group = wave * (64 / lpt) + lane / lpt;
+    const int cand = (E + lpt - 1) / lpt;
+    for (int tl0 = 0; tl0 < tb; tl0 += groups_per_block) {
+        const int tl = tl0 + my_group;
+        const bool active = tl < tb && (t_block + tl) < T;
+        uint32_t taken = 0;   // bit c: candidate c already chosen (cand <= 16 since E <= 1024)
+        for (int j = 0; j < k; ++j) {
+            AT bv = neg_inf<AT>();
+            int bi = 0x7fffffff;
+            if (active) {
+                for (int c = 0; c < cand; ++c) {
+                    const int e = gl + c * lpt;
+                    if (e >= E || ((taken >> c) & 1u)) continue;
+                    AT v = lg[static_cast<size_t>(tl) * E + e];
+                    if (score == RHP_SCORE_SIGMOID) v = rhp_sigmoid(v);
+                    if (bias) v = v + bias[e];
+                    if (v != v) v = neg_inf<AT>();
+                    if (better(v, e, bv, bi)) { bv = v; bi = e; }
+                }
+            }
+            for (int o = lpt >> 1; o >= 1; o >>= 1) {
+                AT ov = __shfl_xor(bv, o, 64);
+                int oi = __shfl_xor(bi, o, 64);
+                if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+            }
+            if (active) {
+                if ((bi & (lpt - 1)) == gl) taken |= 1u << (bi / lpt);
+                if (gl == 0) sel[tl * k + j] = bi;
+            }
+        }
+    }
+    __syncthreads();
+
+    // Gates, one thread per token, sums in slot order.
+    for (int tl = tid; tl < tb; tl += nthreads) {
+        const int64_t t = t_block + tl;
+        if (t >= T) continue;
+        const AT* l = lg + static_cast<size_t>(tl) * E;
+        const int* s = sel + tl * k;
+        AT g[kMaxTopK];
+        AT sum = AT(0);
+        if (score == RHP_SCORE_SOFTMAX) {
+            AT m = l[s[0]];
+            for (int j = 1; j < k; ++j) m = (l[s[j]] > m) ? l[s[j]] : m;
+            for (int j = 0; j < k; ++j) {
+                g[j] = rhp_exp_t(l[s[j]] - m);
+                sum = (j == 0) ? g[j] : sum + g[j];
+            }
+            for (int j = 0; j < k; ++j) g[j] = (g[j] / sum) * scale;
+        } else {
+            for (int j = 0; j < k; ++j) {
+                g[j] = rhp_sigmoid(l[s[j]]);
+                sum = (j == 0) ? g[j] : sum + g[j];
+            }
+            for (int j = 0; j < k; ++j) g[j] = (normalize ? g[j] / sum : g[j]) * scale;
+        }
+        for (int j = 0; j < k; ++j) {
+            topi[t * k + j] = s[j];
+            gates[t * k + j] = g[j];
+        }
+    }
+}
+
 template <class XT, class AT>
 __global__ __launch_bounds__(kThreads) void route_kernel(const XT* __restrict__ x, const AT* __restrict__ w,
                                                          const AT* __restrict__ bias, int64_t T, int h, int E, int k,
@@ -139,74 +217,117 @@ __global__ __launch_bounds__(kThreads) void route_kernel(const XT* __restrict__ 
     }
     __syncthreads();
 
-    // Phase 3: top-k by wavefront shuffles.  A group of lpt lanes handles one
-    // token; each lane owns experts lane_in_group + c * lpt.
-    int lpt = 1;
-    while (lpt < E && lpt < 64) lpt <<= 1;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int gl = lane & (lpt - 1);
-    const int groups_per_block = (kThreads / 64) * (64 / lpt);
-    const int my_group = wave * (64 / lpt) + lane / lpt;
-    const int cand = (E + lpt - 1) / lpt;
-    for (int tl0 = 0; tl0 < rs.tb; tl0 += groups_per_block) {
-        const int tl = tl0 + my_group;
-        const bool active = tl < rs.tb && (t_block + tl) < T;
-        uint32_t taken = 0;   // bit c: candidate c already chosen (cand <= 16 since E <= 1024)
-        for (int j = 0; j < k; ++j) {
-            AT bv = neg_inf<AT>();
-            int bi = 0x7fffffff;
-            if (active) {
-                for (int c = 0; c < cand; ++c) {
-                    const int e = gl + c * lpt;
-                    if (e >= E || ((taken >> c) & 1u)) continue;
-                    AT v = lg[static_cast<size_t>(tl) * E + e];
-                    if (score == RHP_SCORE_SIGMOID) v = rhp_sigmoid(v);
-                    if (bias) v = v + bias[e];
-                    if (v != v) v = neg_inf<AT>();
-                    if (better(v, e, bv, bi)) { bv = v; bi = e; }
+    select_and_gate<AT>(lg, sel, t_block, rs.tb, kThreads, T, E, k, score, normalize, scale, bias, topi, gates);
+}
+
+// Router logits of bfloat16 tokens, the production path.  One lane per token
+// (64 tokens per block): every lane of a wave runs the same chains, so the
+// router weights it multiplies by are wave-uniform and come through scalar
+// loads, while each lane streams its own token row in whole 128-byte lines.
+// Work is split over the block's waves one of two ways:
+//   segment mode (few experts): wave w takes segments w, w + nw, ... of each
+//     group of EC experts; the segment chains go to LDS and are then added
+//     left to right;
+//   expert mode (many experts): wave w takes expert groups w, w + nw, ... and
+//     runs their segments in order, adding each finished chain to the running
+//     total in registers.
+// Either way every logit is the same fma chains summed in the same order as
+// route_kernel's (and the oracle's), bit for bit.  Experts past E in the last
+// group are computed on a clamped row and discarded.
+constexpr int kRtTokens = 64;
+constexpr int kRtMaxWaves = 16;
+
+// Chains of EC experts (rows wr) over one segment [i0, i0 + seg) of a token row.
+template <int EC>
+__device__ __forceinline__ void segment_chains(const bf16* xr, const float* const* wr, int i0, int seg, float* acc) {
+#pragma unroll
+    for (int b = 0; b < EC; ++b) acc[b] = 0.0f;
+    for (int g = 0; g < seg; g += 64) {
+        uint4 xv[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            if (g + c * 8 < seg) xv[c] = *reinterpret_cast<const uint4*>(xr + i0 + g + c * 8);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            if (g + c * 8 >= seg) break;
+            const uint32_t q[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+            float xf[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xf[2 * i] = __uint_as_float(q[i] << 16);
+                xf[2 * i + 1] = __uint_as_float(q[i] & 0xffff0000u);
+            }
+            const int i = i0 + g + c * 8;
+#pragma unroll
+            for (int ii = 0; ii < 8; ++ii)
+#pragma unroll
+                for (int b = 0; b < EC; ++b) acc[b] = fma_t(xf[ii], wr[b][i + ii], acc[b]);
+        }
+    }
+}
+
+template <int EC>
+__global__ __launch_bounds__(64 * kRtMaxWaves) void route_bf16_kernel(const bf16* __restrict__ x,
+                                                                    const float* __restrict__ w,
+                                                                    const float* __restrict__ bias, int64_t T, int h,
+                                                                    int E, int k, int score, int normalize, float scale,
+                                                                    int seg, int S, int expert_mode,
+                                                                    float* __restrict__ logits,
+                                                                    int32_t* __restrict__ topi,
+                                                                    float* __restrict__ gates) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    float* lg = reinterpret_cast<float*>(smem_raw);                                 // [64][E]
+    int* sel = reinterpret_cast<int*>(lg + static_cast<size_t>(kRtTokens) * E);     // [64][k]
+    float* part = reinterpret_cast<float*>(sel + kRtTokens * k);                    // [S][EC][64], segment mode
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
+    const int64_t t_block = static_cast<int64_t>(blockIdx.x) * kRtTokens;
+    const int64_t t = t_block + lane < T ? t_block + lane : t_block;   // lanes past T repeat a valid row
+    const bf16* xr = x + t * h;
+    if (expert_mode) {
+        for (int e0 = wave * EC; e0 < E; e0 += nw * EC) {
+            const float* wr[EC];
+#pragma unroll
+            for (int b = 0; b < EC; ++b) wr[b] = w + static_cast<int64_t>(min(e0 + b, E - 1)) * h;
+            float total[EC], acc[EC];
+            for (int s = 0; s < S; ++s) {
+                segment_chains<EC>(xr, wr, s * seg, seg, acc);
+#pragma unroll
+                for (int b = 0; b < EC; ++b) total[b] = s == 0 ? acc[b] : total[b] + acc[b];
+            }
+#pragma unroll
+            for (int b = 0; b < EC; ++b)
+                if (e0 + b < E) lg[lane * E + e0 + b] = total[b];
+        }
+        __syncthreads();
+    } else {
+        for (int e0 = 0; e0 < E; e0 += EC) {
+            const float* wr[EC];
+#pragma unroll
+            for (int b = 0; b < EC; ++b) wr[b] = w + static_cast<int64_t>(min(e0 + b, E - 1)) * h;
+            for (int s = wave; s < S; s += nw) {
+                float acc[EC];
+                segment_chains<EC>(xr, wr, s * seg, seg, acc);
+#pragma unroll
+                for (int b = 0; b < EC; ++b) part[(s * EC + b) * kRtTokens + lane] = acc[b];
+            }
+            __syncthreads();
+            for (int idx = threadIdx.x; idx < EC * kRtTokens; idx += blockDim.x) {
+                const int b = idx / kRtTokens, tl = idx % kRtTokens;
+                if (e0 + b < E) {
+                    float total = part[b * kRtTokens + tl];
+                    for (int s = 1; s < S; ++s) total = total + part[(s * EC + b) * kRtTokens + tl];
+                    lg[tl * E + e0 + b] = total;
                 }
             }
-            for (int o = lpt >> 1; o >= 1; o >>= 1) {
-                AT ov = __shfl_xor(bv, o, 64);
-                int oi = __shfl_xor(bi, o, 64);
-                if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-            }
-            if (active) {
-                if ((bi & (lpt - 1)) == gl) taken |= 1u << (bi / lpt);
-                if (gl == 0) sel[tl * k + j] = bi;
-            }
+            __syncthreads();
         }
     }
-    __syncthreads();
-
-    // Phase 4: gates, one thread per token, sums in slot order.
-    for (int tl = tid; tl < rs.tb; tl += kThreads) {
-        const int64_t t = t_block + tl;
-        if (t >= T) continue;
-        const AT* l = lg + static_cast<size_t>(tl) * E;
-        const int* s = sel + tl * k;
-        AT g[kMaxTopK];
-        AT sum = AT(0);
-        if (score == RHP_SCORE_SOFTMAX) {
-            AT m = l[s[0]];
-            for (int j = 1; j < k; ++j) m = (l[s[j]] > m) ? l[s[j]] : m;
-            for (int j = 0; j < k; ++j) {
-                g[j] = rhp_exp_t(l[s[j]] - m);
-                sum = (j == 0) ? g[j] : sum + g[j];
-            }
-            for (int j = 0; j < k; ++j) g[j] = (g[j] / sum) * scale;
-        } else {
-            for (int j = 0; j < k; ++j) {
-                g[j] = rhp_sigmoid(l[s[j]]);
-                sum = (j == 0) ? g[j] : sum + g[j];
-            }
-            for (int j = 0; j < k; ++j) g[j] = (normalize ? g[j] / sum : g[j]) * scale;
-        }
-        for (int j = 0; j < k; ++j) {
-            topi[t * k + j] = s[j];
-            gates[t * k + j] = g[j];
-        }
-    }
+    const int tb = static_cast<int>(min<int64_t>(kRtTokens, T - t_block));
+    for (int idx = threadIdx.x; idx < tb * E; idx += blockDim.x) logits[t_block * E + idx] = lg[idx];
+    select_and_gate<float>(lg, sel, t_block, kRtTokens, blockDim.x, T, E, k, score, normalize, scale, bias, topi,
+                           gates);
 }
 
 }  // namespace
@@ -453,6 +574,39 @@ __global__ __launch_bounds__(kThreads) void route_bwd_kernel(const AT* __restric
     }
 }
 
+// Routing of bfloat16 tokens: route_bf16_kernel, whenever its LDS fits in
+// 64 KB; 0 = launched (or nothing to do), 1 = not taken.
+int launch_route_bf16(const void* x, const void* w, const void* bias, int64_t T, int h, int E, int k, int score,
+                      int normalize, double scale, void* logits, int32_t* topi, void* gates, hipStream_t stream,
+                      int* status) {
+    const int seg = std::min(256, h), S = h / seg;
+    const int ec = E >= 64 ? 16 : 8;
+    const int n_ec = (E + ec - 1) / ec;
+    const int expert_mode = n_ec >= S ? 1 : 0;
+    const size_t smem = static_cast<size_t>(kRtTokens) * E * sizeof(float) + static_cast<size_t>(kRtTokens) * k * sizeof(int) +
+                        (expert_mode ? 0 : static_cast<size_t>(S) * ec * kRtTokens * sizeof(float));
+    if (smem > 64 * 1024) {
+        *status = 1;
+        return 0;
+    }
+    *status = 0;
+    if (T == 0) return 0;
+    const int nw = std::min(expert_mode ? n_ec : S, kRtMaxWaves);
+    const dim3 grid(static_cast<unsigned>((T + kRtTokens - 1) / kRtTokens)), block(64 * nw);
+    const bf16* xb = static_cast<const bf16*>(x);
+    const float* wf = static_cast<const float*>(w);
+    const float* bf = static_cast<const float*>(bias);
+    if (ec == 16)
+        hipLaunchKernelGGL(route_bf16_kernel<16>, grid, block, smem, stream, xb, wf, bf, T, h, E, k, score, normalize,
+                           static_cast<float>(scale), seg, S, expert_mode, static_cast<float*>(logits), topi,
+                           static_cast<float*>(gates));
+    else
+        hipLaunchKernelGGL(route_bf16_kernel<8>, grid, block, smem, stream, xb, wf, bf, T, h, E, k, score, normalize,
+                           static_cast<float>(scale), seg, S, expert_mode, static_cast<float*>(logits), topi,
+                           static_cast<float*>(gates));
+    return check_launch("route_bf16_kernel");
+}
+
 template <class XT, class AT>
 int launch_route(const void* x, const void* w, const void* bias, int64_t T, int h, int E, int k, int score,
                  int normalize, double scale, void* logits, int32_t* topi, void* gates, hipStream_t stream) {
@@ -504,9 +658,14 @@ extern "C" int rhp_route(const void* x, int x_dtype, const void* router_w, int r
     if (x_dtype == RHP_F32)
         return launch_route<float, float>(x, router_w, bias, T, h, E, k, score, normalize, scale, logits, topi, gates,
                                           stream);
-    if (x_dtype == RHP_BF16)
+    if (x_dtype == RHP_BF16) {
+        int not_taken = 0;
+        const int rc = launch_route_bf16(x, router_w, bias, T, h, E, k, score, normalize, scale, logits, topi, gates,
+                                         stream, &not_taken);
+        if (!not_taken) return rc;
         return launch_route<bf16, float>(x, router_w, bias, T, h, E, k, score, normalize, scale, logits, topi, gates,
                                          stream);
+    }
     return fail(std::string("rhp_route: unsupported x dtype ") + dtype_name(x_dtype));
 }
 

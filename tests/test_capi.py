@@ -72,5 +72,6 @@ def test_workspace_queries_are_pure():
     assert L.rhp_dispatch_workspace_bytes(8192, 2, 8, 1) > 0
     assert L.rhp_dispatch_workspace_bytes(-1, 2, 8, 1) == 0
     a = L.rhp_router_wgrad_workspace_bytes(8192, 4096, 8, 2, C.F32)
-    assert a == ((8192 * 2 + 255) // 256 + 8) * 4096 * 4
+    # one float32 row of partial sums per 64-row piece of each expert's segment (at most T k / 64 + E pieces)
+    assert a == ((8192 * 2 + 63) // 64 + 8) * 4096 * 4
     assert L.rhp_router_wgrad_workspace_bytes(8192, 4096, 8, 2, C.F64) == 2 * a

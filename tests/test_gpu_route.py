@@ -27,6 +27,14 @@ ROUTE_CASES = [
     ("ep128-zipf", 8192, 2048, 128, 8, torch.bfloat16, "softmax", "zipf", 0.02),
     ("reference-default", 48, 8, 6, 2, torch.float64, "softmax", None, 0.35),
     ("odd-e", 333, 256, 5, 3, torch.bfloat16, "sigmoid", None, 0.05),
+    # bfloat16 kernel edges: a hidden size below one 256-element segment (ragged last 64-element group),
+    # expert counts that are not a multiple of the 8- or 16-expert groups, 32 segments (waves loop over
+    # segments), the expert-parallel mode (at least as many expert groups as segments), and more experts
+    # than its LDS holds (generic kernel)
+    ("bf16-h200-e20", 130, 200, 20, 4, torch.bfloat16, "softmax", "normal", 0.05),
+    ("bf16-h8192-e72", 100, 8192, 72, 6, torch.bfloat16, "sigmoid", "normal", 0.02),
+    ("bf16-expert-mode-e200", 150, 1024, 200, 8, torch.bfloat16, "softmax", "zipf", 0.02),
+    ("bf16-e300-generic", 70, 256, 300, 4, torch.bfloat16, "softmax", None, 0.05),
 ]
 
 

@@ -38,10 +38,34 @@ def _store(a: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a)).to(dtype)
 
 
+# (T, h, k, E, window, shared experts): the bfloat16 kernels are compiled for k <= 2 and k <= 8 with up to
+# two shared experts (one or several 64-lane passes, ragged last pass) and fall back to a generic kernel
+# beyond; every case holds slots of other devices (pair_row = -1).
+BF16_SHAPES = [
+    (97, 4096, 2, 8, (0, 6), 0),
+    (64, 2056, 2, 8, (2, 8), 2),
+    (50, 1024, 1, 4, (0, 3), 1),
+    (70, 1032, 8, 16, (4, 16), 2),
+    (33, 2048, 6, 64, (0, 40), 2),
+    (45, 2048, 8, 128, (16, 32), 0),
+    (21, 1000, 5, 12, (0, 12), 0),
+    (40, 512, 12, 16, (0, 12), 1),
+    (30, 768, 4, 8, (0, 8), 5),
+]
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
 @pytest.mark.parametrize("window", [(0, 10), (3, 7)], ids=["all", "share"])
 def test_permute_combine_token_bwd_bit_exact(dtype, window):
-    T, h, k, E = 300, 256, 3, 10
+    _rows_bit_exact(dtype, 300, 256, 3, 10, window, 1)
+
+
+@pytest.mark.parametrize("shape", BF16_SHAPES, ids=lambda s: f"T{s[0]}-h{s[1]}-k{s[2]}-E{s[3]}-S{s[5]}")
+def test_rows_bf16_shapes_bit_exact(shape):
+    _rows_bit_exact(torch.bfloat16, *shape)
+
+
+def _rows_bit_exact(dtype, T, h, k, E, window, n_shared):
     e0, e1 = window
     acc = NP_ACC[dtype]
     gdt = torch.float64 if dtype == torch.float64 else torch.float32
@@ -50,12 +74,12 @@ def test_permute_combine_token_bwd_bit_exact(dtype, window):
     x = seeded((T, h), 1, 1.0, dtype)
     y = seeded((P, h), 2, 1.0, dtype)
     gates = seeded((T, k), 3, 0.5, gdt).abs()
-    shared = [seeded((T, h), 4, 1.0, dtype)]
+    shared = [seeded((T, h), 40 + s, 1.0, dtype) for s in range(n_shared)]
     pair_row = torch.from_numpy(plan["pair_row"].astype(np.int32))
-    say(f"rows {dtype} window={window} T={T} h={h} k={k} P={P}")
+    say(f"rows {dtype} window={window} T={T} h={h} k={k} E={E} shared={n_shared} P={P}")
 
     xp = K.permute(x.to(DEV), pair_row.to(DEV), k, P)
-    out = K.combine(y.to(DEV), x.to(DEV), gates.to(DEV), topi.to(DEV), pair_row.to(DEV), [shared[0].to(DEV)])
+    out = K.combine(y.to(DEV), x.to(DEV), gates.to(DEV), topi.to(DEV), pair_row.to(DEV), [s.to(DEV) for s in shared])
     torch.cuda.synchronize()
 
     # permute: an exact row copy
@@ -67,7 +91,7 @@ def test_permute_combine_token_bwd_bit_exact(dtype, window):
     assert torch.equal(xp.cpu(), ref_xp)
 
     # combine: acc = 0; acc += g * y in ascending expert id; out = x + acc + shared
-    xn, yn, gn, sn = _to_np(x, acc), _to_np(y, acc), gates.numpy().astype(acc), _to_np(shared[0], acc)
+    xn, yn, gn = _to_np(x, acc), _to_np(y, acc), gates.numpy().astype(acc)
     order = np.argsort(topi.numpy(), axis=1, kind="stable")
     accum = np.zeros((T, h), acc)
     rows = plan["pair_row"].reshape(T, k)
@@ -77,7 +101,10 @@ def test_permute_combine_token_bwd_bit_exact(dtype, window):
         gj = gn[np.arange(T), j][:, None]
         contrib = gj * yn[np.clip(r, 0, None)]
         accum = np.where((r >= 0)[:, None], accum + contrib, accum)
-    ref_out = _store((xn + accum) + sn, dtype)
+    ref = xn + accum
+    for sh in shared:
+        ref = ref + _to_np(sh, acc)
+    ref_out = _store(ref, dtype)
     assert torch.equal(out.cpu(), ref_out)
 
     # combine backward: dy = g * dout (exact); dgates = <dout, y> (reduction)
@@ -99,9 +126,9 @@ def test_permute_combine_token_bwd_bit_exact(dtype, window):
     dxp = seeded((P, h), 6, 1.0, dtype)
     dl = seeded((T, k), 7, 0.3, gdt)
     w = seeded((E, h), 8, 0.05, gdt)
-    sdx = [seeded((T, h), 9, 1.0, dtype)]
+    sdx = [seeded((T, h), 90 + s, 1.0, dtype) for s in range(n_shared)]
     dx = K.token_bwd(dout.to(DEV), dxp.to(DEV), pair_row.to(DEV), dl.to(DEV), topi.to(DEV), w.to(DEV),
-                     [sdx[0].to(DEV)])
+                     [s.to(DEV) for s in sdx])
     torch.cuda.synchronize()
     a = dn.copy()
     dxpn = _to_np(dxp, acc)
@@ -111,7 +138,8 @@ def test_permute_combine_token_bwd_bit_exact(dtype, window):
     dln, wn = dl.numpy(), w.numpy()
     for j in range(k):
         a = a + (dln[:, j][:, None] * wn[topi.numpy()[:, j]]).astype(acc)
-    a = a + _to_np(sdx[0], acc)
+    for sh in sdx:
+        a = a + _to_np(sh, acc)
     assert torch.equal(dx.cpu(), _store(a, dtype))
 
 
