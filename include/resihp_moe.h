@@ -159,7 +159,7 @@ size_t rhp_router_wgrad_workspace_bytes(int64_t T, int h, int E, int k, int r_dt
  * Router weight gradient dW[e,:] = sum over pairs p = t*k+j routed to e of
  * dlogits_sel[p] * x[t,:].  perm / offsets are a dispatch plan over ALL E
  * experts (e0 = 0, e1 = E); each expert's rows are summed in plan order in
- * pieces of 256 rows, and the pieces are added in ascending order, so the
+ * pieces of 64 rows, and the pieces are added in ascending order, so the
  * result is deterministic.  Accumulation in r_dtype.  dw: [E,h] r_dtype.
  */
 int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, const int32_t* offsets, const void* x,
@@ -186,14 +186,28 @@ int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, const int32_t
  * Groups beyond RHP_MAX_GROUPS_PER_LAUNCH are split into several launches.
  */
 
+/*
+ * K-split workspace of the row-grouped products (forward and input-gradient;
+ * optional, NULL disables the split).  On each XCD the tiles past the last
+ * whole round of one tile per CU are cut along K into pieces that run on the
+ * otherwise idle CUs; pieces keep fp32 partial tiles here and the last piece
+ * of a tile to finish adds them in piece order (deterministic) and writes the
+ * tile.  The workspace ends in arrival counters that must be zero before its
+ * first use; every call leaves them zero again.  Calls that share a workspace
+ * must not run concurrently (stream-order them).  No reference counterpart:
+ * scheduling only, the products are those of moe.py:82-83.
+ */
+size_t rhp_expert_split_workspace_bytes(void);
+
 /* hpre[r] = xp[r] @ w1^T  ([M_g, F1]);  act[r] = silu(gate) * up  or  gelu(hpre)  ([M_g, f]). */
 int rhp_expert_fc1_fwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,
                        int h, int f, const void* const* xp, const void* const* w1, void* const* hpre,
-                       void* const* act_out, hipStream_t stream);
+                       void* const* act_out, void* split_ws, size_t split_ws_bytes, hipStream_t stream);
 
 /* y[r] = act[r] @ w2^T  ([M_g, h]). */
 int rhp_expert_fc2_fwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int h,
-                       int f, const void* const* act_in, const void* const* w2, void* const* y, hipStream_t stream);
+                       int f, const void* const* act_in, const void* const* w2, void* const* y, void* split_ws,
+                       size_t split_ws_bytes, hipStream_t stream);
 
 /*
  * Backward through fc2 and the activation:
@@ -202,7 +216,8 @@ int rhp_expert_fc2_fwd(int G, const int32_t* offsets, int rows_from_offsets, int
  */
 int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,
                        int h, int f, const void* const* dy, const void* const* act_in, const void* const* hpre,
-                       const void* const* w2, void* const* dhpre, void* const* dw2, hipStream_t stream);
+                       const void* const* w2, void* const* dhpre, void* const* dw2, void* split_ws,
+                       size_t split_ws_bytes, hipStream_t stream);
 
 /*
  * Backward through fc1:
@@ -211,7 +226,8 @@ int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_offsets, int
  */
 int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,
                        int h, int f, const void* const* dhpre, const void* const* xp, const void* const* w1,
-                       void* const* dxp, void* const* dw1, hipStream_t stream);
+                       void* const* dxp, void* const* dw1, void* split_ws, size_t split_ws_bytes,
+                       hipStream_t stream);
 
 /* ------------------------------------------------------------------ fp8 experts (delayed scaling) */
 

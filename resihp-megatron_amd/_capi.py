@@ -38,10 +38,11 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "rhp_token_bwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _pp, _i, _i, _i64, _i, _i, _i, _p, _p]),
     "rhp_router_wgrad_workspace_bytes": (_sz, [_i64, _i, _i, _i, _i]),
     "rhp_router_wgrad": (_i, [_p, _p, _p, _p, _i, _i, _i64, _i, _i, _i, _p, _p, _sz, _p]),
-    "rhp_expert_fc1_fwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _p]),
-    "rhp_expert_fc2_fwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _pp, _pp, _pp, _p]),
-    "rhp_expert_fc2_bwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _pp, _p]),
-    "rhp_expert_fc1_bwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _p]),
+    "rhp_expert_split_workspace_bytes": (_sz, []),
+    "rhp_expert_fc1_fwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _p, _sz, _p]),
+    "rhp_expert_fc2_fwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _pp, _pp, _pp, _p, _sz, _p]),
+    "rhp_expert_fc2_bwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _pp, _p, _sz, _p]),
+    "rhp_expert_fc1_bwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _p, _sz, _p]),
     "rhp_fp8_padded_offsets": (_i, [_p, _i, _i, _p, _p]),
     "rhp_fp8_cast": (_i, [_p, _i, _i64, _i, _i, _p, _p, _i64, _p, _i, _i, _i, _p, _p, _p, _p, _p]),
     "rhp_fp8_amax_roll": (_i, [_p, _p, _i, _i, _p]),

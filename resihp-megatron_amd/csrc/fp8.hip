@@ -293,7 +293,7 @@ template <int MODE, int EPI, int YF, int XF>
 __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
     __shared__ __align__(1024) uint8_t lds[kF8LdsBytes];
     Tile t;
-    if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
+    if (find_tile<MODE>(p, x_per_tile<EPI>(), kTile, blockIdx.x, &t) != kTileOk) return;
     t.g = __builtin_amdgcn_readfirstlane(t.g);
     t.x0 = __builtin_amdgcn_readfirstlane(t.x0);
     t.x_lim = __builtin_amdgcn_readfirstlane(t.x_lim);

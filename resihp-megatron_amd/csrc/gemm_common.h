@@ -36,6 +36,15 @@ struct Params {
     const float* scale_inv_y;
     const float* scale_inv_x;
     int scale_x_stride;
+    // Split of the last, partial round of tiles along K (row-grouped modes).
+    // split_cap > 1 enables it: each XCD's tiles past its last whole round of
+    // cu_per_xcd tiles are cut into up to split_cap pieces; a piece writes its
+    // fp32 accumulators to split_part, and the last piece of a tile to finish
+    // (split_cnt counter) adds the pieces in piece order and runs the epilogue.
+    float* split_part;        // [8 * cu_per_xcd][kTile * kTile] fp32 partial tiles
+    int32_t* split_cnt;       // [8 * cu_per_xcd] arrival counters, zero between launches
+    int split_cap;
+    int cu_per_xcd;
 };
 
 // ------------------------------------------------------------------ activations
@@ -72,19 +81,36 @@ struct Tile {
     int y0, y_lim;      // first Y row relative to the group's row 0, valid count
     int64_t row0;       // FWD/DGRAD: row of the group's first row in the row buffers
     int k_begin, k_end; // reduction range (WGRAD: group rows)
+    // K split: this block computes piece `piece` of `pieces`; piece q of the
+    // tile keeps its partial sums in split_part slot `slot + q * stride` and
+    // the tile's arrival counter is split_cnt[slot].
+    int piece, pieces, slot, stride;
 };
 
-// Finds this block's tile.  xt_cols output columns (X rows) and yt_rows output
-// rows (Y rows) per tile.  Blocks beyond the real tile count return false;
-// the others are remapped so that each XCD runs a contiguous range of tiles.
+constexpr int kXcds = 8;
+// A split pays only where a tile's reduction is long: each piece publishes
+// a 256 KB partial tile behind an L2-wide release, and the last one reads all
+// of them back.  Measured at K = 1408-4096 (a tile of 22-64 K steps) the split
+// lost up to 8 %, at K = 14336 and 28672 it gained 4 % and 2 %.
+constexpr int kSplitMinK64 = 128;    // K steps of 64 a tile needs to be split at all
+constexpr int kSplitMinSteps = 16;   // K steps of 64 a split piece keeps at least
+
+enum TileFound { kTileDone = 0, kTileOk = 1, kTileSkip = 2 };
+
+// Finds the tile of work item `bid` (a block id: item bid runs on XCD
+// bid % 8).  xt_cols output columns (X rows) and yt_rows output rows (Y rows)
+// per tile.  Items are remapped so that each XCD runs a contiguous range of
+// tiles.  Returns kTileDone past the last item of bid's XCD (so a block that
+// walks bid, bid + 8 n, ... stops there), kTileSkip for a tile with no rows
+// to compute, kTileOk otherwise.
 template <int MODE>
-__device__ __forceinline__ bool find_tile(const Params& p, int xt_cols, int yt_rows, Tile* t) {
+__device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_rows, uint32_t bid, Tile* t) {
     const int xt_n = (p.N + xt_cols - 1) / xt_cols;
     if (MODE == kWgrad) {
         const int yt_n = (p.Mo + yt_rows - 1) / yt_rows;
         const uint32_t total = static_cast<uint32_t>(p.G) * xt_n * yt_n;
-        if (blockIdx.x >= total) return false;
-        const uint32_t L = xcd_remap(blockIdx.x, total);
+        if (bid >= total) return kTileDone;
+        const uint32_t L = xcd_remap(bid, total);
         const int per_group = xt_n * yt_n;
         t->g = L / per_group;
         const int rem = L % per_group;
@@ -97,17 +123,56 @@ __device__ __forceinline__ bool find_tile(const Params& p, int xt_cols, int yt_r
         t->row0 = p.rows_from_offsets ? r0 : 0;
         t->k_begin = 0;
         t->k_end = r1 - r0;
+        t->piece = 0;
+        t->pieces = 1;
+        t->slot = 0;
+        t->stride = 0;
         // A shared row buffer holds rows_cap rows: never read past it.
         if (p.rows_from_offsets) t->k_end = max(0, min(t->k_end, p.rows_cap - r0));
-        return true;
+        return kTileOk;
     }
     uint32_t total = 0;
     for (int g = 0; g < p.G; ++g) {
         const int M = p.offsets[g + 1] - p.offsets[g];
         total += static_cast<uint32_t>((M + yt_rows - 1) / yt_rows) * xt_n;
     }
-    if (blockIdx.x >= total) return false;
-    uint32_t L = xcd_remap(blockIdx.x, total);
+    t->piece = 0;
+    t->pieces = 1;
+    t->slot = 0;
+    t->stride = 0;
+    uint32_t L;
+    if (p.split_cap > 1) {
+        // Hardware block b runs on XCD b % 8 as that XCD's (b / 8)-th block;
+        // XCD x owns the contiguous tile range [start, start + n).  Its first
+        // F tiles fill whole rounds of cu_per_xcd blocks; the rx tiles of the
+        // last round are cut along K into s pieces each, so that the round's
+        // rx * s blocks keep the XCD's CUs busy for 1/s of a tile's time.
+        const uint32_t C = static_cast<uint32_t>(p.cu_per_xcd);
+        const uint32_t x = bid % kXcds, j = bid / kXcds;
+        const uint32_t q = total / kXcds, r = total % kXcds;
+        const uint32_t n = q + (x < r ? 1u : 0u), start = x * q + (x < r ? x : r);
+        const uint32_t F = n / C * C, rx = n - F;
+        const uint32_t nk = static_cast<uint32_t>((p.K + 63) / 64);
+        uint32_t s = rx && nk >= static_cast<uint32_t>(kSplitMinK64) ? C / rx : 1u;
+        s = min(s, static_cast<uint32_t>(p.split_cap));
+        s = min(s, nk / kSplitMinSteps);
+        if (j < F || s < 2) {
+            if (j >= n) return kTileDone;
+            L = start + j;
+        } else {
+            const uint32_t u = j - F;
+            if (u >= rx * s) return kTileDone;
+            const uint32_t tt = u % rx;
+            L = start + F + tt;
+            t->piece = static_cast<int>(u / rx);
+            t->pieces = static_cast<int>(s);
+            t->slot = static_cast<int>(x * C + tt);
+            t->stride = static_cast<int>(rx);
+        }
+    } else {
+        if (bid >= total) return kTileDone;
+        L = xcd_remap(bid, total);
+    }
     for (int g = 0; g < p.G; ++g) {
         const int M = p.offsets[g + 1] - p.offsets[g];
         const int mt = (M + yt_rows - 1) / yt_rows;
@@ -122,13 +187,18 @@ __device__ __forceinline__ bool find_tile(const Params& p, int xt_cols, int yt_r
             t->row0 = p.rows_from_offsets ? p.offsets[g] : 0;
             t->k_begin = 0;
             t->k_end = p.K;
+            if (t->pieces > 1) {
+                const int nk = (p.K + 63) / 64;
+                t->k_begin = (t->piece * nk / t->pieces) * 64;
+                t->k_end = min(p.K, ((t->piece + 1) * nk / t->pieces) * 64);
+            }
             // A shared row buffer holds rows_cap rows: never touch rows past it.
             if (p.rows_from_offsets) t->y_lim = min(t->y_lim, p.rows_cap - static_cast<int>(t->row0) - t->y0);
-            return t->y_lim > 0;
+            return t->y_lim > 0 ? kTileOk : kTileSkip;
         }
         L -= n_tiles;
     }
-    return false;
+    return kTileDone;
 }
 
 // X columns covered by one MFMA tile: SwiGLU FWD tiles cover 128 activation
@@ -362,33 +432,53 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
     }
 }
 
-// Epilogue, in two halves of 128 Y rows.  The pre-activation values a
-// backward epilogue reads are loaded first, so their latency overlaps the
-// staging; then the waves owning the half write their fp32 accumulators to
-// LDS ([128 rows][256 X] at kEpPitchF floats per row), and every thread takes
-// 4-column pieces, so each wave instruction reads or writes whole contiguous
-// row segments in HBM.  Barriers here wait only for LDS accesses: the global
-// stores of one half drain while the next is staged.  A wave owns WY Y rows
-// (NT threads in the workgroup); for MFMA tile (i, j) a lane holds Y row
-// wy * WY + 32 j + (lane & 31) and X columns wx * 128 + 32 i + 8 q +
-// 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller guarantees that every
-// load into the LDS buffer has completed.
-template <int MODE, int EPI, int NT = kThreadsMfma, int WY = kWaveY>
-__device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][WY / 32],
-                                         int wx, int wy, int lane, float mul = 1.0f) {
-    static_assert(WY <= kEpRows && kEpRows % WY == 0, "a wave's rows lie in one half");
-    float* ep = reinterpret_cast<float*>(lds);
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        AuxHalf<EPI, NT> aux;
-        load_aux_half<MODE, EPI, NT>(p, t, half * kEpRows, aux);
-        lds_barrier();
-        if ((wy * WY) / kEpRows == half) {
+// The partial tiles of a K-split tile's pieces: piece q at first + q * stride
+// (float4 units), each thread's accumulators at float4 (i FY + j) 4 + v,
+// thread-major.  pieces = 0: no split, the accumulators are the tile.
+struct SplitSum {
+    const float4* first;
+    int pieces;
+    size_t stride;
+};
+
+// One half of the epilogue (rows [HALF * 128, +128) of the tile): load the
+// half's aux values, stage the fp32 results in LDS, then write the half.
+template <int HALF, int MODE, int EPI, int NT, int WY>
+__device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, float* ep, f32x16_t (&acc)[4][WY / 32],
+                                              int wx, int wy, int lane, float mul, const SplitSum& split) {
+    constexpr int FY = WY / 32;
+    AuxHalf<EPI, NT> aux;
+    load_aux_half<MODE, EPI, NT>(p, t, HALF * kEpRows, aux);
+    lds_barrier();
+    if ((wy * WY) / kEpRows == HALF) {
+        if (split.pieces) {
+            // The sum of the pieces, in piece order.
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < WY / 32; ++j) {
-                    const int y = wy * WY + j * 32 + (lane & 31) - half * kEpRows;
+                for (int j = 0; j < FY; ++j) {
+                    const int y = wy * WY + j * 32 + (lane & 31) - HALF * kEpRows;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int x = wx * 128 + i * 32 + q * 8 + 4 * (lane >> 5);
+                        const float4* src = split.first + ((i * FY + j) * 4 + q) * NT + threadIdx.x;
+                        float4 v = src[0];
+                        for (int pc = 1; pc < split.pieces; ++pc) {
+                            const float4 w = src[pc * split.stride];
+                            v.x += w.x;
+                            v.y += w.y;
+                            v.z += w.z;
+                            v.w += w.w;
+                        }
+                        *reinterpret_cast<float4*>(ep + y * kEpPitchF + x) = v;
+                    }
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < FY; ++j) {
+                    const int y = wy * WY + j * 32 + (lane & 31) - HALF * kEpRows;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int x = wx * 128 + i * 32 + q * 8 + 4 * (lane >> 5);
@@ -401,9 +491,31 @@ __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t
                     }
                 }
         }
-        lds_barrier();
-        epilogue_half<MODE, EPI, NT>(p, t, ep, half * kEpRows, aux);
     }
+    lds_barrier();
+    epilogue_half<MODE, EPI, NT>(p, t, ep, HALF * kEpRows, aux);
+}
+
+// Epilogue, in two halves of 128 Y rows.  The pre-activation values a
+// backward epilogue reads are loaded first, so their latency overlaps the
+// staging; then the waves owning the half write their fp32 accumulators to
+// LDS ([128 rows][256 X] at kEpPitchF floats per row), and every thread takes
+// 4-column pieces, so each wave instruction reads or writes whole contiguous
+// row segments in HBM.  Barriers here wait only for LDS accesses: the global
+// stores of one half drain while the next is staged.  A wave owns WY Y rows
+// (NT threads in the workgroup); for MFMA tile (i, j) a lane holds Y row
+// wy * WY + 32 j + (lane & 31) and X columns wx * 128 + 32 i + 8 q +
+// 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller guarantees that every
+// load into the LDS buffer has completed.  With a K split, the staged values
+// are the sum of the pieces' partial tiles instead of acc.
+template <int MODE, int EPI, int NT = kThreadsMfma, int WY = kWaveY>
+__device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][WY / 32],
+                                         int wx, int wy, int lane, float mul = 1.0f,
+                                         SplitSum split = SplitSum{nullptr, 0, 0}) {
+    static_assert(WY <= kEpRows && kEpRows % WY == 0, "a wave's rows lie in one half");
+    float* ep = reinterpret_cast<float*>(lds);
+    epilogue_pass<0, MODE, EPI, NT, WY>(p, t, ep, acc, wx, wy, lane, mul, split);
+    epilogue_pass<1, MODE, EPI, NT, WY>(p, t, ep, acc, wx, wy, lane, mul, split);
 }
 
 // Scheduling hint: MF MFMAs with RD LDS reads spread evenly between them.

@@ -22,6 +22,7 @@
 // Work unit: a 256 x 256 output tile.  Tiles are ordered group-major, then by
 // output column block, then by row block, and block ids are remapped so each
 // XCD runs a contiguous range of that order.
+#include <atomic>
 #include <type_traits>
 
 #include "gemm_common.h"
@@ -101,14 +102,55 @@ constexpr int kLdsSlotsBytes = kSlots * kT64Bytes > kEpBytes ? kSlots * kT64Byte
 static_assert(kLdsSlotsBytes <= 163840, "five 32 KB slots");
 constexpr uint32_t kPastView = 0x7ffffff0u;   // soffset that puts every lane past its buffer view
 
+// A piece of a K-split tile: every piece stores its fp32 accumulators (laid
+// out thread-major, so each store instruction of a wave is contiguous), makes
+// them visible device-wide and counts itself in.  The piece that arrives last
+// returns true: its epilogue then stages the sum of all pieces, read from
+// memory in piece order (the same bits whichever piece is last), instead of
+// its own accumulators.  It resets the counter for the next launch.  No block
+// ever waits for another.
+template <int NT, int FY>
+__device__ __forceinline__ bool split_arrive(const Params& p, const Tile& t, const f32x16_t (&acc)[4][FY],
+                                             uint8_t* lds) {
+    constexpr int kVec = 4 * FY * 4;   // float4 per thread
+    static_assert(NT * kVec * 4 == kTile * kTile, "a piece holds a whole tile");
+    const int tid = threadIdx.x;
+    float4* mine = reinterpret_cast<float4*>(p.split_part) + static_cast<size_t>(t.slot + t.piece * t.stride) * (NT * kVec);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < FY; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                mine[((i * FY + j) * 4 + v) * NT + tid] =
+                    make_float4(acc[i][j][4 * v], acc[i][j][4 * v + 1], acc[i][j][4 * v + 2], acc[i][j][4 * v + 3]);
+    // Each wave waits for its own stores; after the barrier one thread makes
+    // the whole block's stores visible device-wide and counts the piece in.
+    // (An agent-scope fence writes back the XCD's L2; one per piece, not one
+    // per wave, keeps it from disturbing the tiles the other CUs stream.)
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();                      // also: every LDS read of the main loop is done
+    int* flag = reinterpret_cast<int*>(lds);
+    if (tid == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const int arrived = __hip_atomic_fetch_add(p.split_cnt + t.slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (arrived == t.pieces - 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            p.split_cnt[t.slot] = 0;   // every piece of this launch has arrived: reset for the next one
+        }
+        flag[0] = arrived;
+    }
+    __syncthreads();
+    return flag[0] == t.pieces - 1;
+}
+
+// One tile: the K loop through the slot ring, then the epilogue (or, for a
+// piece of a K-split tile, the hand-over to the piece that finishes last).
 template <int MODE, int EPI, int NW>
-__global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
+__device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* lds) {
     // NW waves: wave w owns X rows [128 (w % 2), +128) and Y rows [WY (w / 2), +WY).
     constexpr int WY = kTile / (NW / 2), FY = WY / 32;
     constexpr int kPerWave = kT64Bytes / 1024 / NW;   // loads per wave per operand tile
-    __shared__ __align__(1024) uint8_t lds[kLdsSlotsBytes];
-    Tile t;
-    if (!find_tile<MODE>(p, x_per_tile<EPI>(), kTile, &t)) return;
     t.g = __builtin_amdgcn_readfirstlane(t.g);
     t.x0 = __builtin_amdgcn_readfirstlane(t.x0);
     t.x_lim = __builtin_amdgcn_readfirstlane(t.x_lim);
@@ -117,6 +159,10 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
     t.row0 = __builtin_amdgcn_readfirstlane(static_cast<int>(t.row0));
     t.k_begin = __builtin_amdgcn_readfirstlane(t.k_begin);
     t.k_end = __builtin_amdgcn_readfirstlane(t.k_end);
+    t.piece = __builtin_amdgcn_readfirstlane(t.piece);
+    t.pieces = __builtin_amdgcn_readfirstlane(t.pieces);
+    t.slot = __builtin_amdgcn_readfirstlane(t.slot);
+    t.stride = __builtin_amdgcn_readfirstlane(t.stride);
     const int g = t.g;
     // The wave index is uniform: held in a scalar register, the LDS destination
     // of each direct load is scalar arithmetic (no VALU -> SGPR move per load).
@@ -306,7 +352,23 @@ __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
         }
         wait_loads_all();   // the tiles past the last step
     }
+    if (MODE != kWgrad && t.pieces > 1) {
+        if (!split_arrive<64 * NW, FY>(p, t, acc, lds)) return;
+        const SplitSum sum{reinterpret_cast<const float4*>(p.split_part) + static_cast<size_t>(t.slot) * (kTile * kTile / 4),
+                           t.pieces, static_cast<size_t>(t.stride) * (kTile * kTile / 4)};
+        epilogue<MODE, EPI, 64 * NW, WY>(p, t, lds, acc, wx, wy, lane, 1.0f, sum);
+        return;
+    }
     epilogue<MODE, EPI, 64 * NW, WY>(p, t, lds, acc, wx, wy, lane);
+}
+
+// One block per tile (hardware block b runs on XCD b % 8).
+template <int MODE, int EPI, int NW>
+__global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
+    __shared__ __align__(1024) uint8_t lds[kLdsSlotsBytes];
+    Tile t;
+    if (find_tile<MODE>(p, x_per_tile<EPI>(), kTile, blockIdx.x, &t) != kTileOk) return;
+    gg_bf16_tile<MODE, EPI, NW>(p, t, lds);
 }
 
 // ------------------------------------------------------------------ generic kernel (any dtype)
@@ -320,7 +382,7 @@ template <class S, int MODE, int EPI>
 __global__ __launch_bounds__(256) void gg_simt_kernel(Params p) {
     using A = typename Elem<S>::acc;
     Tile t;
-    if (!find_tile<MODE>(p, kSimtTile, kSimtTile, &t)) return;
+    if (find_tile<MODE>(p, kSimtTile, kSimtTile, blockIdx.x, &t) != kTileOk) return;
     const int g = t.g;
     const S* Ap = static_cast<const S*>(p.a[g]);
     const S* Bp = static_cast<const S*>(p.b[g]);
@@ -386,7 +448,32 @@ struct Job {
     void* const* c;
     void* const* c2;
     const void* const* aux;
+    void* split_ws;   // K-split workspace (rhp_expert_split_workspace_bytes), or null
+    int cus_per_xcd;  // CUs per XCD of the device the launch runs on
 };
+
+// K-split workspace: 8 XCDs x up to kSplitMaxCus pieces of one fp32 tile each,
+// then one arrival counter per piece slot.
+constexpr int kSplitMaxCus = 32;   // CUs per XCD the workspace is sized for
+constexpr int kSplitCap = 8;       // pieces per tile at most
+constexpr size_t kSplitSlots = static_cast<size_t>(kXcds) * kSplitMaxCus;
+constexpr size_t kSplitPartBytes = kSplitSlots * kTile * kTile * sizeof(float);
+constexpr size_t kSplitBytes = kSplitPartBytes + kSplitSlots * sizeof(int32_t);
+
+// CUs per XCD of the current device (cached per device id); 0 if unknown.
+int cus_per_xcd() {
+    static std::atomic<int> cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int c = cache[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        c = std::max(1, cus / kXcds);
+        cache[dev].store(c, std::memory_order_relaxed);
+    }
+    return c;
+}
 
 template <int MODE, int EPI>
 unsigned mfma_blocks(const Params& p, int64_t rows_cap) {
@@ -405,8 +492,11 @@ unsigned simt_blocks(const Params& p, int64_t rows_cap) {
 template <int MODE, int EPI>
 void launch_one(const Job& j, const Params& p, hipStream_t s) {
     if (j.mfma) {
-        const unsigned nb = mfma_blocks<MODE, EPI>(p, j.rows_cap);
+        unsigned nb = mfma_blocks<MODE, EPI>(p, j.rows_cap);
         if (!nb) return;
+        // A K split adds at most one round of pieces to each XCD's items.
+        if (MODE != kWgrad && p.split_cap > 1)
+            nb = kXcds * ((nb + kXcds - 1) / kXcds + static_cast<unsigned>(p.cu_per_xcd));
         constexpr int nw = MODE == kFwd ? 4 : kWaves;
         hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, nw>), dim3(nb), dim3(64 * nw), 0, s, p);
         return;
@@ -435,7 +525,9 @@ void launch(const Job& j, const Params& p, hipStream_t s) {
 }
 
 // Runs a job in launches of at most kMaxG groups.
-int run(const Job& j, const char* what, hipStream_t s) {
+int run(const Job& job, const char* what, hipStream_t s) {
+    Job j = job;
+    j.cus_per_xcd = cus_per_xcd();
     for (int g0 = 0; g0 < j.G; g0 += kMaxG) {
         const int gn = std::min(kMaxG, j.G - g0);
         Params p{};
@@ -459,6 +551,17 @@ int run(const Job& j, const char* what, hipStream_t s) {
         p.ldaux = j.ldaux;
         p.f = j.f;
         p.rows_cap = static_cast<int>(j.rows_cap);
+        // Only reductions long enough to be split get the split (and its larger
+        // grid: the extra, mostly empty blocks cost about 1 % of a short product).
+        if (j.split_ws && j.mfma && j.mode != kWgrad && j.K >= kSplitMinK64 * 64) {
+            const int C = std::min(kSplitMaxCus, j.cus_per_xcd);
+            if (C > 1) {
+                p.split_part = static_cast<float*>(j.split_ws);
+                p.split_cnt = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(j.split_ws) + kSplitPartBytes);
+                p.split_cap = kSplitCap;
+                p.cu_per_xcd = C;
+            }
+        }
         launch(j, p, s);
         if (int rc = check_launch(what)) return rc;
     }
@@ -501,16 +604,28 @@ bool mfma_ok(int dtype, int h, int f, int act, int64_t rows_cap) {
            kTile * widest * 2 < limit;
 }
 
+int check_split_ws(const char* fn, const void* ws, size_t bytes) {
+    if (ws == nullptr) return 0;
+    if (bytes < kSplitBytes || !aligned16(ws))
+        return fail(std::string(fn) + ": split workspace must be 16-byte aligned and hold "
+                    "rhp_expert_split_workspace_bytes() bytes");
+    return 0;
+}
+
 }  // namespace
 }  // namespace rhp
 
 using namespace rhp;
 
+extern "C" size_t rhp_expert_split_workspace_bytes(void) { return kSplitBytes; }
+
 extern "C" int rhp_expert_fc1_fwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype,
                                   int act, int h, int f, const void* const* xp, const void* const* w1,
-                                  void* const* hpre, void* const* act_out, hipStream_t stream) {
+                                  void* const* hpre, void* const* act_out, void* split_ws, size_t split_ws_bytes,
+                                  hipStream_t stream) {
     clear_error();
     if (int rc = check_common("rhp_expert_fc1_fwd", G, offsets, rows_cap, dtype, act, h, f)) return rc;
+    if (int rc = check_split_ws("rhp_expert_fc1_fwd", split_ws, split_ws_bytes)) return rc;
     RHP_REQUIRE(all_set(xp, G) && all_set(w1, G) && all_set((const void* const*)hpre, G) &&
                     all_set((const void* const*)act_out, G),
                 "rhp_expert_fc1_fwd: null pointer");
@@ -537,14 +652,16 @@ extern "C" int rhp_expert_fc1_fwd(int G, const int32_t* offsets, int rows_from_o
     j.b = w1;
     j.c = hpre;
     j.c2 = act_out;
+    j.split_ws = split_ws;
     return run(j, "expert_fc1_fwd", stream);
 }
 
 extern "C" int rhp_expert_fc2_fwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype,
                                   int h, int f, const void* const* act_in, const void* const* w2, void* const* y,
-                                  hipStream_t stream) {
+                                  void* split_ws, size_t split_ws_bytes, hipStream_t stream) {
     clear_error();
     if (int rc = check_common("rhp_expert_fc2_fwd", G, offsets, rows_cap, dtype, RHP_ACT_GELU, h, f)) return rc;
+    if (int rc = check_split_ws("rhp_expert_fc2_fwd", split_ws, split_ws_bytes)) return rc;
     RHP_REQUIRE(all_set(act_in, G) && all_set(w2, G) && all_set((const void* const*)y, G),
                 "rhp_expert_fc2_fwd: null pointer");
     Job j{};
@@ -566,15 +683,17 @@ extern "C" int rhp_expert_fc2_fwd(int G, const int32_t* offsets, int rows_from_o
     j.a = act_in;
     j.b = w2;
     j.c = y;
+    j.split_ws = split_ws;
     return run(j, "expert_fc2_fwd", stream);
 }
 
 extern "C" int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype,
                                   int act, int h, int f, const void* const* dy, const void* const* act_in,
                                   const void* const* hpre, const void* const* w2, void* const* dhpre,
-                                  void* const* dw2, hipStream_t stream) {
+                                  void* const* dw2, void* split_ws, size_t split_ws_bytes, hipStream_t stream) {
     clear_error();
     if (int rc = check_common("rhp_expert_fc2_bwd", G, offsets, rows_cap, dtype, act, h, f)) return rc;
+    if (int rc = check_split_ws("rhp_expert_fc2_bwd", split_ws, split_ws_bytes)) return rc;
     RHP_REQUIRE(all_set(dy, G) && all_set(act_in, G) && all_set(hpre, G) && all_set(w2, G) &&
                     all_set((const void* const*)dhpre, G) && all_set((const void* const*)dw2, G),
                 "rhp_expert_fc2_bwd: null pointer");
@@ -604,6 +723,7 @@ extern "C" int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_o
     d.b = w2;
     d.c = dhpre;
     d.aux = hpre;
+    d.split_ws = split_ws;
     if (int rc = run(d, "expert_fc2_dgrad", stream)) return rc;
     // dw2[g] = dy_g^T @ act_g
     Job w{};
@@ -629,9 +749,11 @@ extern "C" int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_o
 
 extern "C" int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype,
                                   int act, int h, int f, const void* const* dhpre, const void* const* xp,
-                                  const void* const* w1, void* const* dxp, void* const* dw1, hipStream_t stream) {
+                                  const void* const* w1, void* const* dxp, void* const* dw1, void* split_ws,
+                                  size_t split_ws_bytes, hipStream_t stream) {
     clear_error();
     if (int rc = check_common("rhp_expert_fc1_bwd", G, offsets, rows_cap, dtype, act, h, f)) return rc;
+    if (int rc = check_split_ws("rhp_expert_fc1_bwd", split_ws, split_ws_bytes)) return rc;
     RHP_REQUIRE(all_set(dhpre, G) && all_set(xp, G) && all_set(w1, G) && all_set((const void* const*)dw1, G),
                 "rhp_expert_fc1_bwd: null pointer");
     const int F1 = act == RHP_ACT_SWIGLU ? 2 * f : f;
@@ -659,6 +781,7 @@ extern "C" int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_o
         d.a = dhpre;
         d.b = w1;
         d.c = dxp;
+        d.split_ws = split_ws;
         if (int rc = run(d, "expert_fc1_dgrad", stream)) return rc;
     }
     // dw1[g] = dhpre_g^T @ xp_g

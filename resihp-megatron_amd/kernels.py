@@ -284,9 +284,33 @@ def _shared_rows(rows_from_offsets: bool, rows_cap: int) -> int | None:
     return rows_cap if rows_from_offsets else None
 
 
+_split_ws_cache: dict[int, torch.Tensor] = {}
+
+
+def split_workspace(dev: torch.device) -> torch.Tensor:
+    """The K-split workspace of the expert GEMMs on ``dev``: allocated (zeroed) once per device.
+
+    Its arrival counters must be zero before a call, and every call leaves them zero; the
+    GEMM calls that use it are stream-ordered on the current stream.
+    """
+    idx = torch.device(dev).index if torch.device(dev).index is not None else torch.cuda.current_device()
+    ws = _split_ws_cache.get(idx)
+    if ws is None:
+        ws = torch.zeros(C.lib().rhp_expert_split_workspace_bytes(), dtype=torch.uint8, device=f"cuda:{idx}")
+        _split_ws_cache[idx] = ws
+    return ws
+
+
+def _split_args(dev: torch.device, split: bool) -> tuple:
+    if not split:
+        return None, 0
+    ws = split_workspace(dev)
+    return _ptr(ws), ws.numel()
+
+
 def expert_fc1_fwd(xs: list[torch.Tensor], offsets: torch.Tensor, rows_from_offsets: bool, rows_cap: int,
                    w1: list[torch.Tensor], f: int, act: str, hpre: list[torch.Tensor],
-                   act_out: list[torch.Tensor]) -> None:
+                   act_out: list[torch.Tensor], split: bool = True) -> None:
     dev = _need_cuda(offsets, *xs, *w1, *hpre, *act_out)
     G, dt, h = len(w1), w1[0].dtype, w1[0].shape[1]
     F1 = 2 * f if act == "swiglu" else f
@@ -297,11 +321,11 @@ def expert_fc1_fwd(xs: list[torch.Tensor], offsets: torch.Tensor, rows_from_offs
     _check_groups("hpre", hpre, G, dt, F1, rows)
     _check_groups("act", act_out, G, dt, f, rows)
     _call("rhp_expert_fc1_fwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w1[0]),
-          act_code(act), h, f, _arr(xs), _arr(w1), _arr(hpre), _arr(act_out))
+          act_code(act), h, f, _arr(xs), _arr(w1), _arr(hpre), _arr(act_out), *_split_args(dev, split))
 
 
 def expert_fc2_fwd(acts: list[torch.Tensor], offsets: torch.Tensor, rows_from_offsets: bool, rows_cap: int,
-                   w2: list[torch.Tensor], ys: list[torch.Tensor]) -> None:
+                   w2: list[torch.Tensor], ys: list[torch.Tensor], split: bool = True) -> None:
     dev = _need_cuda(offsets, *acts, *w2, *ys)
     G, dt, (h, f) = len(w2), w2[0].dtype, tuple(w2[0].shape)
     rows = _shared_rows(rows_from_offsets, rows_cap)
@@ -310,12 +334,12 @@ def expert_fc2_fwd(acts: list[torch.Tensor], offsets: torch.Tensor, rows_from_of
     _check_groups("act", acts, G, dt, f, rows)
     _check_groups("y", ys, G, dt, h, rows)
     _call("rhp_expert_fc2_fwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w2[0]), h, f,
-          _arr(acts), _arr(w2), _arr(ys))
+          _arr(acts), _arr(w2), _arr(ys), *_split_args(dev, split))
 
 
 def expert_fc2_bwd(dys: list[torch.Tensor], acts: list[torch.Tensor], hpres: list[torch.Tensor],
                    offsets: torch.Tensor, rows_from_offsets: bool, rows_cap: int, w2: list[torch.Tensor], act: str,
-                   dhpre: list[torch.Tensor], dw2: list[torch.Tensor]) -> None:
+                   dhpre: list[torch.Tensor], dw2: list[torch.Tensor], split: bool = True) -> None:
     dev = _need_cuda(offsets, *dys, *acts, *hpres, *w2, *dhpre, *dw2)
     G, dt, (h, f) = len(w2), w2[0].dtype, tuple(w2[0].shape)
     F1 = 2 * f if act == "swiglu" else f
@@ -328,12 +352,13 @@ def expert_fc2_bwd(dys: list[torch.Tensor], acts: list[torch.Tensor], hpres: lis
     _check_groups("hpre", hpres, G, dt, F1, rows)
     _check_groups("dhpre", dhpre, G, dt, F1, rows)
     _call("rhp_expert_fc2_bwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w2[0]),
-          act_code(act), h, f, _arr(dys), _arr(acts), _arr(hpres), _arr(w2), _arr(dhpre), _arr(dw2))
+          act_code(act), h, f, _arr(dys), _arr(acts), _arr(hpres), _arr(w2), _arr(dhpre), _arr(dw2),
+          *_split_args(dev, split))
 
 
 def expert_fc1_bwd(dhpre: list[torch.Tensor], xs: list[torch.Tensor], offsets: torch.Tensor,
                    rows_from_offsets: bool, rows_cap: int, w1: list[torch.Tensor], f: int, act: str,
-                   dxs: list[torch.Tensor] | None, dw1: list[torch.Tensor]) -> None:
+                   dxs: list[torch.Tensor] | None, dw1: list[torch.Tensor], split: bool = True) -> None:
     dev = _need_cuda(offsets, *dhpre, *xs, *w1, *(dxs or []), *dw1)
     G, dt, h = len(w1), w1[0].dtype, w1[0].shape[1]
     F1 = 2 * f if act == "swiglu" else f
@@ -346,7 +371,8 @@ def expert_fc1_bwd(dhpre: list[torch.Tensor], xs: list[torch.Tensor], offsets: t
     if dxs:
         _check_groups("dx", dxs, G, dt, h, rows)
     _call("rhp_expert_fc1_bwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w1[0]),
-          act_code(act), h, f, _arr(dhpre), _arr(xs), _arr(w1), _arr(dxs) if dxs else None, _arr(dw1))
+          act_code(act), h, f, _arr(dhpre), _arr(xs), _arr(w1), _arr(dxs) if dxs else None, _arr(dw1),
+          *_split_args(dev, split))
 
 
 # ----------------------------------------------------------------------------- fp8 experts

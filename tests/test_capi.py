@@ -60,9 +60,15 @@ def test_dispatch_and_gemm_reject_bad_arguments():
         C.call("rhp_dispatch", fake, 10, 2, 8, 0, 8, 1, fake, fake, fake, fake, fake, fake, 0, None)
     ptrs = C.ptr_array([4096])
     with pytest.raises(RuntimeError, match="at least one group"):
-        C.call("rhp_expert_fc1_fwd", 0, fake, 1, 0, C.BF16, C.ACT_SWIGLU, 64, 64, ptrs, ptrs, ptrs, ptrs, None)
+        C.call("rhp_expert_fc1_fwd", 0, fake, 1, 0, C.BF16, C.ACT_SWIGLU, 64, 64, ptrs, ptrs, ptrs, ptrs, None, 0,
+               None)
     with pytest.raises(RuntimeError, match="unsupported dtype"):
-        C.call("rhp_expert_fc2_fwd", 1, fake, 1, 0, C.E4M3, 64, 64, ptrs, ptrs, ptrs, None)
+        C.call("rhp_expert_fc2_fwd", 1, fake, 1, 0, C.E4M3, 64, 64, ptrs, ptrs, ptrs, None, 0, None)
+    with pytest.raises(RuntimeError, match="split workspace"):
+        C.call("rhp_expert_fc2_fwd", 1, fake, 1, 0, C.BF16, 64, 64, ptrs, ptrs, ptrs, fake, 1024, None)
+    with pytest.raises(RuntimeError, match="split workspace"):
+        C.call("rhp_expert_fc1_bwd", 1, fake, 1, 0, C.BF16, C.ACT_SWIGLU, 64, 64, ptrs, ptrs, ptrs, ptrs, ptrs,
+               ctypes.c_void_p(4097), C.lib().rhp_expert_split_workspace_bytes(), None)
     with pytest.raises(RuntimeError, match="at most 8 shared"):
         C.call("rhp_combine", fake, fake, fake, C.F32, fake, fake, ptrs, 9, C.BF16, 4, 64, 2, fake, None)
 
@@ -75,3 +81,5 @@ def test_workspace_queries_are_pure():
     # one float32 row of partial sums per 64-row piece of each expert's segment (at most T k / 64 + E pieces)
     assert a == ((8192 * 2 + 63) // 64 + 8) * 4096 * 4
     assert L.rhp_router_wgrad_workspace_bytes(8192, 4096, 8, 2, C.F64) == 2 * a
+    # K-split workspace: 8 XCDs x 32 CUs of one fp32 256 x 256 tile each, then one int32 counter per slot
+    assert L.rhp_expert_split_workspace_bytes() == 256 * 256 * 256 * 4 + 256 * 4

@@ -135,3 +135,58 @@ def test_gemm_deterministic():
     torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     assert sum(counts) == 733
+
+
+# K split of the last round of tiles.  Each XCD runs its share of tiles in rounds of one tile per CU;
+# where a tile's reduction is long (at least 128 K steps of 64), the tiles of an XCD's last, partial
+# round are cut along K into pieces whose fp32 partial tiles the last piece to finish adds in piece
+# order.  (name, h, f, counts, rows checked against float64): "deep" puts one fc2 forward and one fc1
+# input-gradient tile on each of six XCDs, cut in eight pieces; "rounds" gives every XCD 33 tiles of
+# each, one whole round of 32 and one tile (the last row tile) cut in eight.
+SPLIT_CASES = [
+    ("deep", 512, 8192, [300, 40], None),
+    ("rounds", 2048, 8192, [8448], list(range(0, 64)) + list(range(8192, 8448))),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
+def test_k_split_tiles(case):
+    name, h, f, counts, rows = case
+    dt, G, act = torch.bfloat16, len(counts), "swiglu"
+    F1 = 2 * f
+    offs = torch.tensor([0] + list(torch.tensor(counts).cumsum(0).tolist()), dtype=torch.int32)
+    P = int(offs[-1])
+    a = seeded((P, f), 1, 1.0, dt)
+    dh = seeded((P, F1), 2, 1.0, dt)
+    w1 = [seeded((F1, h), 10 + g, 0.02, dt) for g in range(G)]
+    w2 = [seeded((h, f), 100 + g, 0.02, dt) for g in range(G)]
+    d = lambda t: t.to(DEV)  # noqa: E731
+    offs_d, a_d, dh_d = d(offs), d(a), d(dh)
+    w1_d, w2_d = [d(w) for w in w1], [d(w) for w in w2]
+    xp_d = d(seeded((P, h), 3, 1.0, dt))
+    say(f"gemm k-split {name}: G={G} P={P} h={h} f={f}")
+
+    def run(split):
+        y = torch.empty(P, h, dtype=dt, device=DEV)
+        K.expert_fc2_fwd([a_d] * G, offs_d, True, P, w2_d, [y] * G, split=split)
+        dxp = torch.empty(P, h, dtype=dt, device=DEV)
+        dw1 = [torch.empty_like(w) for w in w1_d]
+        K.expert_fc1_bwd([dh_d] * G, [xp_d] * G, offs_d, True, P, w1_d, f, act, [dxp] * G, dw1, split=split)
+        torch.cuda.synchronize()
+        return y.cpu(), dxp.cpu()
+
+    y_s, dx_s = run(True)
+    y_s2, dx_s2 = run(True)
+    y_n, dx_n = run(False)
+    # the last piece sums in piece order: the same bits on every run
+    assert torch.equal(y_s, y_s2) and torch.equal(dx_s, dx_s2)
+    # split and unsplit differ only in fp32 summation order before the bf16 rounding
+    assert rel_err(y_s, y_n.double()) <= 1e-2 and rel_err(dx_s, dx_n.double()) <= 1e-2
+    c64 = lambda t: t.detach().cpu().double()  # noqa: E731
+    for g in range(G):
+        r0, r1 = int(offs[g]), int(offs[g + 1])
+        sel = torch.tensor([r for r in (rows if rows is not None else range(r0, r1)) if r0 <= r < r1])
+        ref_y = c64(a[sel]) @ c64(w2[g]).t()
+        ref_dx = c64(dh[sel]) @ c64(w1[g])
+        assert rel_err(c64(y_s[sel]), ref_y) <= 1e-2, ("y", g)
+        assert rel_err(c64(dx_s[sel]), ref_dx) <= 1e-2, ("dxp", g)
