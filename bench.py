@@ -1,6 +1,7 @@
 """MoE-layer throughput benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload mixtral|dsv2lite|ep128-share|mixtral-fp8]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload mixtral|dsv2lite|ep128-share|mixtral-fp8|mixtral-adam]
                     [--no-cpu-baseline]
 
 One step is one forward + backward of the MoE layer over one batch of
@@ -13,7 +14,9 @@ shared experts and a sigmoid router with selection bias (dsv2lite), one
 GPU's 16-expert share of a 128-expert top-8 layer under a Zipf(1.1)
 selection prior (ep128-share), and the Mixtral shape with 16384 tokens and
 fp8 experts under delayed scaling (mixtral-fp8; its step includes the end of
-iteration amax-history roll).
+iteration amax-history roll).  ``--workload mixtral-adam`` instead times the
+optimizer step after the layer: one fused Adam step over the Mixtral layer's
+parameters, gradients and moments, against the HBM roofline.
 
 Prints one JSON line: whole-job tokens/s, the grouped-GEMM roofline fraction
 (algorithmic FLOPs / the GEMM kernels' HIP-event time / dense bf16 peak),
@@ -161,6 +164,85 @@ def cpu_baseline(name: str, sample_tokens: int, reps: int = 3) -> dict:
                       f"fwd+bwd, median of {reps} after 1 warm-up; torch {torch.__version__}"}
 
 
+def adam_bench(args) -> int:
+    """The optimizer step after the layer: one fused Adam step (rhp_adam_step) over the Mixtral layer's
+    parameters -- router float32 [8, 4096], 8 experts' fc1 [28672, 4096] and fc2 [4096, 14336] bfloat16 --
+    with their gradients and name-keyed moment state resident in HBM."""
+    pkg = _package()
+    import importlib
+
+    K = importlib.import_module(f"{pkg.__name__}.kernels")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    E, h, f = 8, 4096, 14336
+    shapes = {torch.float32: [(E, h)], torch.bfloat16: [(2 * f, h)] * E + [(h, f)] * E}
+    groups = {}
+    for dt, shp in shapes.items():
+        ps = [(torch.randn(s, generator=g, device=dev, dtype=torch.float32) * 0.02).to(dt) for s in shp]
+        gs = [(torch.randn(s, generator=g, device=dev, dtype=torch.float32) * 1e-3).to(dt) for s in shp]
+        groups[dt] = (ps, gs, [torch.zeros_like(x) for x in ps], [torch.zeros_like(x) for x in ps])
+    n_el = {dt: sum(x.numel() for x in v[0]) for dt, v in groups.items()}
+    step_no = [0]
+
+    def step():
+        step_no[0] += 1
+        for ps, gs, ms, vs in groups.values():
+            K.adam_step(ps, gs, ms, vs, 1e-4, (0.9, 0.95), 1e-8, 0.1, step_no[0])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record(stream)
+    for _ in range(args.steps):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = a.elapsed_time(b) / args.steps
+    elems = sum(n_el.values())
+    nbytes = 14 * n_el[torch.bfloat16] + 28 * n_el[torch.float32]   # p, g, m, v read; p, m, v written
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    result = {
+        "metric": "Adam step parameters/s (Mixtral-8x7B MoE layer parameters, 1 GPU)",
+        "value": elems * args.steps / elapsed, "unit": "parameters/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": elapsed * 1e3 / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 experts, fp32 router (moments in the parameter dtype)",
+        "data": "synthetic (random parameters and gradients drawn on device)",
+        "config": {"workload": f"mixtral-adam: one Adam step (lr 1e-4, betas 0.9/0.95, weight decay 0.1) over "
+                               f"{elems} parameters: router fp32 [8, 4096], 8 x fc1 [28672, 4096] and 8 x fc2 "
+                               f"[4096, 14336] bf16", "parameters": elems},
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": gbps / PEAK_HBM_GBPS, "traffic": None, "kernel": "adam_kernel",
+                     "algorithmic": "14 bytes per bf16 parameter, 28 per fp32 (each array read or written once)"},
+    }
+    if not args.no_cpu_baseline:
+        if str(ROOT) not in sys.path:
+            sys.path.insert(0, str(ROOT))
+        import numpy as np
+        from oracle import adam_c
+
+        n = 1 << 24
+        rng = np.random.default_rng(0)
+        bits = lambda x: (x.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)  # noqa: E731
+        hp, hg = bits(rng.standard_normal(n) * 0.02), bits(rng.standard_normal(n) * 1e-3)
+        hm, hv = np.zeros(n, np.uint16), np.zeros(n, np.uint16)
+        times = []
+        for i in range(4):
+            c0 = time.perf_counter()
+            adam_c.adam_step(hp, hg, hm, hv, 1e-4, (0.9, 0.95), 1e-8, 0.1, i + 1)
+            if i:
+                times.append(time.perf_counter() - c0)
+        med = sorted(times)[len(times) // 2]
+        result["cpu_baseline"] = {"value": n / med, "unit": "parameters/s", "cores": 1, "kind": "port",
+                                  "sample": f"{n} bf16 parameters, C oracle of the same update (one thread), "
+                                            f"median of 3 after 1 warm-up"}
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def copy_probe(nbytes: int) -> int:
     """A plain device copy of a known size: profiled with FETCH_SIZE / WRITE_SIZE, it converts those
     counters into bytes (each copy reads and writes ``nbytes``)."""
@@ -187,7 +269,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="mixtral", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="mixtral", choices=sorted(WORKLOADS) + ["mixtral-adam"])
     ap.add_argument("--cpu-sample", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -199,6 +281,8 @@ def main() -> int:
         print(json.dumps({"error": "this build runs the MoE layer on one GPU; multi-GPU expert parallelism "
                                    "(the all-to-all dispatch) is not part of it", "n_gpus": args.gpus}))
         return 2
+    if args.workload == "mixtral-adam":
+        return adam_bench(args)
     pkg = _package()
     import importlib
 

@@ -229,6 +229,27 @@ int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_offsets, int
                        void* const* dxp, void* const* dw1, void* split_ws, size_t split_ws_bytes,
                        hipStream_t stream);
 
+/* ------------------------------------------------------------------ optimizer step */
+
+/*
+ * One Adam step over `count` tensors of one dtype (F64, F32 or BF16), in
+ * place: resihp/runtime/optim.py:32-46 (the update of
+ * torch.optim.Adam(foreach=False); moment state exp_avg / exp_avg_sq of the
+ * parameter's dtype, as optim.py:24-25 allocates it).  params, exp_avg,
+ * exp_avg_sq and numel are host arrays of `count` entries; grads may be NULL
+ * or hold NULL entries (a parameter without a gradient steps with a zero
+ * gradient, optim.py:38).  `step` is the step number after this update
+ * (optim.py:33: step_count += 1 first), from 1.  Each element evaluates the
+ * operations of optim.py:39-46 in order with their torch roundings, IEEE
+ * square root and division; bfloat16 tensors round every intermediate to
+ * bfloat16 and the weight decay to bfloat16 (torch's add(alpha=)).  All
+ * tensors must be 16-byte aligned.  One pass over the data: 14 bytes per
+ * bfloat16 element (7 per array element read or written once).
+ */
+int rhp_adam_step(int count, void* const* params, const void* const* grads, void* const* exp_avg,
+                  void* const* exp_avg_sq, const int64_t* numel, int dtype, double lr, double beta1, double beta2,
+                  double eps, double weight_decay, int64_t step, hipStream_t stream);
+
 /* ------------------------------------------------------------------ fp8 experts (delayed scaling) */
 
 /*

@@ -9,6 +9,8 @@ device.  Nothing here computes on the CPU; every entry point goes through
 
 from __future__ import annotations
 
+import ctypes
+
 from dataclasses import dataclass
 
 import torch
@@ -373,6 +375,34 @@ def expert_fc1_bwd(dhpre: list[torch.Tensor], xs: list[torch.Tensor], offsets: t
     _call("rhp_expert_fc1_bwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w1[0]),
           act_code(act), h, f, _arr(dhpre), _arr(xs), _arr(w1), _arr(dxs) if dxs else None, _arr(dw1),
           *_split_args(dev, split))
+
+
+# ----------------------------------------------------------------------------- optimizer
+
+
+def adam_step(params: list[torch.Tensor], grads: list[torch.Tensor | None], exp_avg: list[torch.Tensor],
+              exp_avg_sq: list[torch.Tensor], lr: float, betas: tuple[float, float], eps: float,
+              weight_decay: float, step: int) -> None:
+    """One fused Adam step (resihp/runtime/optim.py:32-46) over tensors of one dtype, in place.
+
+    ``step`` is the step number after this update (from 1); a ``None`` gradient steps with zeros.
+    """
+    if not params:
+        return
+    dev = _need_cuda(*params, *[g for g in grads if g is not None], *exp_avg, *exp_avg_sq)
+    dt = params[0].dtype
+    _expect(len(grads) == len(params) == len(exp_avg) == len(exp_avg_sq), "one grad and two moments per parameter")
+    for i, p in enumerate(params):
+        for what, t in (("grad", grads[i]), ("exp_avg", exp_avg[i]), ("exp_avg_sq", exp_avg_sq[i]), ("param", p)):
+            if t is None:
+                continue
+            _expect(t.dtype == dt, f"{what} {i} has dtype {t.dtype}, expected {dt}")
+            _expect(t.shape == p.shape and t.is_contiguous(), f"{what} {i} must be contiguous with the param's shape")
+    numel = (ctypes.c_int64 * len(params))(*[p.numel() for p in params])
+    garr = C.ptr_array([0 if g is None else g.data_ptr() for g in grads])
+    _call("rhp_adam_step", dev, len(params), _arr(params), garr, _arr(exp_avg), _arr(exp_avg_sq), numel,
+          dtype_code(params[0]), float(lr), float(betas[0]), float(betas[1]), float(eps), float(weight_decay),
+          int(step))
 
 
 # ----------------------------------------------------------------------------- fp8 experts

@@ -22,7 +22,6 @@ writes ``router.expert_bias`` until the forward has succeeded.
 
 from __future__ import annotations
 
-import math
 import zlib
 from dataclasses import dataclass
 
@@ -221,19 +220,18 @@ class Adam:
 
     @torch.no_grad()
     def step(self) -> None:
+        """optim.py:32-46 as one fused pass per dtype (rhp_adam_step): the same operations per element,
+        with IEEE square root and division."""
         self.step_count += 1
-        b1, b2 = self.betas
-        bc1 = 1 - b1 ** self.step_count
-        bc2_sqrt = math.sqrt(1 - b2 ** self.step_count)
+        groups: dict[torch.dtype, list[str]] = {}
         for n, p in self.params.items():
-            g = p.grad if p.grad is not None else torch.zeros_like(p)
-            if self.weight_decay:
-                g = g.add(p, alpha=self.weight_decay)
-            s = self.state[n]
-            s["exp_avg"].lerp_(g, 1 - b1)
-            s["exp_avg_sq"].mul_(b2).addcmul_(g, g.conj(), value=1 - b2)
-            denom = (s["exp_avg_sq"].sqrt() / bc2_sqrt).add_(self.eps)
-            p.addcdiv_(s["exp_avg"], denom, value=-self.lr / bc1)
+            if not p.is_cuda:
+                raise RuntimeError(f"Adam: parameter {n} is not on a HIP device; the fused step runs on the GPU")
+            groups.setdefault(p.dtype, []).append(n)
+        for names in groups.values():
+            K.adam_step([self.params[n].data for n in names], [self.params[n].grad for n in names],
+                        [self.state[n]["exp_avg"] for n in names], [self.state[n]["exp_avg_sq"] for n in names],
+                        self.lr, self.betas, self.eps, self.weight_decay, self.step_count)
 
     def state_tensors(self) -> dict[str, torch.Tensor]:
         out: dict[str, torch.Tensor] = {}

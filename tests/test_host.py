@@ -104,3 +104,11 @@ def test_ep_runtime_refuses_cross_gpu_groups():
     with pytest.raises(NotImplementedError):
         rt.forward(torch.zeros(2, 8))
     assert rt.token_range() == (0, 48)
+
+
+def test_adam_refuses_host_parameters():
+    """The fused optimizer step runs on the GPU only: no silent CPU fallback."""
+    opt = moe.Adam({"w": torch.nn.Parameter(torch.zeros(4))})
+    with pytest.raises(RuntimeError, match="HIP device"):
+        opt.step()
+    assert opt.state_tensors().keys() == {"param/w", "exp_avg/w", "exp_avg_sq/w"}
