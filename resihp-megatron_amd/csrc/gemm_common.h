@@ -4,6 +4,8 @@
 #pragma once
 
 #include <algorithm>
+#include <atomic>
+#include <string>
 
 #include "rhp_common.h"
 
@@ -45,6 +47,7 @@ struct Params {
     int32_t* split_cnt;       // [8 * cu_per_xcd] arrival counters, zero between launches
     int split_cap;
     int cu_per_xcd;
+    int split_kstep;          // the kernel's K step: pieces start and end on multiples of it
 };
 
 // ------------------------------------------------------------------ activations
@@ -90,10 +93,18 @@ struct Tile {
 constexpr int kXcds = 8;
 // A split pays only where a tile's reduction is long: each piece publishes
 // a 256 KB partial tile behind an L2-wide release, and the last one reads all
-// of them back.  Measured at K = 1408-4096 (a tile of 22-64 K steps) the split
-// lost up to 8 %, at K = 14336 and 28672 it gained 4 % and 2 %.
-constexpr int kSplitMinK64 = 128;    // K steps of 64 a tile needs to be split at all
-constexpr int kSplitMinSteps = 16;   // K steps of 64 a split piece keeps at least
+// of them back.  Measured at K = 1408-4096 the split lost up to 8 %, at
+// K = 14336 and 28672 it gained 4 % and 2 %.
+constexpr int kSplitMinK = 8192;        // reduction length a tile needs to be split at all
+constexpr int kSplitMinPieceK = 1024;   // reduction length a split piece keeps at least
+
+// K-split workspace: 8 XCDs x up to kSplitMaxCus pieces of one fp32 tile each,
+// then one arrival counter per piece slot.
+constexpr int kSplitMaxCus = 32;   // CUs per XCD the workspace is sized for
+constexpr int kSplitCap = 8;       // pieces per tile at most
+constexpr size_t kSplitSlots = static_cast<size_t>(kXcds) * kSplitMaxCus;
+constexpr size_t kSplitPartBytes = kSplitSlots * kTile * kTile * sizeof(float);
+constexpr size_t kSplitBytes = kSplitPartBytes + kSplitSlots * sizeof(int32_t);
 
 enum TileFound { kTileDone = 0, kTileOk = 1, kTileSkip = 2 };
 
@@ -152,10 +163,9 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
         const uint32_t q = total / kXcds, r = total % kXcds;
         const uint32_t n = q + (x < r ? 1u : 0u), start = x * q + (x < r ? x : r);
         const uint32_t F = n / C * C, rx = n - F;
-        const uint32_t nk = static_cast<uint32_t>((p.K + 63) / 64);
-        uint32_t s = rx && nk >= static_cast<uint32_t>(kSplitMinK64) ? C / rx : 1u;
+        uint32_t s = rx && p.K >= kSplitMinK ? C / rx : 1u;
         s = min(s, static_cast<uint32_t>(p.split_cap));
-        s = min(s, nk / kSplitMinSteps);
+        s = min(s, static_cast<uint32_t>(p.K / kSplitMinPieceK));
         if (j < F || s < 2) {
             if (j >= n) return kTileDone;
             L = start + j;
@@ -188,9 +198,10 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
             t->k_begin = 0;
             t->k_end = p.K;
             if (t->pieces > 1) {
-                const int nk = (p.K + 63) / 64;
-                t->k_begin = (t->piece * nk / t->pieces) * 64;
-                t->k_end = min(p.K, ((t->piece + 1) * nk / t->pieces) * 64);
+                const int ks = p.split_kstep > 0 ? p.split_kstep : 64;
+                const int nk = (p.K + ks - 1) / ks;
+                t->k_begin = (t->piece * nk / t->pieces) * ks;
+                t->k_end = min(p.K, ((t->piece + 1) * nk / t->pieces) * ks);
             }
             // A shared row buffer holds rows_cap rows: never touch rows past it.
             if (p.rows_from_offsets) t->y_lim = min(t->y_lim, p.rows_cap - static_cast<int>(t->row0) - t->y0);
@@ -470,6 +481,10 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
                             v.z += w.z;
                             v.w += w.w;
                         }
+                        v.x *= mul;
+                        v.y *= mul;
+                        v.z *= mul;
+                        v.w *= mul;
                         *reinterpret_cast<float4*>(ep + y * kEpPitchF + x) = v;
                     }
                 }
@@ -518,6 +533,54 @@ __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t
     epilogue_pass<1, MODE, EPI, NT, WY>(p, t, ep, acc, wx, wy, lane, mul, split);
 }
 
+// A piece of a K-split tile: every piece stores its fp32 accumulators (laid
+// out thread-major, so each store instruction of a wave is contiguous), makes
+// them visible device-wide and counts itself in.  The piece that arrives last
+// returns true: its epilogue then stages the sum of all pieces, read from
+// memory in piece order (the same bits whichever piece is last), instead of
+// its own accumulators.  It resets the counter for the next launch.  No block
+// ever waits for another.
+template <int NT, int FY>
+__device__ __forceinline__ bool split_arrive(const Params& p, const Tile& t, const f32x16_t (&acc)[4][FY],
+                                             uint8_t* lds) {
+    constexpr int kVec = 4 * FY * 4;   // float4 per thread
+    static_assert(NT * kVec * 4 == kTile * kTile, "a piece holds a whole tile");
+    const int tid = threadIdx.x;
+    float4* mine = reinterpret_cast<float4*>(p.split_part) + static_cast<size_t>(t.slot + t.piece * t.stride) * (NT * kVec);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < FY; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                mine[((i * FY + j) * 4 + v) * NT + tid] =
+                    make_float4(acc[i][j][4 * v], acc[i][j][4 * v + 1], acc[i][j][4 * v + 2], acc[i][j][4 * v + 3]);
+    // Each wave waits for its own stores; after the barrier one thread makes
+    // the whole block's stores visible device-wide and counts the piece in.
+    // (An agent-scope fence writes back the XCD's L2; one per piece, not one
+    // per wave, keeps it from disturbing the tiles the other CUs stream.)
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();                      // also: every LDS read of the main loop is done
+    int* flag = reinterpret_cast<int*>(lds);
+    if (tid == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const int arrived = __hip_atomic_fetch_add(p.split_cnt + t.slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (arrived == t.pieces - 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            p.split_cnt[t.slot] = 0;   // every piece of this launch has arrived: reset for the next one
+        }
+        flag[0] = arrived;
+    }
+    __syncthreads();
+    return flag[0] == t.pieces - 1;
+}
+
+// The SplitSum of a K-split tile (piece slots of split_part).
+__device__ __forceinline__ SplitSum split_sum_of(const Params& p, const Tile& t) {
+    return SplitSum{reinterpret_cast<const float4*>(p.split_part) + static_cast<size_t>(t.slot) * (kTile * kTile / 4),
+                    t.pieces, static_cast<size_t>(t.stride) * (kTile * kTile / 4)};
+}
+
 // Scheduling hint: MF MFMAs with RD LDS reads spread evenly between them.
 template <int Q, int MF, int RD>
 __device__ __forceinline__ void interleave_reads() {
@@ -561,6 +624,31 @@ __device__ __forceinline__ void wait_loads_all() { __builtin_amdgcn_s_waitcnt(0x
 // slots.  The offset of chunk c is k64_off(r, 0) ^ (c << 4).
 __device__ __forceinline__ uint32_t k64_off(int row, int chunk) {
     return static_cast<uint32_t>(row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4));
+}
+
+// ------------------------------------------------------------------ host helpers of the K split
+
+// CUs per XCD of the current device (cached per device id); 0 if unknown.
+int cus_per_xcd() {
+    static std::atomic<int> cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int c = cache[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        c = std::max(1, cus / kXcds);
+        cache[dev].store(c, std::memory_order_relaxed);
+    }
+    return c;
+}
+
+int check_split_ws(const char* fn, const void* ws, size_t bytes) {
+    if (ws == nullptr) return 0;
+    if (bytes < kSplitBytes || !aligned16(ws))
+        return fail(std::string(fn) + ": split workspace must be 16-byte aligned and hold "
+                    "rhp_expert_split_workspace_bytes() bytes");
+    return 0;
 }
 
 }  // namespace

@@ -22,7 +22,6 @@
 // Work unit: a 256 x 256 output tile.  Tiles are ordered group-major, then by
 // output column block, then by row block, and block ids are remapped so each
 // XCD runs a contiguous range of that order.
-#include <atomic>
 #include <type_traits>
 
 #include "gemm_common.h"
@@ -101,48 +100,6 @@ constexpr int kSlots = 5;
 constexpr int kLdsSlotsBytes = kSlots * kT64Bytes > kEpBytes ? kSlots * kT64Bytes : kEpBytes;
 static_assert(kLdsSlotsBytes <= 163840, "five 32 KB slots");
 constexpr uint32_t kPastView = 0x7ffffff0u;   // soffset that puts every lane past its buffer view
-
-// A piece of a K-split tile: every piece stores its fp32 accumulators (laid
-// out thread-major, so each store instruction of a wave is contiguous), makes
-// them visible device-wide and counts itself in.  The piece that arrives last
-// returns true: its epilogue then stages the sum of all pieces, read from
-// memory in piece order (the same bits whichever piece is last), instead of
-// its own accumulators.  It resets the counter for the next launch.  No block
-// ever waits for another.
-template <int NT, int FY>
-__device__ __forceinline__ bool split_arrive(const Params& p, const Tile& t, const f32x16_t (&acc)[4][FY],
-                                             uint8_t* lds) {
-    constexpr int kVec = 4 * FY * 4;   // float4 per thread
-    static_assert(NT * kVec * 4 == kTile * kTile, "a piece holds a whole tile");
-    const int tid = threadIdx.x;
-    float4* mine = reinterpret_cast<float4*>(p.split_part) + static_cast<size_t>(t.slot + t.piece * t.stride) * (NT * kVec);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < FY; ++j)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                mine[((i * FY + j) * 4 + v) * NT + tid] =
-                    make_float4(acc[i][j][4 * v], acc[i][j][4 * v + 1], acc[i][j][4 * v + 2], acc[i][j][4 * v + 3]);
-    // Each wave waits for its own stores; after the barrier one thread makes
-    // the whole block's stores visible device-wide and counts the piece in.
-    // (An agent-scope fence writes back the XCD's L2; one per piece, not one
-    // per wave, keeps it from disturbing the tiles the other CUs stream.)
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-    __syncthreads();                      // also: every LDS read of the main loop is done
-    int* flag = reinterpret_cast<int*>(lds);
-    if (tid == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const int arrived = __hip_atomic_fetch_add(p.split_cnt + t.slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (arrived == t.pieces - 1) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            p.split_cnt[t.slot] = 0;   // every piece of this launch has arrived: reset for the next one
-        }
-        flag[0] = arrived;
-    }
-    __syncthreads();
-    return flag[0] == t.pieces - 1;
-}
 
 // One tile: the K loop through the slot ring, then the epilogue (or, for a
 // piece of a K-split tile, the hand-over to the piece that finishes last).
@@ -354,9 +311,7 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
     }
     if (MODE != kWgrad && t.pieces > 1) {
         if (!split_arrive<64 * NW, FY>(p, t, acc, lds)) return;
-        const SplitSum sum{reinterpret_cast<const float4*>(p.split_part) + static_cast<size_t>(t.slot) * (kTile * kTile / 4),
-                           t.pieces, static_cast<size_t>(t.stride) * (kTile * kTile / 4)};
-        epilogue<MODE, EPI, 64 * NW, WY>(p, t, lds, acc, wx, wy, lane, 1.0f, sum);
+        epilogue<MODE, EPI, 64 * NW, WY>(p, t, lds, acc, wx, wy, lane, 1.0f, split_sum_of(p, t));
         return;
     }
     epilogue<MODE, EPI, 64 * NW, WY>(p, t, lds, acc, wx, wy, lane);
@@ -452,29 +407,6 @@ struct Job {
     int cus_per_xcd;  // CUs per XCD of the device the launch runs on
 };
 
-// K-split workspace: 8 XCDs x up to kSplitMaxCus pieces of one fp32 tile each,
-// then one arrival counter per piece slot.
-constexpr int kSplitMaxCus = 32;   // CUs per XCD the workspace is sized for
-constexpr int kSplitCap = 8;       // pieces per tile at most
-constexpr size_t kSplitSlots = static_cast<size_t>(kXcds) * kSplitMaxCus;
-constexpr size_t kSplitPartBytes = kSplitSlots * kTile * kTile * sizeof(float);
-constexpr size_t kSplitBytes = kSplitPartBytes + kSplitSlots * sizeof(int32_t);
-
-// CUs per XCD of the current device (cached per device id); 0 if unknown.
-int cus_per_xcd() {
-    static std::atomic<int> cache[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    int c = cache[dev].load(std::memory_order_relaxed);
-    if (c == 0) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-        c = std::max(1, cus / kXcds);
-        cache[dev].store(c, std::memory_order_relaxed);
-    }
-    return c;
-}
-
 template <int MODE, int EPI>
 unsigned mfma_blocks(const Params& p, int64_t rows_cap) {
     const int64_t xt = (p.N + x_per_tile<EPI>() - 1) / x_per_tile<EPI>();
@@ -553,13 +485,14 @@ int run(const Job& job, const char* what, hipStream_t s) {
         p.rows_cap = static_cast<int>(j.rows_cap);
         // Only reductions long enough to be split get the split (and its larger
         // grid: the extra, mostly empty blocks cost about 1 % of a short product).
-        if (j.split_ws && j.mfma && j.mode != kWgrad && j.K >= kSplitMinK64 * 64) {
+        if (j.split_ws && j.mfma && j.mode != kWgrad && j.K >= kSplitMinK) {
             const int C = std::min(kSplitMaxCus, j.cus_per_xcd);
             if (C > 1) {
                 p.split_part = static_cast<float*>(j.split_ws);
                 p.split_cnt = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(j.split_ws) + kSplitPartBytes);
                 p.split_cap = kSplitCap;
                 p.cu_per_xcd = C;
+                p.split_kstep = 64;
             }
         }
         launch(j, p, s);
@@ -602,14 +535,6 @@ bool mfma_ok(int dtype, int h, int f, int act, int64_t rows_cap) {
     const int64_t limit = int64_t(1) << 31;
     return dtype == RHP_BF16 && h % 64 == 0 && f % 64 == 0 && rows_cap * widest * 2 < limit && F1 * h * 2 < limit &&
            kTile * widest * 2 < limit;
-}
-
-int check_split_ws(const char* fn, const void* ws, size_t bytes) {
-    if (ws == nullptr) return 0;
-    if (bytes < kSplitBytes || !aligned16(ws))
-        return fail(std::string(fn) + ": split workspace must be 16-byte aligned and hold "
-                    "rhp_expert_split_workspace_bytes() bytes");
-    return 0;
 }
 
 }  // namespace
