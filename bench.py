@@ -49,7 +49,8 @@ WORKLOADS = {
     "mixtral-fp8": (16384, 4096, 14336, 8, 2, "softmax", 0, None, 1, None, True),
 }
 
-GEMM_CALLS = ("rhp_expert_fc1_fwd", "rhp_expert_fc2_fwd", "rhp_expert_fc2_bwd", "rhp_expert_fc1_bwd", "rhp_fp8_gemm")
+GEMM_CALLS = ("rhp_expert_fc1_fwd", "rhp_expert_fc2_fwd", "rhp_expert_fc2_bwd", "rhp_expert_fc1_bwd", "rhp_fp8_gemm",
+              "rhp_fp8_gemm_cast")
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 
 

@@ -307,6 +307,28 @@ int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets, int64_t ro
                  void* const* c, int64_t ldc, void* const* c2, int64_t ldc2, const void* const* aux, int64_t ldaux,
                  const float* y_scale_inv, const float* x_scale_inv, int x_scale_stride, hipStream_t stream);
 
+/*
+ * A row-grouped rhp_fp8_gemm (kgroups = 0) whose epilogue casts its bf16
+ * activation output straight to fp8, fusing the cast that the next products
+ * need (the quantise step of the fp8 recipe, reference_model.py:204-207, on
+ * the expert FFN of moe.py:82-83 and its backward):
+ *   epi 1 / 2 (SwiGLU / GELU forward): c = hpre (bf16, as rhp_fp8_gemm); the
+ *            activation [rows, N] is cast instead of stored (no c2);
+ *   epi 3 / 4 (SwiGLU / GELU backward): aux = hpre; the pre-activation gradient
+ *            ([rows, 2N] SwiGLU, [rows, N] GELU) is cast instead of stored (c = NULL).
+ * The cast takes poff, history, hist_len, q_fmt, margin, amax_bits, scale_inv,
+ * q and qt with the meaning of rhp_fp8_cast (cols = the cast output's columns,
+ * the same offsets).  Results are bit for bit those of rhp_fp8_gemm followed by
+ * rhp_fp8_cast of its bf16 output.  Formats: y e4m3 and q e4m3 forward, y e5m2
+ * and q e5m2 backward; x e4m3.
+ */
+int rhp_fp8_gemm_cast(int epi, int G, const int32_t* offsets, const int32_t* poff, int64_t rows_cap, int y_fmt,
+                      int x_fmt, int N, int K, int f, const void* const* y, int64_t ldy, const void* const* x,
+                      int64_t ldx, void* const* c, int64_t ldc, const void* const* aux, int64_t ldaux,
+                      const float* y_scale_inv, const float* x_scale_inv, int x_scale_stride, const float* history,
+                      int hist_len, int q_fmt, int margin, uint32_t* amax_bits, float* scale_inv, void* q, void* qt,
+                      hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

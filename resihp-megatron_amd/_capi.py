@@ -49,6 +49,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "rhp_fp8_amax_roll": (_i, [_p, _p, _i, _i, _p]),
     "rhp_fp8_gemm": (_i, [_i, _i, _i, _p, _i64, _i, _i, _i, _i, _i, _i, _pp, _i64, _pp, _i64, _pp, _i64, _pp, _i64,
                           _pp, _i64, _p, _p, _i, _p]),
+    "rhp_fp8_gemm_cast": (_i, [_i, _i, _p, _p, _i64, _i, _i, _i, _i, _i, _pp, _i64, _pp, _i64, _pp, _i64, _pp, _i64,
+                               _p, _p, _i, _p, _i, _i, _i, _p, _p, _p, _p, _p]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -28,38 +28,6 @@
 namespace rhp {
 namespace {
 
-constexpr int kFmtE4m3 = 0;   // MFMA operand format codes (cbsz / blgp)
-constexpr int kFmtE5m2 = 1;
-
-__host__ __device__ constexpr float fp8_max(int fmt) { return fmt == kFmtE4m3 ? 448.0f : 57344.0f; }
-
-// scale = fp8_max / max(history) / 2^margin, evaluated in double and rounded
-// once to float; 1 when the maximum is not a positive finite number.
-__device__ __forceinline__ float history_scale(const float* hist, int L, float fmax, int margin) {
-    float a = -__builtin_huge_valf();
-    bool nan = false;
-    for (int i = 0; i < L; ++i) {
-        const float v = hist[i];
-        nan |= v != v;
-        a = v > a ? v : a;
-    }
-    if (nan || !(a > 0.0f) || a == __builtin_huge_valf()) return 1.0f;
-    return static_cast<float>(static_cast<double>(fmax) / static_cast<double>(a) / __builtin_ldexp(1.0, margin));
-}
-
-template <int FMT>
-__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
-    uint32_t w;
-    if (FMT == kFmtE4m3) {
-        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
-        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(w), true));
-    } else {
-        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false));
-        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(c, d, static_cast<int>(w), true));
-    }
-    return w;
-}
-
 // ------------------------------------------------------------------ cast + transpose
 
 struct CastParams {
@@ -79,19 +47,6 @@ struct CastParams {
 
 constexpr int kCastRows = 128;   // rows of one block's tile (row tiles of an expert: padded rows / 128)
 constexpr int kCastCols = 128;   // columns of one block's tile (partial tiles mask 64-column segments)
-
-// 4 x 4 byte transpose: word j holds bytes (row j, cols 0..3); word i of the
-// result holds bytes (rows 0..3, col i).
-__device__ __forceinline__ void transpose4x4(const uint32_t a[4], uint32_t b[4]) {
-    const uint32_t t0 = __builtin_amdgcn_perm(a[1], a[0], 0x05010400u);   // a0.0 a1.0 a0.1 a1.1
-    const uint32_t t1 = __builtin_amdgcn_perm(a[1], a[0], 0x07030602u);   // a0.2 a1.2 a0.3 a1.3
-    const uint32_t t2 = __builtin_amdgcn_perm(a[3], a[2], 0x05010400u);   // a2.0 a3.0 a2.1 a3.1
-    const uint32_t t3 = __builtin_amdgcn_perm(a[3], a[2], 0x07030602u);   // a2.2 a3.2 a2.3 a3.3
-    b[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-    b[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-    b[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-    b[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-}
 
 // One block: 128 rows x 128 columns of one expert, wave w owning rows 32 w ..
 // +31.  Load i of lane l reads row 32 w + 4 i + l / 16, columns 8 (l % 16) ..
@@ -289,9 +244,14 @@ __device__ __forceinline__ i32x8_t f8_frag(const uint8_t* tile, uint32_t fr, int
     return v;
 }
 
-template <int MODE, int EPI, int YF, int XF>
+template <int MODE, int EPI, int YF, int XF, int QF>
 __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
     __shared__ __align__(1024) uint8_t lds[kF8LdsBytes];
+    if constexpr (QF >= 0) {
+        // The quantising epilogue's 1 / scale, written once (block 0 exists in every launch).
+        if (blockIdx.x == 0 && threadIdx.x == 0)
+            *p.q_scale_inv = 1.0f / history_scale(p.q_hist, p.q_L, fp8_max(QF), p.q_margin);
+    }
     Tile t;
     if (find_tile<MODE>(p, x_per_tile<EPI>(), kTile, blockIdx.x, &t) != kTileOk) return;
     t.g = __builtin_amdgcn_readfirstlane(t.g);
@@ -439,12 +399,30 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
         wait_loads_all();   // the tiles past the last step
     }
     const float mul = p.scale_inv_y[0] * p.scale_inv_x[g * p.scale_x_stride];
-    epilogue<MODE, EPI>(p, t, lds, acc, wx, wy, lane, mul);
+    epilogue<MODE, EPI, kThreadsMfma, kWaveY, QF>(p, t, lds, acc, wx, wy, lane, mul);
 }
 
-template <int MODE, int EPI, int YF, int XF>
+template <int MODE, int EPI, int YF, int XF, int QF = -1>
 void launch_fp8(const Params& p, unsigned nb, hipStream_t s) {
-    hipLaunchKernelGGL((gg_fp8_kernel<MODE, EPI, YF, XF>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+    hipLaunchKernelGGL((gg_fp8_kernel<MODE, EPI, YF, XF, QF>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+}
+
+// The quantising combinations: activations cast to e4m3 in the forward,
+// pre-activation gradients to e5m2 in the backward.
+bool launch_fp8_quant(int epi, int yf, int xf, int qf, const Params& p, unsigned nb, hipStream_t s) {
+    if (xf != kFmtE4m3) return false;
+    if (epi == kEpiSwigluFwd && yf == kFmtE4m3 && qf == kFmtE4m3) {
+        launch_fp8<kFwd, kEpiSwigluFwd, kFmtE4m3, kFmtE4m3, kFmtE4m3>(p, nb, s);
+    } else if (epi == kEpiGeluFwd && yf == kFmtE4m3 && qf == kFmtE4m3) {
+        launch_fp8<kFwd, kEpiGeluFwd, kFmtE4m3, kFmtE4m3, kFmtE4m3>(p, nb, s);
+    } else if (epi == kEpiSwigluBwd && yf == kFmtE5m2 && qf == kFmtE5m2) {
+        launch_fp8<kFwd, kEpiSwigluBwd, kFmtE5m2, kFmtE4m3, kFmtE5m2>(p, nb, s);
+    } else if (epi == kEpiGeluBwd && yf == kFmtE5m2 && qf == kFmtE5m2) {
+        launch_fp8<kFwd, kEpiGeluBwd, kFmtE5m2, kFmtE4m3, kFmtE5m2>(p, nb, s);
+    } else {
+        return false;
+    }
+    return true;
 }
 
 // The (mode, epilogue, formats) combinations the expert layer uses.
@@ -528,20 +506,32 @@ extern "C" int rhp_fp8_amax_roll(float* history, uint32_t* amax_bits, int n, int
     return check_launch("rhp_fp8_amax_roll");
 }
 
-extern "C" int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt,
-                            int x_fmt, int N, int K, int Mo, int f, const void* const* y, int64_t ldy,
-                            const void* const* x, int64_t ldx, void* const* c, int64_t ldc, void* const* c2,
-                            int64_t ldc2, const void* const* aux, int64_t ldaux, const float* y_scale_inv,
-                            const float* x_scale_inv, int x_scale_stride, hipStream_t stream) {
-    clear_error();
+namespace {
+
+// The cast a quantising epilogue applies (rhp_fp8_gemm_cast).
+struct CastOut {
+    const int32_t* poff;
+    const float* history;
+    int hist_len, fmt, margin;
+    uint32_t* amax_bits;
+    float* scale_inv;
+    uint8_t* q;
+    uint8_t* qt;
+};
+
+int fp8_gemm_run(int kgroups, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt, int x_fmt, int N,
+                 int K, int Mo, int f, const void* const* y, int64_t ldy, const void* const* x, int64_t ldx,
+                 void* const* c, int64_t ldc, void* const* c2, int64_t ldc2, const void* const* aux, int64_t ldaux,
+                 const float* y_scale_inv, const float* x_scale_inv, int x_scale_stride, const CastOut* cast,
+                 hipStream_t stream) {
     const int yf = fp8_fmt(y_fmt), xf = fp8_fmt(x_fmt);
     RHP_REQUIRE(yf >= 0 && xf >= 0, "rhp_fp8_gemm: operand formats must be RHP_E4M3 or RHP_E5M2");
     RHP_REQUIRE(G >= 1 && G <= RHP_MAX_GROUPS_PER_LAUNCH, "rhp_fp8_gemm: 1 to 64 groups per call");
-    RHP_REQUIRE(offsets && y && x && c && y_scale_inv && x_scale_inv, "rhp_fp8_gemm: null pointer");
+    RHP_REQUIRE(offsets && y && x && (c || cast) && y_scale_inv && x_scale_inv, "rhp_fp8_gemm: null pointer");
     RHP_REQUIRE(x_scale_stride == 0 || x_scale_stride == 1, "rhp_fp8_gemm: x scale stride must be 0 or 1");
     RHP_REQUIRE(N > 0 && N % 64 == 0, "rhp_fp8_gemm: N must be a positive multiple of 64");
     RHP_REQUIRE(rows_cap >= 0 && rows_cap < (int64_t(1) << 31), "rhp_fp8_gemm: rows_cap out of range");
-    RHP_REQUIRE(ldc > 0 && ldc < (int64_t(1) << 31), "rhp_fp8_gemm: bad ldc");
+    RHP_REQUIRE(!c || (ldc > 0 && ldc < (int64_t(1) << 31)), "rhp_fp8_gemm: bad ldc");
     // The epilogue writes (and reads aux) through views of kTile rows with 32-bit byte offsets.
     RHP_REQUIRE(std::max({ldc, ldc2, ldaux}) * 2 * kTile < (int64_t(1) << 31),
                 "rhp_fp8_gemm: output, activation and pre-activation rows must be narrower than 2^22 elements");
@@ -554,8 +544,8 @@ extern "C" int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets,
         p.b[g] = x[g];
     }
     for (int g = 0; g < G; ++g) {
-        RHP_REQUIRE(c[g] != nullptr, "rhp_fp8_gemm: null output");
-        p.c[g] = c[g];
+        RHP_REQUIRE(cast || c[g] != nullptr, "rhp_fp8_gemm: null output");
+        p.c[g] = c ? c[g] : nullptr;
         p.c2[g] = c2 ? c2[g] : nullptr;
         p.aux[g] = aux ? aux[g] : nullptr;
     }
@@ -570,7 +560,8 @@ extern "C" int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets,
         const int64_t xrows = epi == kEpiSwigluFwd ? 2 * int64_t(f) : N;
         RHP_REQUIRE(rows_cap * ldy < (int64_t(1) << 31) && xrows * ldx < (int64_t(1) << 31),
                     "rhp_fp8_gemm: operands must stay below 2 GiB");
-        if (epi == kEpiSwigluFwd || epi == kEpiGeluFwd) RHP_REQUIRE(c2 != nullptr, "rhp_fp8_gemm: activation output missing");
+        if ((epi == kEpiSwigluFwd || epi == kEpiGeluFwd) && !cast)
+            RHP_REQUIRE(c2 != nullptr, "rhp_fp8_gemm: activation output missing");
         if (epi == kEpiSwigluBwd || epi == kEpiGeluBwd) RHP_REQUIRE(aux != nullptr, "rhp_fp8_gemm: pre-activation input missing");
         if (epi == kEpiSwigluFwd || epi == kEpiSwigluBwd) RHP_REQUIRE(f == N && f % 64 == 0, "rhp_fp8_gemm: SwiGLU needs N == f");
     }
@@ -593,7 +584,62 @@ extern "C" int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets,
     const int64_t xt = (N + (epi == kEpiSwigluFwd ? 127 : 255)) / (epi == kEpiSwigluFwd ? 128 : 256);
     const int64_t nb = kgroups ? G * xt * ((Mo + kTile - 1) / kTile) : ((rows_cap + kTile - 1) / kTile + G) * xt;
     if (nb == 0) return 0;
+    if (cast) {
+        p.q = cast->q;
+        p.qt = cast->qt;
+        p.q_poff = cast->poff;
+        p.q_hist = cast->history;
+        p.q_amax = cast->amax_bits;
+        p.q_scale_inv = cast->scale_inv;
+        p.q_ld = epi == kEpiSwigluBwd ? 2 * N : N;
+        p.q_L = cast->hist_len;
+        p.q_margin = cast->margin;
+        RHP_REQUIRE(launch_fp8_quant(epi, yf, xf, fp8_fmt(cast->fmt), p, static_cast<unsigned>(nb), stream),
+                    "rhp_fp8_gemm_cast: unsupported combination of epilogue and formats");
+        return check_launch("rhp_fp8_gemm_cast");
+    }
     RHP_REQUIRE(launch_fp8_any(mode, epi, yf, xf, p, static_cast<unsigned>(nb), stream),
                 "rhp_fp8_gemm: unsupported combination of product, epilogue and formats");
     return check_launch("rhp_fp8_gemm");
+}
+
+}  // namespace
+
+extern "C" int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt,
+                            int x_fmt, int N, int K, int Mo, int f, const void* const* y, int64_t ldy,
+                            const void* const* x, int64_t ldx, void* const* c, int64_t ldc, void* const* c2,
+                            int64_t ldc2, const void* const* aux, int64_t ldaux, const float* y_scale_inv,
+                            const float* x_scale_inv, int x_scale_stride, hipStream_t stream) {
+    clear_error();
+    return fp8_gemm_run(kgroups, epi, G, offsets, rows_cap, y_fmt, x_fmt, N, K, Mo, f, y, ldy, x, ldx, c, ldc, c2,
+                        ldc2, aux, ldaux, y_scale_inv, x_scale_inv, x_scale_stride, nullptr, stream);
+}
+
+extern "C" int rhp_fp8_gemm_cast(int epi, int G, const int32_t* offsets, const int32_t* poff, int64_t rows_cap,
+                                 int y_fmt, int x_fmt, int N, int K, int f, const void* const* y, int64_t ldy,
+                                 const void* const* x, int64_t ldx, void* const* c, int64_t ldc,
+                                 const void* const* aux, int64_t ldaux, const float* y_scale_inv,
+                                 const float* x_scale_inv, int x_scale_stride, const float* history, int hist_len,
+                                 int q_fmt, int margin, uint32_t* amax_bits, float* scale_inv, void* q, void* qt,
+                                 hipStream_t stream) {
+    clear_error();
+    const bool fwd = epi == kEpiSwigluFwd || epi == kEpiGeluFwd;
+    RHP_REQUIRE(fwd || epi == kEpiSwigluBwd || epi == kEpiGeluBwd,
+                "rhp_fp8_gemm_cast: the epilogue must be an activation forward or backward (1 to 4)");
+    RHP_REQUIRE(fp8_fmt(q_fmt) >= 0, "rhp_fp8_gemm_cast: format must be RHP_E4M3 or RHP_E5M2");
+    RHP_REQUIRE(poff && history && amax_bits && scale_inv, "rhp_fp8_gemm_cast: null pointer");
+    RHP_REQUIRE(q || qt, "rhp_fp8_gemm_cast: nothing to write");
+    RHP_REQUIRE(hist_len >= 1 && margin >= 0 && margin < 64, "rhp_fp8_gemm_cast: bad history or margin");
+    RHP_REQUIRE((!q || aligned16(q)) && (!qt || aligned16(qt)), "rhp_fp8_gemm_cast: outputs must be 16-byte aligned");
+    RHP_REQUIRE(fwd ? c != nullptr : c == nullptr,
+                "rhp_fp8_gemm_cast: forward epilogues store the pre-activation in c, backward ones store no bf16 output");
+    RHP_REQUIRE(N > 0 && N < (int64_t(1) << 21), "rhp_fp8_gemm_cast: N out of range");
+    const int64_t cols = epi == kEpiSwigluBwd ? 2 * int64_t(N) : N;
+    // Code rows are addressed with 32-bit byte offsets, row-major and transposed.
+    RHP_REQUIRE(rows_cap >= 0 && (rows_cap + 128 * int64_t(G)) * cols < (int64_t(1) << 31),
+                "rhp_fp8_gemm_cast: quantised outputs must stay below 2 GiB");
+    const CastOut cast{poff, history, hist_len, q_fmt, margin, amax_bits, scale_inv, static_cast<uint8_t*>(q),
+                       static_cast<uint8_t*>(qt)};
+    return fp8_gemm_run(0, epi, G, offsets, rows_cap, y_fmt, x_fmt, N, K, 0, f, y, ldy, x, ldx, c, ldc, nullptr, 0,
+                        aux, ldaux, y_scale_inv, x_scale_inv, x_scale_stride, &cast, stream);
 }

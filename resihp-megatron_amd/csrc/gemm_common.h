@@ -48,6 +48,20 @@ struct Params {
     int split_cap;
     int cu_per_xcd;
     int split_kstep;          // the kernel's K step: pieces start and end on multiples of it
+    // Quantising epilogues (fp8 kernels): the activation (forward) or the
+    // pre-activation gradient (backward) leaves as fp8 codes instead of bf16,
+    // cast with the delayed scale of q_hist exactly as the cast kernel casts
+    // the bf16 rows: row-major to q (q_ld bytes a row) and, per group,
+    // transposed to qt (group g: [q_ld][R_g] at qt + q_ld * poff[g], R_g =
+    // q_poff[g + 1] - q_poff[g], rows past the group's count zero), raising
+    // *q_amax to the largest magnitude.  Either of q and qt may be null.
+    uint8_t* q;
+    uint8_t* qt;
+    const int32_t* q_poff;
+    const float* q_hist;
+    uint32_t* q_amax;
+    float* q_scale_inv;
+    int q_ld, q_L, q_margin;
 };
 
 // ------------------------------------------------------------------ activations
@@ -286,6 +300,53 @@ __device__ __forceinline__ void load_bf16x4(const uint16_t* p, float* o) {
 
 constexpr uint32_t kOutOfRange = 0x80000000u;   // a buffer offset past every view: loads read zero, stores drop
 
+// ------------------------------------------------------------------ fp8 codes
+
+constexpr int kFmtE4m3 = 0;   // MFMA operand format codes (cbsz / blgp)
+constexpr int kFmtE5m2 = 1;
+
+__host__ __device__ constexpr float fp8_max(int fmt) { return fmt == kFmtE4m3 ? 448.0f : 57344.0f; }
+
+// scale = fp8_max / max(history) / 2^margin, evaluated in double and rounded
+// once to float; 1 when the maximum is not a positive finite number.
+__device__ __forceinline__ float history_scale(const float* hist, int L, float fmax, int margin) {
+    float a = -__builtin_huge_valf();
+    bool nan = false;
+    for (int i = 0; i < L; ++i) {
+        const float v = hist[i];
+        nan |= v != v;
+        a = v > a ? v : a;
+    }
+    if (nan || !(a > 0.0f) || a == __builtin_huge_valf()) return 1.0f;
+    return static_cast<float>(static_cast<double>(fmax) / static_cast<double>(a) / __builtin_ldexp(1.0, margin));
+}
+
+template <int FMT>
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
+    uint32_t w;
+    if (FMT == kFmtE4m3) {
+        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
+        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(w), true));
+    } else {
+        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false));
+        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(c, d, static_cast<int>(w), true));
+    }
+    return w;
+}
+
+// 4 x 4 byte transpose: word j holds bytes (row j, cols 0..3); word i of the
+// result holds bytes (rows 0..3, col i).
+__device__ __forceinline__ void transpose4x4(const uint32_t a[4], uint32_t b[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(a[1], a[0], 0x05010400u);   // a0.0 a1.0 a0.1 a1.1
+    const uint32_t t1 = __builtin_amdgcn_perm(a[1], a[0], 0x07030602u);   // a0.2 a1.2 a0.3 a1.3
+    const uint32_t t2 = __builtin_amdgcn_perm(a[3], a[2], 0x05010400u);   // a2.0 a3.0 a2.1 a3.1
+    const uint32_t t3 = __builtin_amdgcn_perm(a[3], a[2], 0x07030602u);   // a2.2 a3.2 a2.3 a3.3
+    b[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    b[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    b[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    b[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+
 // Epilogue staging: half a tile of fp32 accumulators, rows padded by 16 bytes
 // so that the 16 lanes of a ds_write_b128 (16 consecutive rows) hit distinct
 // bank groups.
@@ -443,6 +504,179 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
     }
 }
 
+// ------------------------------------------------------------------ quantising epilogue
+
+// The cast's scale (the same in every block) and this thread's running
+// maximum of |output|.
+struct QuantAcc {
+    float scale;
+    float m;
+};
+
+// Four outputs of a piece as fp8 codes.  They are rounded to bf16 first,
+// exactly as the bf16 epilogue stores them, and then cast as the cast kernel
+// casts a bf16 row, so codes and amax equal those of the unfused pair.
+// valid = false (a row past the group's rows, a column past the tile's)
+// makes the piece zero, as the cast kernel reads such rows.
+template <int QF>
+__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, bool valid, QuantAcc& qa) {
+    const uint32_t w0 = pack_bf16x2(a, b), w1 = pack_bf16x2(c, d);
+    float v[4] = {__uint_as_float(w0 << 16), __uint_as_float(w0 & 0xffff0000u), __uint_as_float(w1 << 16),
+                  __uint_as_float(w1 & 0xffff0000u)};
+    const float lim = fp8_max(QF);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = valid ? v[e] : 0.0f;
+    // The maximum is exact in any order (NaN never wins), so the piece's four go in as one.
+    qa.m = fmaxf(qa.m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    asm volatile("" : "+v"(qa.m));   // fold it in here: sunk to its one use, every value would stay live
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = fminf(fmaxf(v[e] * qa.scale, -lim), lim);
+    return pack4<QF>(v[0], v[1], v[2], v[3]);
+}
+
+// A byte view of a tile's rows of the row-major codes (see tile_view); an
+// empty view when there is no row-major output, so every store drops.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t code_view(uint8_t* base, int64_t first, int ld, int x0, int rows) {
+    if (!base) return __builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc(base + first * ld + x0, 0, min(rows, kTile) * ld, 0x00020000);
+}
+
+// Where a quantising epilogue keeps code word w of row r of a half: in the
+// row's own staging space, which only the wave that computes the row reads,
+// so a wave overwrites a row as soon as it has read it.  Rows of 16-row
+// chunk c start 8 c words further in, so that the transposed reads below
+// (eight chunks by eight word columns a wave) fall in distinct banks.
+__device__ __forceinline__ int code_word(int r, int w) { return r * kEpPitchF + w + 8 * (r >> 4); }
+
+// The transposed codes of one half (rows [r0, r0 + 128) of the tile), W
+// words a row (code_word); word w of a row holds columns 4 (w % WP) .. + 3
+// of output part w / WP (part 1 starts at column f).  Work item b covers word
+// column b / 8 and rows 16 (b % 8) .. + 15: a thread reads 16 words,
+// transposes four 4 x 4 byte blocks and stores 16 bytes to each of 4
+// transposed rows, so eight consecutive threads fill one 128-byte line.  A
+// half that holds a row of the group is written whole: rows past the group's
+// count are zero codes, the padding of the transposed copy (its rows are the
+// group's count rounded up to 128).
+template <int W, int WP, int NT>
+__device__ __forceinline__ void store_transposed_half(const Params& p, const Tile& t, const float* tw, int r0) {
+    if (!p.qt || r0 >= t.y_lim) return;
+    const int pg = p.q_poff[t.g];
+    const int R = p.q_poff[t.g + 1] - pg;
+    uint8_t* base = p.qt + static_cast<int64_t>(p.q_ld) * pg + t.y0 + r0;
+#pragma unroll
+    for (int k = 0; k < (W * 8 + NT - 1) / NT; ++k) {
+        const int b = static_cast<int>(threadIdx.x) + k * NT;
+        const int chunk = b & 7, cw = b >> 3;
+        const int cl = 4 * (cw % WP);
+        if (b < W * 8 && cl < t.x_lim) {
+            uint32_t a[16], o[4][4];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a[j] = __float_as_uint(tw[code_word(16 * chunk + j, cw)]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t bq[4];
+                transpose4x4(a + 4 * q, bq);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[i][q] = bq[i];
+            }
+            uint8_t* dst = base + static_cast<int64_t>((cw / WP) * p.f + t.x0 + cl) * R + 16 * chunk;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(i) * R) = make_uint4(o[i][0], o[i][1], o[i][2], o[i][3]);
+        }
+    }
+}
+
+// epilogue_half with a quantising output.  The forward epilogues still store
+// the pre-activation (bf16, for the backward) and send the activation to the
+// codes; the backward epilogues send their one output, the pre-activation
+// gradient (SwiGLU: gate part at column x, up part at f + x), to the codes.
+// Every staged row is read by one wave only, which puts the row's codes in
+// its place (code_word) for the transposed copy.
+template <int MODE, int EPI, int NT, int QF>
+__device__ __forceinline__ void epilogue_half_q(const Params& p, const Tile& t, float* ep, int r0,
+                                                const AuxHalf<EPI, NT>& aux, QuantAcc& qa) {
+    const int g = t.g;
+    const int64_t first = tile_first_row<MODE>(t);
+    const __amdgpu_buffer_rsrc_t qv = code_view(p.q, first, p.q_ld, t.x0, t.y_lim);
+    if constexpr (EPI == kEpiSwigluFwd) {
+        // Thread t covers activation columns 4 (t % 32) .. + 3 of rows r0 + t / 32 + (NT / 32) n.
+        constexpr int kW = 32, kN = kEpRows * 32 / NT;
+        const __amdgpu_buffer_rsrc_t hv = tile_view(p.c[g], first, p.ldc, t.x0, t.y_lim);
+        const int rr = threadIdx.x >> 5, a = (threadIdx.x & 31) * 4;
+        const int xg = (a >> 6) * 128 + (a & 63);
+        const bool ok = a < t.x_lim;
+        uint32_t oh = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc + a) * 2) : kOutOfRange;
+        uint32_t oq = ok ? static_cast<uint32_t>((r0 + rr) * p.q_ld + a) : kOutOfRange;
+        const uint32_t sh = static_cast<uint32_t>((NT / 32) * p.ldc * 2), sq = static_cast<uint32_t>((NT / 32) * p.q_ld);
+        const uint32_t up = static_cast<uint32_t>(p.f * 2);
+#pragma unroll
+        for (int n = 0; n < kN; ++n, oh += sh, oq += sq) {
+            const int r = rr + n * (NT / 32);
+            const float4 gv = lds_f4(ep, r, xg), uv = lds_f4(ep, r, xg + 64);
+            view_store_bf16x4(hv, oh, 0, gv.x, gv.y, gv.z, gv.w);
+            view_store_bf16x4(hv, oh, up, uv.x, uv.y, uv.z, uv.w);
+            const uint32_t code = quant4<QF>(silu_f(gv.x) * uv.x, silu_f(gv.y) * uv.y, silu_f(gv.z) * uv.z,
+                                             silu_f(gv.w) * uv.w, ok && r0 + r < t.y_lim, qa);
+            __builtin_amdgcn_raw_buffer_store_b32(code, qv, static_cast<int>(oq), 0, 0);
+            ep[code_word(r, threadIdx.x & 31)] = __uint_as_float(code);
+        }
+        lds_barrier();
+        store_transposed_half<kW, kW, NT>(p, t, ep, r0);
+    } else {
+        // Thread t covers columns 4 (t % 64) .. + 3 of rows r0 + t / 64 + (NT / 64) n.
+        constexpr int kParts = EPI == kEpiSwigluBwd ? 2 : 1, kW = 64 * kParts, kN = kEpRows * 64 / NT;
+        const int rr = threadIdx.x >> 6, x = (threadIdx.x & 63) * 4;
+        const bool ok = x < t.x_lim;
+        __amdgpu_buffer_rsrc_t hv = qv;
+        uint32_t oh = 0, sh = 0;
+        if constexpr (EPI == kEpiGeluFwd) {
+            hv = tile_view(p.c[g], first, p.ldc, t.x0, t.y_lim);
+            oh = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc + x) * 2) : kOutOfRange;
+            sh = static_cast<uint32_t>((NT / 64) * p.ldc * 2);
+        }
+        uint32_t oq = ok ? static_cast<uint32_t>((r0 + rr) * p.q_ld + x) : kOutOfRange;
+        const uint32_t sq = static_cast<uint32_t>((NT / 64) * p.q_ld);
+#pragma unroll
+        for (int n = 0; n < kN; ++n, oh += sh, oq += sq) {
+            const int r = rr + n * (NT / 64);
+            const bool valid = ok && r0 + r < t.y_lim;
+            const float4 v = lds_f4(ep, r, x);
+            uint32_t code[kParts];
+            if constexpr (EPI == kEpiGeluFwd) {
+                view_store_bf16x4(hv, oh, 0, v.x, v.y, v.z, v.w);
+                code[0] = quant4<QF>(gelu_f(v.x), gelu_f(v.y), gelu_f(v.z), gelu_f(v.w), valid, qa);
+            } else if constexpr (EPI == kEpiGeluBwd) {
+                float h[4];
+                unpack_bf16x4(aux.v[n][0], h);
+                code[0] = quant4<QF>(v.x * dgelu_f(h[0]), v.y * dgelu_f(h[1]), v.z * dgelu_f(h[2]),
+                                     v.w * dgelu_f(h[3]), valid, qa);
+            } else {
+                static_assert(EPI == kEpiSwigluBwd, "quantising epilogues: SwiGLU / GELU, forward or backward");
+                float gv[4], uv[4];
+                unpack_bf16x4(aux.v[n][0], gv);
+                unpack_bf16x4(aux.v[n][kParts - 1], uv);
+                const float dv[4] = {v.x, v.y, v.z, v.w};
+                float dg[4], du[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    dg[e] = dv[e] * uv[e] * dsilu_f(gv[e]);
+                    du[e] = dv[e] * silu_f(gv[e]);
+                }
+                code[0] = quant4<QF>(dg[0], dg[1], dg[2], dg[3], valid, qa);
+                code[kParts - 1] = quant4<QF>(du[0], du[1], du[2], du[3], valid, qa);
+            }
+#pragma unroll
+            for (int pt = 0; pt < kParts; ++pt) {
+                __builtin_amdgcn_raw_buffer_store_b32(code[pt], qv, static_cast<int>(oq), pt * p.f, 0);
+                ep[code_word(r, pt * 64 + (threadIdx.x & 63))] = __uint_as_float(code[pt]);
+            }
+        }
+        lds_barrier();
+        store_transposed_half<kW, 64, NT>(p, t, ep, r0);
+    }
+}
+
 // The partial tiles of a K-split tile's pieces: piece q at first + q * stride
 // (float4 units), each thread's accumulators at float4 (i FY + j) 4 + v,
 // thread-major.  pieces = 0: no split, the accumulators are the tile.
@@ -454,9 +688,9 @@ struct SplitSum {
 
 // One half of the epilogue (rows [HALF * 128, +128) of the tile): load the
 // half's aux values, stage the fp32 results in LDS, then write the half.
-template <int HALF, int MODE, int EPI, int NT, int WY>
+template <int HALF, int MODE, int EPI, int NT, int WY, int QF>
 __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, float* ep, f32x16_t (&acc)[4][WY / 32],
-                                              int wx, int wy, int lane, float mul, const SplitSum& split) {
+                                              int wx, int wy, int lane, float mul, const SplitSum& split, QuantAcc& qa) {
     constexpr int FY = WY / 32;
     AuxHalf<EPI, NT> aux;
     load_aux_half<MODE, EPI, NT>(p, t, HALF * kEpRows, aux);
@@ -508,7 +742,10 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
         }
     }
     lds_barrier();
-    epilogue_half<MODE, EPI, NT>(p, t, ep, HALF * kEpRows, aux);
+    if constexpr (QF >= 0)
+        epilogue_half_q<MODE, EPI, NT, QF>(p, t, ep, HALF * kEpRows, aux, qa);
+    else
+        epilogue_half<MODE, EPI, NT>(p, t, ep, HALF * kEpRows, aux);
 }
 
 // Epilogue, in two halves of 128 Y rows.  The pre-activation values a
@@ -522,15 +759,31 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
 // wy * WY + 32 j + (lane & 31) and X columns wx * 128 + 32 i + 8 q +
 // 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller guarantees that every
 // load into the LDS buffer has completed.  With a K split, the staged values
-// are the sum of the pieces' partial tiles instead of acc.
-template <int MODE, int EPI, int NT = kThreadsMfma, int WY = kWaveY>
+// are the sum of the pieces' partial tiles instead of acc.  QF >= 0 (an fp8
+// format) makes the epilogue quantising (the Params q fields): each wave
+// raises the amax once, after both halves.
+template <int MODE, int EPI, int NT = kThreadsMfma, int WY = kWaveY, int QF = -1>
 __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][WY / 32],
                                          int wx, int wy, int lane, float mul = 1.0f,
                                          SplitSum split = SplitSum{nullptr, 0, 0}) {
     static_assert(WY <= kEpRows && kEpRows % WY == 0, "a wave's rows lie in one half");
     float* ep = reinterpret_cast<float*>(lds);
-    epilogue_pass<0, MODE, EPI, NT, WY>(p, t, ep, acc, wx, wy, lane, mul, split);
-    epilogue_pass<1, MODE, EPI, NT, WY>(p, t, ep, acc, wx, wy, lane, mul, split);
+    QuantAcc qa{1.0f, 0.0f};
+    if constexpr (QF >= 0) qa.scale = history_scale(p.q_hist, p.q_L, fp8_max(QF), p.q_margin);
+    epilogue_pass<0, MODE, EPI, NT, WY, QF>(p, t, ep, acc, wx, wy, lane, mul, split, qa);
+    epilogue_pass<1, MODE, EPI, NT, WY, QF>(p, t, ep, acc, wx, wy, lane, mul, split, qa);
+    if constexpr (QF >= 0) {
+        // Wave maximum, then one atomic per wave; non-negative floats order like
+        // their bits, and a maximum not above the value read (possibly stale,
+        // never larger than the true one) has nothing to add.
+        float m = qa.m;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        if ((threadIdx.x & 63) == 0 && m > 0.0f) {
+            const uint32_t seen = __hip_atomic_load(p.q_amax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (__float_as_uint(m) > seen) atomicMax(p.q_amax, __float_as_uint(m));
+        }
+    }
 }
 
 // A piece of a K-split tile: every piece stores its fp32 accumulators (laid

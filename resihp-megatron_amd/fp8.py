@@ -77,15 +77,35 @@ class Fp8State:
             self._ranges[key] = (t, t.clone())
         return self._ranges[key]
 
+    def codes(self, i: int, rows: int, cols: int, rows_cap: int, G: int, device: torch.device,
+              row_major: bool = True, transposed: bool = True) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+        """Uninitialised (row-major, per-expert transposed) code buffers for a cast of tensor i."""
+        fdt = K.FP8_FORMATS[FORMATS.get(i, "e4m3")][1]
+        q = torch.empty(rows, cols, dtype=fdt, device=device) if row_major else None
+        qt = torch.empty(K.fp8_transposed_numel(cols, rows_cap, G), dtype=fdt, device=device) if transposed else None
+        return q, qt
+
     def cast(self, i: int, x: torch.Tensor, offsets: torch.Tensor, poff: torch.Tensor, rows_cap: int,
              row_major: bool = True, transposed: bool = True) -> tuple[torch.Tensor | None, torch.Tensor | None]:
         """Casts rows of ``x`` with tensor i's scale; returns (row-major fp8, per-expert transposed fp8)."""
-        fmt = FORMATS.get(i, "e4m3")
-        fdt = K.FP8_FORMATS[fmt][1]
         rows, cols = x.shape
-        G = offsets.numel() - 1
-        q = torch.empty(rows, cols, dtype=fdt, device=x.device) if row_major else None
-        qt = torch.empty(K.fp8_transposed_numel(cols, rows_cap, G), dtype=fdt, device=x.device) if transposed else None
-        K.fp8_cast(x, offsets, poff, rows_cap, self.history[i], fmt, self.amax[i:i + 1], self.scale_inv[i:i + 1], q, qt,
-                   self.margin)
+        q, qt = self.codes(i, rows, cols, rows_cap, offsets.numel() - 1, x.device, row_major, transposed)
+        K.fp8_cast(x, offsets, poff, rows_cap, self.history[i], FORMATS.get(i, "e4m3"), self.amax[i:i + 1],
+                   self.scale_inv[i:i + 1], q, qt, self.margin)
+        return q, qt
+
+    def gemm_cast(self, i: int, epi: str, offsets: torch.Tensor, poff: torch.Tensor, rows_cap: int,
+                  ys: list[torch.Tensor], y_fmt: str, xs: list[torch.Tensor], N: int, K_: int, f: int,
+                  y_scale_inv: torch.Tensor, x_scale_inv: torch.Tensor, cs: list[torch.Tensor] | None = None,
+                  auxs: list[torch.Tensor] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """An fp8 product whose epilogue casts its activation output as tensor i (``K.fp8_gemm_cast``).
+
+        Returns the (row-major, per-expert transposed) codes, equal to those of the product's bf16 output
+        cast with ``cast``.
+        """
+        cols = 2 * N if epi == "swiglu_bwd" else N
+        q, qt = self.codes(i, ys[0].shape[0], cols, rows_cap, offsets.numel() - 1, ys[0].device)
+        K.fp8_gemm_cast(epi, offsets, poff, rows_cap, ys, y_fmt, xs, "e4m3", N, K_, f, y_scale_inv, x_scale_inv,
+                        self.history[i], FORMATS.get(i, "e4m3"), self.amax[i:i + 1], self.scale_inv[i:i + 1], q, qt,
+                        cs=cs, auxs=auxs, margin=self.margin)
         return q, qt

@@ -501,3 +501,56 @@ def fp8_gemm(kgroups: bool, epi: str, offsets: torch.Tensor, rows_cap: int, ys: 
           _arr(ys), ldy, _arr(xs), ldx, _arr(cs), cs[0].shape[1], c2p, c2s[0].shape[1] if c2s else 0, auxp,
           auxs[0].shape[1] if auxs else 0, _ptr(y_scale_inv), _ptr(x_scale_inv),
           0 if x_scale_inv.numel() == 1 else 1)
+
+
+def fp8_gemm_cast(epi: str, offsets: torch.Tensor, poff: torch.Tensor, rows_cap: int, ys: list[torch.Tensor],
+                  y_fmt: str, xs: list[torch.Tensor], x_fmt: str, N: int, K: int, f: int,
+                  y_scale_inv: torch.Tensor, x_scale_inv: torch.Tensor, history: torch.Tensor, q_fmt: str,
+                  amax_bits: torch.Tensor, scale_inv: torch.Tensor, q: torch.Tensor | None, qt: torch.Tensor | None,
+                  cs: list[torch.Tensor] | None = None, auxs: list[torch.Tensor] | None = None,
+                  margin: int = 0) -> None:
+    """Row-grouped fp8 product whose epilogue casts its activation output to fp8 (rhp_fp8_gemm_cast).
+
+    Forward epilogues store the pre-activation in ``cs`` and cast the activation; backward epilogues read
+    the pre-activation from ``auxs`` and cast the pre-activation gradient.  The codes equal those of
+    ``fp8_gemm`` followed by ``fp8_cast`` of its bf16 output, bit for bit.
+    """
+    G = offsets.numel() - 1
+    dev = _need_cuda(offsets, poff, *ys, *xs, *(cs or []), *(auxs or []), y_scale_inv, x_scale_inv, history,
+                     amax_bits, scale_inv, q, qt)
+    ycode, ydt, _ = FP8_FORMATS[y_fmt]
+    xcode, xdt, _ = FP8_FORMATS[x_fmt]
+    qcode, qdt, _ = FP8_FORMATS[q_fmt]
+    fwd = epi in ("swiglu_fwd", "gelu_fwd")
+    _expect(epi in ("swiglu_fwd", "gelu_fwd", "swiglu_bwd", "gelu_bwd"), f"no quantising form of epilogue {epi!r}")
+    _expect(len(ys) == G and len(xs) == G, f"expected {G} operands per side")
+    for t in ys:
+        _expect(t.dtype == ydt and t.dim() == 2 and t.shape[1] == K and t.shape[0] >= rows_cap,
+                f"y operands must be {ydt} [>= {rows_cap}, {K}]")
+    xrows = 2 * f if epi == "swiglu_fwd" else N
+    for t in xs:
+        _expect(t.dtype == xdt and tuple(t.shape) == (xrows, K), f"x operands must be {xdt} [{xrows}, {K}]")
+    if fwd:
+        _expect(cs is not None and len(cs) == G and auxs is None, "forward epilogues take G pre-activation outputs")
+    else:
+        _expect(cs is None and auxs is not None and len(auxs) == G, "backward epilogues take G pre-activation inputs")
+    for t in (cs or []) + (auxs or []):
+        _expect(t.dtype == torch.bfloat16 and t.dim() == 2, "pre-activations must be bf16 matrices")
+    _expect(poff.dtype == torch.int32 and poff.numel() == G + 1, "poff must be int32 [G+1]")
+    _expect(history.dtype == torch.float32 and history.dim() == 1, "history must be float32 [L]")
+    _expect(amax_bits.dtype == torch.int32 and amax_bits.numel() == 1, "amax_bits must be int32 [1]")
+    _expect(scale_inv.dtype == torch.float32 and scale_inv.numel() == 1, "scale_inv must be float32 [1]")
+    _expect(x_scale_inv.dtype == torch.float32 and x_scale_inv.numel() in (1, G), "x_scale_inv must be float32 [1] or [G]")
+    _expect(y_scale_inv.dtype == torch.float32 and y_scale_inv.numel() == 1, "y_scale_inv must be float32 [1]")
+    cols = 2 * N if epi == "swiglu_bwd" else N
+    _expect(q is not None or qt is not None, "nothing to write")
+    if q is not None:
+        _expect(q.dtype == qdt and q.dim() == 2 and q.shape[1] == cols and q.shape[0] >= rows_cap,
+                f"q must be {qdt} [>= {rows_cap}, {cols}]")
+    if qt is not None:
+        _expect(qt.dtype == qdt and qt.numel() >= fp8_transposed_numel(cols, rows_cap, G), "qt is too small")
+    _call("rhp_fp8_gemm_cast", dev, EPI_CODES[epi], G, _ptr(offsets), _ptr(poff), rows_cap, ycode, xcode, N, K, f,
+          _arr(ys), K, _arr(xs), K, _arr(cs) if cs else None, cs[0].shape[1] if cs else 0,
+          _arr(auxs) if auxs else None, auxs[0].shape[1] if auxs else 0, _ptr(y_scale_inv), _ptr(x_scale_inv),
+          0 if x_scale_inv.numel() == 1 else 1, _ptr(history), history.numel(), qcode, margin, _ptr(amax_bits),
+          _ptr(scale_inv), _ptr(q), _ptr(qt))

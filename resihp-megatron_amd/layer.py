@@ -51,8 +51,11 @@ def _fc1_rows(act: str, f: int) -> int:
     return 2 * f if act == "swiglu" else f
 
 
-def _fp8_forward(st: Fp8State, meta: LayerMeta, offsets, P, xp, fc1s, fc2s, hpre, act, y):
-    """Expert FFN forward in fp8; returns what the backward needs (codes and transposed copies)."""
+def _fp8_forward(st: Fp8State, meta: LayerMeta, offsets, P, xp, fc1s, fc2s, hpre, y):
+    """Expert FFN forward in fp8; returns what the backward needs (codes and transposed copies).
+
+    The fc1 product's epilogue casts the activation straight to fp8 (no bf16 activation rows).
+    """
     G, f = st.G, meta.ffn
     h = xp.shape[1]
     dev = xp.device
@@ -73,16 +76,18 @@ def _fp8_forward(st: Fp8State, meta: LayerMeta, offsets, P, xp, fc1s, fc2s, hpre
     if P > 0:
         xq, xqt = st.cast(X, xp, offsets, poff, P)
         epi = "swiglu_fwd" if meta.act == "swiglu" else "gelu_fwd"
-        K.fp8_gemm(False, epi, offsets, P, [xq] * G, "e4m3", w1q, "e4m3", f, h, 0, f, [hpre] * G,
-                   st.scale_inv[X:X + 1], sw1, c2s=[act] * G)
-        aq, aqt = st.cast(ACT, act, offsets, poff, P)
+        aq, aqt = st.gemm_cast(ACT, epi, offsets, poff, P, [xq] * G, "e4m3", w1q, f, h, f, st.scale_inv[X:X + 1],
+                               sw1, cs=[hpre] * G)
         K.fp8_gemm(False, "store", offsets, P, [aq] * G, "e4m3", w2q, "e4m3", h, f, 0, f, [y] * G,
                    st.scale_inv[ACT:ACT + 1], sw2)
     return dict(poff=poff, xqt=xqt, aqt=aqt, w1qt=w1qt, w2qt=w2qt, sw1=sw1, sw2=sw2)
 
 
 def _fp8_backward(st: Fp8State, q8: dict, meta: LayerMeta, offsets, P, dy, hpre, dxp, dw1, dw2):
-    """Expert FFN backward in fp8 (e5m2 gradients, e4m3 weights and activations)."""
+    """Expert FFN backward in fp8 (e5m2 gradients, e4m3 weights and activations).
+
+    The fc2 input-gradient product's epilogue casts the pre-activation gradient straight to fp8.
+    """
     G, f = st.G, meta.ffn
     h = dy.shape[1]
     F1 = _fc1_rows(meta.act, f)
@@ -93,13 +98,11 @@ def _fp8_backward(st: Fp8State, q8: dict, meta: LayerMeta, offsets, P, dy, hpre,
     poff = q8["poff"]
     s = st.scale_inv
     dyq, dyqt = st.cast(DY, dy, offsets, poff, P)
-    dhpre = dy.new_empty(P, F1)
     epi = "swiglu_bwd" if meta.act == "swiglu" else "gelu_bwd"
-    K.fp8_gemm(False, epi, offsets, P, [dyq] * G, "e5m2", q8["w2qt"], "e4m3", f, h, 0, f, [dhpre] * G,
-               s[DY:DY + 1], q8["sw2"], auxs=[hpre] * G)
+    dhq, dhqt = st.gemm_cast(DH, epi, offsets, poff, P, [dyq] * G, "e5m2", q8["w2qt"], f, h, f, s[DY:DY + 1],
+                             q8["sw2"], auxs=[hpre] * G)
     K.fp8_gemm(True, "store", poff, P, [dyqt], "e5m2", [q8["aqt"]], "e4m3", f, 0, h, f, list(dw2), s[DY:DY + 1],
                s[ACT:ACT + 1])
-    dhq, dhqt = st.cast(DH, dhpre, offsets, poff, P)
     if dxp is not None:
         K.fp8_gemm(False, "store", offsets, P, [dhq] * G, "e5m2", q8["w1qt"], "e4m3", h, F1, 0, f, [dxp] * G,
                    s[DH:DH + 1], q8["sw1"])
@@ -125,11 +128,11 @@ class _MoELayerFn(torch.autograd.Function):
         F1 = _fc1_rows(meta.act, f)
         xp = K.permute(x, plan.pair_row, k, P)
         hpre = x.new_empty(P, F1)
-        act = x.new_empty(P, f)
+        act = x.new_empty(0 if fp8 is not None else P, f)   # the fp8 path keeps only the activation's codes
         y = x.new_empty(P, h)
         q8 = None
         if fp8 is not None:
-            q8 = _fp8_forward(fp8, meta, plan.offsets, P, xp, fc1s, fc2s, hpre, act, y)
+            q8 = _fp8_forward(fp8, meta, plan.offsets, P, xp, fc1s, fc2s, hpre, y)
         elif P > 0:
             K.expert_fc1_fwd([xp] * G, plan.offsets, True, P, fc1s, f, meta.act, [hpre] * G, [act] * G)
             K.expert_fc2_fwd([act] * G, plan.offsets, True, P, fc2s, [y] * G)

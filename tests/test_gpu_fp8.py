@@ -185,6 +185,95 @@ def test_fp8_expert_products(case):
         assert rel_err(dw1[g], dhd[r].t() @ xd[r]) <= BAR, f"fc1 wgrad expert {g}"
 
 
+def _fp8_weights(w1, w2):
+    """Cast expert weights as the layer does: row-major fc1 codes, transposed fc2 codes, 1/scales [G]."""
+    G = len(w1)
+    w1q, w2qt = [], []
+    sw1 = torch.empty(G, dtype=torch.float32, device=DEV)
+    sw2 = torch.empty(G, dtype=torch.float32, device=DEV)
+    for g in range(G):
+        hw = _history(50 + g, scale=0.2)
+        _, _, q1, _, _, s1 = _cast(w1[g], [w1[g].shape[0]], hw, "e4m3", qt=False)
+        _, _, _, t2, _, s2 = _cast(w2[g], [w2[g].shape[0]], hw, "e4m3", q=False)
+        w1q.append(q1); sw1[g:g + 1].copy_(s1)
+        w2qt.append(t2[: w2[g].numel()].view(w2[g].shape[1], w2[g].shape[0])); sw2[g:g + 1].copy_(s2)
+    return w1q, sw1, w2qt, sw2
+
+
+def _cast_buffers(P, cols, G, fmt):
+    """Code buffers for a cast, the transposed one pre-filled with a marker byte (padding must be written)."""
+    fdt = K.FP8_FORMATS[fmt][1]
+    amax = torch.zeros(1, dtype=torch.int32, device=DEV)
+    sinv = torch.zeros(1, dtype=torch.float32, device=DEV)
+    q = torch.empty(P, cols, dtype=fdt, device=DEV)
+    qt = torch.full((K.fp8_transposed_numel(cols, P, G),), 0x55, dtype=torch.uint8, device=DEV).view(fdt)
+    return amax, sinv, q, qt
+
+
+def _same_bits(a, b, what):
+    assert torch.equal(_codes(a), _codes(b)), f"{what} differ"
+
+
+# Expert rows cover a full tile plus a tile whose second half is empty (300), a tile whose
+# second half is partly filled (200) and one row into the second half (129); f = 384 leaves the
+# backward products' last column tile half valid.
+FUSED_COUNTS = [200, 0, 300, 129]
+
+
+@pytest.mark.parametrize("act", ["swiglu", "gelu"])
+@pytest.mark.parametrize("hist_scale,margin", [(3.0, 0), (0.02, 0), (3.0, 2)])
+def test_fused_cast_matches_product_then_cast(act, hist_scale, margin):
+    """rhp_fp8_gemm_cast = rhp_fp8_gemm + rhp_fp8_cast of its bf16 activation output, bit for bit."""
+    h, f, counts = 256, 384, FUSED_COUNTS
+    G, P = len(counts), sum(counts)
+    F1 = 2 * f if act == "swiglu" else f
+    say(f"fp8 fused cast {act} hist_scale={hist_scale} margin={margin}: h={h} f={f} counts={counts}")
+    x = seeded((P, h), 61, 1.0, torch.bfloat16)
+    dy = seeded((P, h), 62, 0.01, torch.bfloat16)
+    hp_in = seeded((P, F1), 63, 1.0, torch.bfloat16).to(DEV)
+    w1 = [seeded((F1, h), 70 + g, 0.05, torch.bfloat16) for g in range(G)]
+    w2 = [seeded((h, f), 80 + g, 0.05, torch.bfloat16) for g in range(G)]
+    offs, poff, xq, _, _, sx = _cast(x, counts, _history(64), "e4m3", qt=False)
+    _, _, dyq, _, _, sdy = _cast(dy, counts, _history(65, scale=0.05), "e5m2", qt=False)
+    w1q, sw1, w2qt, sw2 = _fp8_weights(w1, w2)
+    # small histories saturate part of the outputs
+    hist_a = _history(66, scale=hist_scale).to(DEV)
+    hist_d = _history(67, scale=hist_scale * 0.01).to(DEV)
+
+    # forward: pre-activation and activation codes
+    hpre_u = torch.empty(P, F1, dtype=torch.bfloat16, device=DEV)
+    act_u = torch.empty(P, f, dtype=torch.bfloat16, device=DEV)
+    K.fp8_gemm(False, f"{act}_fwd", offs, P, [xq] * G, "e4m3", w1q, "e4m3", f, h, 0, f, [hpre_u] * G, sx, sw1,
+               c2s=[act_u] * G)
+    au = _cast_buffers(P, f, G, "e4m3")
+    K.fp8_cast(act_u, offs, poff, P, hist_a, "e4m3", *au, margin)
+    hpre_f = torch.empty(P, F1, dtype=torch.bfloat16, device=DEV)
+    af = _cast_buffers(P, f, G, "e4m3")
+    K.fp8_gemm_cast(f"{act}_fwd", offs, poff, P, [xq] * G, "e4m3", w1q, "e4m3", f, h, f, sx, sw1, hist_a, "e4m3",
+                    *af, cs=[hpre_f] * G, margin=margin)
+
+    # backward: pre-activation gradient codes
+    dh_u = torch.empty(P, F1, dtype=torch.bfloat16, device=DEV)
+    K.fp8_gemm(False, f"{act}_bwd", offs, P, [dyq] * G, "e5m2", w2qt, "e4m3", f, h, 0, f, [dh_u] * G, sdy, sw2,
+               auxs=[hp_in] * G)
+    du = _cast_buffers(P, F1, G, "e5m2")
+    K.fp8_cast(dh_u, offs, poff, P, hist_d, "e5m2", *du, margin)
+    df = _cast_buffers(P, F1, G, "e5m2")
+    K.fp8_gemm_cast(f"{act}_bwd", offs, poff, P, [dyq] * G, "e5m2", w2qt, "e4m3", f, h, f, sdy, sw2, hist_d, "e5m2",
+                    *df, auxs=[hp_in] * G, margin=margin)
+    torch.cuda.synchronize()
+
+    _same_bits(hpre_f, hpre_u, "pre-activations")
+    for name, (ua, us, uq, uqt), (fa, fs, fq, fqt) in (("activation", au, af), ("pre-activation gradient", du, df)):
+        _same_bits(fq, uq, f"{name} codes")
+        _same_bits(fqt, uqt, f"{name} transposed codes")
+        assert fa.item() == ua.item() and fa.item() != 0, f"{name} amax"
+        assert fs.item() == us.item(), f"{name} 1/scale"
+    if hist_scale < 0.1:   # the saturating case really saturates
+        lim = torch.tensor([0x7e, 0xfe], dtype=torch.uint8)
+        assert torch.isin(_codes(af[2]), lim).any(), "no saturated activation code"
+
+
 def _q(x64, sinv, fmt):
     """Oracle cast (oracle/moe_ref.py quantize) with the scale whose inverse the GPU used, dequantised."""
     scale = float((torch.tensor(1.0) / torch.tensor(float(sinv), dtype=torch.float32)).item())
