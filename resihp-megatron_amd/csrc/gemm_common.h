@@ -122,6 +122,8 @@ constexpr size_t kSplitBytes = kSplitPartBytes + kSplitSlots * sizeof(int32_t);
 
 enum TileFound { kTileDone = 0, kTileOk = 1, kTileSkip = 2 };
 
+constexpr int kWgradPanel = 4;   // row tiles per panel of the K-grouped tile order
+
 // Finds the tile of work item `bid` (a block id: item bid runs on XCD
 // bid % 8).  xt_cols output columns (X rows) and yt_rows output rows (Y rows)
 // per tile.  Items are remapped so that each XCD runs a contiguous range of
@@ -139,7 +141,22 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
         const int per_group = xt_n * yt_n;
         t->g = L / per_group;
         const int rem = L % per_group;
-        const int yt = rem / xt_n, xt = rem % xt_n;
+        // Within a group, panels of kWgradPanel row tiles, column tiles outer
+        // within a panel: the 32 tiles one XCD runs at a time then span 4 row
+        // and 8 column tiles, 12 operand blocks per K step (a row-major order
+        // spans 1-2 rows and 16-32 columns, up to 34 blocks, which the XCD's
+        // L2 cannot keep, and the products fetched 9x their operands).
+        const int full = yt_n / kWgradPanel, in_full = full * kWgradPanel * xt_n;
+        int yt, xt;
+        if (rem < in_full) {
+            const int pn = rem / (kWgradPanel * xt_n), r = rem % (kWgradPanel * xt_n);
+            xt = r / kWgradPanel;
+            yt = pn * kWgradPanel + r % kWgradPanel;
+        } else {
+            const int py = yt_n - full * kWgradPanel, r = rem - in_full;   // the last, shorter panel
+            xt = r / py;
+            yt = full * kWgradPanel + r % py;
+        }
         t->x0 = xt * xt_cols;
         t->x_lim = p.N - t->x0;
         t->y0 = yt * yt_rows;
