@@ -73,6 +73,27 @@ def test_dispatch_and_gemm_reject_bad_arguments():
         C.call("rhp_combine", fake, fake, fake, C.F32, fake, fake, ptrs, 9, C.BF16, 4, 64, 2, fake, None)
 
 
+def _gemm_cast(epi=1, q_fmt=C.E4M3, c=True, history=True, q=True, qt=True, margin=0):
+    fake = ctypes.c_void_p(4096)   # 16-byte aligned, never dereferenced: validation fails first
+    C.call("rhp_fp8_gemm_cast", epi, 2, fake, fake, 512, C.E4M3, C.E4M3, 256, 256, 256, fake, 256, fake, 256,
+           fake if c else None, 512, fake, 512, fake, fake, 1, fake if history else None, 16, q_fmt, margin, fake,
+           fake, fake if q else None, fake if qt else None, None)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(epi=0), "activation forward or backward"),
+    (dict(q_fmt=C.BF16), "RHP_E4M3 or RHP_E5M2"),
+    (dict(history=False), "null pointer"),
+    (dict(q=False, qt=False), "nothing to write"),
+    (dict(margin=64), "bad history or margin"),
+    (dict(epi=1, c=False), "store the pre-activation in c"),
+    (dict(epi=3, c=True), "store no bf16 output"),
+])
+def test_fp8_gemm_cast_rejects_bad_arguments(kw, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        _gemm_cast(**kw)
+
+
 def test_workspace_queries_are_pure():
     L = C.lib()
     assert L.rhp_dispatch_workspace_bytes(8192, 2, 8, 1) > 0
