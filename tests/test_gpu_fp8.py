@@ -224,7 +224,16 @@ FUSED_COUNTS = [200, 0, 300, 129]
 @pytest.mark.parametrize("hist_scale,margin", [(3.0, 0), (0.02, 0), (3.0, 2)])
 def test_fused_cast_matches_product_then_cast(act, hist_scale, margin):
     """rhp_fp8_gemm_cast = rhp_fp8_gemm + rhp_fp8_cast of its bf16 activation output, bit for bit."""
-    h, f, counts = 256, 384, FUSED_COUNTS
+    _fused_case(act, hist_scale, margin, 256, 384, FUSED_COUNTS)
+
+
+@pytest.mark.parametrize("act", ["swiglu", "gelu"])
+def test_fused_cast_edge_rows(act):
+    """Experts of 1, 255, 256, 257 and 513 rows and an empty one; h = 384, f = 640 (half-valid last tiles)."""
+    _fused_case(act, 3.0, 0, 384, 640, [1, 255, 0, 256, 257, 513])
+
+
+def _fused_case(act, hist_scale, margin, h, f, counts):
     G, P = len(counts), sum(counts)
     F1 = 2 * f if act == "swiglu" else f
     say(f"fp8 fused cast {act} hist_scale={hist_scale} margin={margin}: h={h} f={f} counts={counts}")
