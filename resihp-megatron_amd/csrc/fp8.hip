@@ -582,7 +582,7 @@ int fp8_gemm_run(int kgroups, int epi, int G, const int32_t* offsets, int64_t ro
     p.scale_inv_x = x_scale_inv;
     p.scale_x_stride = x_scale_stride;
     const int64_t xt = (N + (epi == kEpiSwigluFwd ? 127 : 255)) / (epi == kEpiSwigluFwd ? 128 : 256);
-    const int64_t nb = kgroups ? G * xt * ((Mo + kTile - 1) / kTile) : ((rows_cap + kTile - 1) / kTile + G) * xt;
+    const int64_t nb = kgroups ? wgrad_blocks(G, xt * ((Mo + kTile - 1) / kTile)) : ((rows_cap + kTile - 1) / kTile + G) * xt;
     if (nb == 0) return 0;
     if (cast) {
         p.q = cast->q;

@@ -124,6 +124,13 @@ enum TileFound { kTileDone = 0, kTileOk = 1, kTileSkip = 2 };
 
 constexpr int kWgradPanel = 4;   // row tiles per panel of the K-grouped tile order
 
+// Blocks of a K-grouped (weight-gradient) launch of G groups of per_group
+// tiles each: XCD x runs tiles [x per_group / 8, (x + 1) per_group / 8) of
+// every group, at most ceil(per_group / 8) a group.
+__host__ __device__ constexpr int64_t wgrad_blocks(int64_t G, int64_t per_group) {
+    return kXcds * G * ((per_group + kXcds - 1) / kXcds);
+}
+
 // Finds the tile of work item `bid` (a block id: item bid runs on XCD
 // bid % 8).  xt_cols output columns (X rows) and yt_rows output rows (Y rows)
 // per tile.  Items are remapped so that each XCD runs a contiguous range of
@@ -134,13 +141,22 @@ template <int MODE>
 __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_rows, uint32_t bid, Tile* t) {
     const int xt_n = (p.N + xt_cols - 1) / xt_cols;
     if (MODE == kWgrad) {
+        // A tile's reduction is its group's rows, so tiles of different groups
+        // differ in work (ragged routing: by 100x).  Every group has the same
+        // tiles, and XCD x takes the same slice of each group's tile order,
+        // [x per_group / 8, (x + 1) per_group / 8), group by group: each XCD
+        // then gets an eighth of every group's work (a contiguous range of
+        // the tile order by count would give the XCDs owning the hottest
+        // groups several times the others' work).  Hardware block b runs on
+        // XCD b % 8 as that XCD's (b / 8)-th block.
         const int yt_n = (p.Mo + yt_rows - 1) / yt_rows;
-        const uint32_t total = static_cast<uint32_t>(p.G) * xt_n * yt_n;
-        if (bid >= total) return kTileDone;
-        const uint32_t L = xcd_remap(bid, total);
         const int per_group = xt_n * yt_n;
-        t->g = L / per_group;
-        const int rem = L % per_group;
+        const uint32_t x = bid % kXcds, j = bid / kXcds;
+        const int lo = static_cast<int>(x) * per_group / kXcds;
+        const uint32_t n = static_cast<uint32_t>((static_cast<int>(x) + 1) * per_group / kXcds - lo);
+        if (n == 0 || j >= static_cast<uint32_t>(p.G) * n) return kTileDone;
+        t->g = static_cast<int>(j / n);
+        const int rem = lo + static_cast<int>(j % n);
         // Within a group, panels of kWgradPanel row tiles, column tiles outer
         // within a panel: the 32 tiles one XCD runs at a time then span 4 row
         // and 8 column tiles, 12 operand blocks per K step (a row-major order

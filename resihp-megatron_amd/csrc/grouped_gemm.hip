@@ -410,14 +410,14 @@ struct Job {
 template <int MODE, int EPI>
 unsigned mfma_blocks(const Params& p, int64_t rows_cap) {
     const int64_t xt = (p.N + x_per_tile<EPI>() - 1) / x_per_tile<EPI>();
-    if (MODE == kWgrad) return static_cast<unsigned>(p.G * xt * ((p.Mo + kTile - 1) / kTile));
+    if (MODE == kWgrad) return static_cast<unsigned>(wgrad_blocks(p.G, xt * ((p.Mo + kTile - 1) / kTile)));
     return static_cast<unsigned>(((rows_cap + kTile - 1) / kTile + p.G) * xt);
 }
 
 template <int MODE>
 unsigned simt_blocks(const Params& p, int64_t rows_cap) {
     const int64_t xt = (p.N + kSimtTile - 1) / kSimtTile;
-    if (MODE == kWgrad) return static_cast<unsigned>(p.G * xt * ((p.Mo + kSimtTile - 1) / kSimtTile));
+    if (MODE == kWgrad) return static_cast<unsigned>(wgrad_blocks(p.G, xt * ((p.Mo + kSimtTile - 1) / kSimtTile)));
     return static_cast<unsigned>(((rows_cap + kSimtTile - 1) / kSimtTile + p.G) * xt);
 }
 
