@@ -27,6 +27,9 @@ CASES = [
     ("bf16-ragged", torch.bfloat16, 512, 384, [300, 0, 17, 700, 1, 256]),
     ("bf16-multi-tile", torch.bfloat16, 1024, 1024, [1024, 513]),
     ("bf16-70-groups", torch.bfloat16, 128, 128, [(7 * i) % 41 for i in range(70)]),
+    # 9 (fc2) and 15 (fc1) weight-gradient tiles per expert: the per-XCD slices
+    # of each expert's tiles hold 1 or 2 tiles; skewed counts with an empty expert.
+    ("bf16-skewed-uneven-slices", torch.bfloat16, 768, 640, [2000, 900, 0, 257, 64, 3]),
     ("bf16-generic-shape", torch.bfloat16, 40, 24, [9, 3, 0]),
     ("f32", torch.float32, 64, 128, [33, 0, 100, 5]),
     ("f64", torch.float64, 64, 128, [33, 0, 100, 5]),
