@@ -166,6 +166,36 @@ int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, const int32_t
                      int x_dtype, int r_dtype, int64_t T, int h, int E, int k, void* dw, void* workspace,
                      size_t workspace_bytes, hipStream_t stream);
 
+/* ----------------------------------------- received rows (receiving side of expert parallelism) */
+
+/*
+ * Plan of a received buffer: the receiving side of EPRuntime.forward
+ * (resihp/runtime/moe.py:199-226).  Each source sends its rows for this GPU
+ * expert-major, (token, slot) ascending within an expert (moe.py:199-207), and
+ * the all-to-all concatenates the sources (:209-212), so the received buffer
+ * holds chunk (s, e) of recv_counts[s * L + e] rows, source-major; the
+ * reference runs the expert FFN chunk by chunk in that order (:213-223).  The
+ * grouped GEMMs need each local expert's rows together:
+ *   offsets[L+1]       expert-major group offsets (sources in order within an expert)
+ *   sort_row[rows]     expert-major row r holds received row sort_row[r]
+ *   unsort_row[rows]   received row q is expert-major row unsort_row[q]
+ * recv_counts: [n_src, L] int32 on the device, the local experts' columns of the
+ * exchanged counts (moe.py:209); rows must equal their sum (the reference
+ * materialises the split sizes on the host, moe.py:210-211).  n_src * L <= 8192.
+ */
+int rhp_recv_plan(const int32_t* recv_counts, int n_src, int L, int64_t rows, int32_t* offsets, int32_t* sort_row,
+                  int32_t* unsort_row, hipStream_t stream);
+
+/*
+ * Row gather: dst[r] = src[idx[r]] for r < rows (whole rows of h elements,
+ * dtype F64 / F32 / BF16, 16-byte aligned); an index outside [0, src_rows)
+ * gives a zero row.  With sort_row it regroups received rows expert-major;
+ * with unsort_row it puts expert outputs and input gradients back into the
+ * received order, in which they return to their sources (moe.py:224).
+ */
+int rhp_gather_rows(const void* src, int dtype, int64_t src_rows, int h, const int32_t* idx, int64_t rows,
+                    void* dst, hipStream_t stream);
+
 /* ------------------------------------------------------- expert grouped GEMMs */
 
 /*
@@ -175,16 +205,28 @@ int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, const int32_t
  * as host arrays of G device pointers; with rows_from_offsets = 1 group g's
  * rows start at row offsets[g] of its buffer (routed experts: every entry is
  * the same permuted buffer), with 0 at row 0 (shared experts: one buffer per
- * group).  offsets is a device array of G+1 int32; rows_cap >= offsets[G]
- * bounds the launch.  Weights are per-group device pointers, so each expert
- * keeps its own parameter tensor.
+ * group).  offsets is a device array of G+1 int32.  rows_cap bounds the
+ * launch: with rows_from_offsets = 1 the shared buffer holds rows_cap >=
+ * offsets[G] rows; with rows_from_offsets = 0 every group's buffer holds
+ * rows_cap rows and no group has more (offsets[g+1] - offsets[g] <= rows_cap).
+ * Rows past rows_cap are never read or written.  Weights are per-group
+ * device pointers, so each expert keeps its own parameter tensor.
  *
  *   fc1 weight w1[g]: [F1, h] row-major, F1 = 2f (SwiGLU: gate rows, then up rows) or f (GELU)
  *   fc2 weight w2[g]: [h, f]
  *
- * dtype: BF16 (MFMA path, needs h % 64 == 0 and f % 64 == 0), F32 or F64.
- * Groups beyond RHP_MAX_GROUPS_PER_LAUNCH are split into several launches.
+ * dtype: BF16, F32 or F64.  bfloat16 products with h % 64 == 0, f % 64 == 0
+ * and weights below 2 GiB run on the MFMA kernel, for any number of rows; its
+ * operand pointers must then be 16-byte aligned (an unaligned pointer is an
+ * error).  Every other call runs the generic kernel (float32 / float64, or
+ * bfloat16 shapes the MFMA kernel does not take); rhp_expert_gemm_kernel()
+ * says which one a call takes.  Groups beyond RHP_MAX_GROUPS_PER_LAUNCH are
+ * split into several launches.
  */
+
+/* Which kernel the expert GEMM entry points run for these operands: the MFMA kernel or the generic one. */
+enum { RHP_GEMM_KERNEL_GENERIC = 0, RHP_GEMM_KERNEL_MFMA = 1 };
+int rhp_expert_gemm_kernel(int dtype, int act, int h, int f);
 
 /*
  * K-split workspace of the row-grouped products (forward and input-gradient;
@@ -193,11 +235,16 @@ int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, const int32_t
  * otherwise idle CUs; pieces keep fp32 partial tiles here and the last piece
  * of a tile to finish adds them in piece order (deterministic) and writes the
  * tile.  The workspace ends in arrival counters that must be zero before its
- * first use; every call leaves them zero again.  Calls that share a workspace
- * must not run concurrently (stream-order them).  No reference counterpart:
- * scheduling only, the products are those of moe.py:82-83.
+ * first use; every call that completes leaves them zero again.  Calls that
+ * share a workspace must not run concurrently (stream-order them, or give
+ * each stream its own workspace).  No reference counterpart: scheduling
+ * only, the products are those of moe.py:82-83.
  */
 size_t rhp_expert_split_workspace_bytes(void);
+
+/* Zeroes the arrival counters of a K-split workspace (a fill kernel on the
+ * stream): before its first use, and after a call that did not complete. */
+int rhp_expert_split_workspace_reset(void* split_ws, size_t split_ws_bytes, hipStream_t stream);
 
 /* hpre[r] = xp[r] @ w1^T  ([M_g, F1]);  act[r] = silu(gate) * up  or  gelu(hpre)  ([M_g, f]). */
 int rhp_expert_fc1_fwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,

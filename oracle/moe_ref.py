@@ -220,6 +220,52 @@ def dispatch(topi: np.ndarray, E: int, e0: int = 0, e1: int | None = None, n_src
     return {"counts": counts, "offsets": offsets, "src_counts": src_counts, "perm": order, "pair_row": pair_row}
 
 
+def received_rows(topis, local, assign=None):
+    """The rows one device receives in expert-parallel dispatch, in order (resihp/runtime/moe.py:193-212).
+
+    ``topis[s]`` holds source s's top-k expert ids ``[T_s, k]`` (sources in EP rank order); ``local``
+    lists the receiving device's experts.  Source s sends this device, for each of its experts in
+    ascending id, its pairs ``(token, slot)`` routed there in ascending order (:199-207); the
+    all-to-all concatenates the sources in rank order (:209-212).  A replicated expert splits its
+    pairs over its holders (:193-198): ``assign(s, e, n)`` then gives, for the n pairs of source s
+    routed to e in that order, which ones come to this device (a boolean list); None keeps all.
+    Returns the source, token and slot of every received row, and ``recv_counts [n_src, len(local)]``.
+    """
+    src, tok, slot = [], [], []
+    local = sorted(local)
+    counts = np.zeros((len(topis), len(local)), np.int64)
+    for s, topi in enumerate(topis):
+        topi = np.asarray(topi, np.int64)
+        k = topi.shape[1]
+        flat = topi.reshape(-1)
+        for i, e in enumerate(local):
+            pairs = np.nonzero(flat == e)[0]        # flat index t*k + j: ascending (token, slot)
+            if assign is not None:
+                pairs = pairs[np.asarray(assign(s, e, pairs.size), bool)]
+            counts[s, i] = pairs.size
+            src.append(np.full(pairs.size, s, np.int64))
+            tok.append(pairs // k)
+            slot.append(pairs % k)
+    cat = lambda parts: np.concatenate(parts) if parts else np.zeros(0, np.int64)  # noqa: E731
+    return cat(src), cat(tok), cat(slot), counts
+
+
+def recv_plan(recv_counts) -> dict[str, np.ndarray]:
+    """Expert-major grouping of a received buffer (the chunk order of resihp/runtime/moe.py:213-222,
+    regrouped by expert): group i holds the rows of local expert i, sources ascending, each chunk in
+    its received order.  ``sort_row[r]`` is the received row at expert-major row r, ``unsort_row`` its
+    inverse, ``offsets`` the group starts."""
+    counts = np.asarray(recv_counts, np.int64)
+    n_src, L = counts.shape
+    chunk = np.repeat(np.arange(n_src * L), counts.reshape(-1))
+    rows = chunk.size
+    sort_row = np.lexsort((np.arange(rows), chunk // L, chunk % L))
+    unsort_row = np.empty(rows, np.int64)
+    unsort_row[sort_row] = np.arange(rows)
+    offsets = np.concatenate([[0], np.cumsum(counts.sum(0))])
+    return {"offsets": offsets, "sort_row": sort_row, "unsort_row": unsort_row}
+
+
 # --------------------------------------------------------------------------- experts
 
 

@@ -14,6 +14,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "libresihp_moe.so"
 F64, F32, BF16, E4M3, E5M2 = 0, 1, 2, 3, 4
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 ACT_GELU, ACT_SWIGLU = 0, 1
+GEMM_KERNEL_GENERIC, GEMM_KERNEL_MFMA = 0, 1
 MAX_GROUPS_PER_LAUNCH = 64
 
 _p = ctypes.c_void_p
@@ -38,7 +39,11 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "rhp_token_bwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _pp, _i, _i, _i64, _i, _i, _i, _p, _p]),
     "rhp_router_wgrad_workspace_bytes": (_sz, [_i64, _i, _i, _i, _i]),
     "rhp_router_wgrad": (_i, [_p, _p, _p, _p, _i, _i, _i64, _i, _i, _i, _p, _p, _sz, _p]),
+    "rhp_recv_plan": (_i, [_p, _i, _i, _i64, _p, _p, _p, _p]),
+    "rhp_gather_rows": (_i, [_p, _i, _i64, _i, _p, _i64, _p, _p]),
     "rhp_expert_split_workspace_bytes": (_sz, []),
+    "rhp_expert_split_workspace_reset": (_i, [_p, _sz, _p]),
+    "rhp_expert_gemm_kernel": (_i, [_i, _i, _i, _i]),
     "rhp_expert_fc1_fwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _p, _sz, _p]),
     "rhp_expert_fc2_fwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _pp, _pp, _pp, _p, _sz, _p]),
     "rhp_expert_fc2_bwd": (_i, [_i, _p, _i, _i64, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _pp, _p, _sz, _p]),

@@ -275,13 +275,12 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
         const uint32_t ld = static_cast<uint32_t>(t.k_end);   // R_g
         const uint8_t* Y = static_cast<const uint8_t*>(p.a[0]) + static_cast<int64_t>(p.Mo) * t.row0;
         const uint8_t* X = static_cast<const uint8_t*>(p.b[0]) + static_cast<int64_t>(p.N) * t.row0;
-        ry = make_dma_rsrc(Y + static_cast<int64_t>(t.y0) * ld, static_cast<int64_t>(t.y_lim) * ld);
-        rx = make_dma_rsrc(X, static_cast<int64_t>(p.N) * ld);
+        // Views of the tile's 256 rows of each transposed copy: byte offsets stay
+        // below 2 GiB for any expert row count up to 8 M.
+        ry = make_dma_rsrc(Y + static_cast<int64_t>(t.y0) * ld, static_cast<int64_t>(min(t.y_lim, kTile)) * ld);
+        rx = make_dma_rsrc(X + static_cast<int64_t>(t.x0) * ld, static_cast<int64_t>(min(t.x_lim, kTile)) * ld);
         f8_map(my, ld, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
-        f8_map(mx, ld, wx * 128, 4, [&](int r) {
-            const int n = t.x0 + r;
-            return n < p.N ? n : 0;
-        });
+        f8_map(mx, ld, wx * 128, 4, [&](int r) { return r < t.x_lim ? r : 0; });
     } else {
         const uint8_t* Y = static_cast<const uint8_t*>(p.a[g]);
         const uint8_t* X = static_cast<const uint8_t*>(p.b[g]);
@@ -552,14 +551,16 @@ int fp8_gemm_run(int kgroups, int epi, int G, const int32_t* offsets, int64_t ro
     if (kgroups) {
         RHP_REQUIRE(epi == kEpiStore, "rhp_fp8_gemm: K-grouped products store plain outputs");
         RHP_REQUIRE(Mo > 0 && Mo % 64 == 0, "rhp_fp8_gemm: Mo must be a positive multiple of 64");
-        RHP_REQUIRE((int64_t(Mo) + N) * (rows_cap + 128 * int64_t(G)) < (int64_t(1) << 31),
-                    "rhp_fp8_gemm: transposed operands must stay below 2 GiB");
+        // Each tile reads 256 rows of an expert's transposed copies through its own view.
+        RHP_REQUIRE((kTile + 1) * (rows_cap + 128) < (int64_t(1) << 31),
+                    "rhp_fp8_gemm: an expert's padded rows must stay below 2^23");
     } else {
         RHP_REQUIRE(K > 0 && K % kF8K == 0, "rhp_fp8_gemm: K must be a positive multiple of 128");
         RHP_REQUIRE(ldy >= K && ldy % 16 == 0 && ldx >= K && ldx % 16 == 0, "rhp_fp8_gemm: bad row pitches");
         const int64_t xrows = epi == kEpiSwigluFwd ? 2 * int64_t(f) : N;
-        RHP_REQUIRE(rows_cap * ldy < (int64_t(1) << 31) && xrows * ldx < (int64_t(1) << 31),
-                    "rhp_fp8_gemm: operands must stay below 2 GiB");
+        // Token rows are read through a view per tile; a weight is read whole.
+        RHP_REQUIRE(kTile * ldy < (int64_t(1) << 31) && xrows * ldx < (int64_t(1) << 31),
+                    "rhp_fp8_gemm: weights must stay below 2 GiB");
         if ((epi == kEpiSwigluFwd || epi == kEpiGeluFwd) && !cast)
             RHP_REQUIRE(c2 != nullptr, "rhp_fp8_gemm: activation output missing");
         if (epi == kEpiSwigluBwd || epi == kEpiGeluBwd) RHP_REQUIRE(aux != nullptr, "rhp_fp8_gemm: pre-activation input missing");
@@ -635,9 +636,8 @@ extern "C" int rhp_fp8_gemm_cast(int epi, int G, const int32_t* offsets, const i
                 "rhp_fp8_gemm_cast: forward epilogues store the pre-activation in c, backward ones store no bf16 output");
     RHP_REQUIRE(N > 0 && N < (int64_t(1) << 21), "rhp_fp8_gemm_cast: N out of range");
     const int64_t cols = epi == kEpiSwigluBwd ? 2 * int64_t(N) : N;
-    // Code rows are addressed with 32-bit byte offsets, row-major and transposed.
-    RHP_REQUIRE(rows_cap >= 0 && (rows_cap + 128 * int64_t(G)) * cols < (int64_t(1) << 31),
-                "rhp_fp8_gemm_cast: quantised outputs must stay below 2 GiB");
+    // Row-major codes go through a view of each tile's rows; transposed codes are addressed in 64 bits.
+    RHP_REQUIRE(rows_cap >= 0 && kTile * cols < (int64_t(1) << 31), "rhp_fp8_gemm_cast: N out of range");
     const CastOut cast{poff, history, hist_len, q_fmt, margin, amax_bits, scale_inv, static_cast<uint8_t*>(q),
                        static_cast<uint8_t*>(qt)};
     return fp8_gemm_run(0, epi, G, offsets, rows_cap, y_fmt, x_fmt, N, K, 0, f, y, ldy, x, ldx, c, ldc, nullptr, 0,

@@ -185,8 +185,9 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
         t->pieces = 1;
         t->slot = 0;
         t->stride = 0;
-        // A shared row buffer holds rows_cap rows: never read past it.
-        if (p.rows_from_offsets) t->k_end = max(0, min(t->k_end, p.rows_cap - r0));
+        // A shared row buffer holds rows_cap rows, and so does each buffer of
+        // groups with a buffer each: never read past it.
+        t->k_end = max(0, min(t->k_end, p.rows_cap - (p.rows_from_offsets ? r0 : 0)));
         return kTileOk;
     }
     uint32_t total = 0;
@@ -250,8 +251,9 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
                 t->k_begin = (t->piece * nk / t->pieces) * ks;
                 t->k_end = min(p.K, ((t->piece + 1) * nk / t->pieces) * ks);
             }
-            // A shared row buffer holds rows_cap rows: never touch rows past it.
-            if (p.rows_from_offsets) t->y_lim = min(t->y_lim, p.rows_cap - static_cast<int>(t->row0) - t->y0);
+            // A shared row buffer holds rows_cap rows, and so does each buffer of
+            // groups with a buffer each: never touch rows past it.
+            t->y_lim = min(t->y_lim, p.rows_cap - static_cast<int>(t->row0) - t->y0);
             return t->y_lim > 0 ? kTileOk : kTileSkip;
         }
         L -= n_tiles;

@@ -103,7 +103,9 @@ constexpr uint32_t kPastView = 0x7ffffff0u;   // soffset that puts every lane pa
 
 // One tile: the K loop through the slot ring, then the epilogue (or, for a
 // piece of a K-split tile, the hand-over to the piece that finishes last).
-template <int MODE, int EPI, int NW>
+// REBASE (weight gradients whose group rows may pass 2 GiB of one operand):
+// every K step's loads go through a view based at the step's first row.
+template <int MODE, int EPI, int NW, bool REBASE = false>
 __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* lds) {
     // NW waves: wave w owns X rows [128 (w % 2), +128) and Y rows [WY (w / 2), +WY).
     constexpr int WY = kTile / (NW / 2), FY = WY / 32;
@@ -134,6 +136,8 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
     Rsrc rx, ry;
     Dma64Map<NW> mx, my;
     if (MODE == kWgrad) {
+        // Views of the group's rows (REBASE: issue_x / issue_y base them at each
+        // step's first row, so byte offsets stay below 2 GiB for any row count).
         const int64_t rows = t.k_end;   // group rows; reads past them return zero
         rx = make_dma_rsrc(B + t.row0 * p.ldb, rows * p.ldb * 2);
         ry = make_dma_rsrc(A + t.row0 * p.lda, rows * p.lda * 2);
@@ -166,10 +170,21 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
     // Loads [j0, j1) of the X (Y) tile of step `step` into slot `slot`; past
     // the last step, zeros.
+    // The view of K-grouped rows [k0, k_end) (WGRAD: every step gets its own base).
+    auto rows_view = [&](const uint16_t* M, uint32_t ld, int k0) {
+        return make_dma_rsrc(M + (t.row0 + k0) * static_cast<int64_t>(ld),
+                             static_cast<int64_t>(t.k_end - k0) * ld * 2);
+    };
     auto issue_x = [&](int step, int slot, int j0 = 0, int j1 = kT64Bytes / 1024 / NW) {
         const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kK64);
         const bool live = step < nk;
         const uint32_t base = lds0 + slot * kT64Bytes + wave * 1024;
+        if constexpr (REBASE) {
+            const Rsrc r = live ? rows_view(B, ldb, static_cast<int>(k0)) : rx;
+#pragma unroll
+            for (int j = j0; j < j1; ++j) dma16(r, mx.vo[j], live ? 0u : kPastView, base + j * NW * 1024);
+            return;
+        }
 #pragma unroll
         for (int j = j0; j < j1; ++j) {
             const uint32_t at = base + j * NW * 1024;
@@ -181,6 +196,12 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
         const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kK64);
         const bool live = step < nk;
         const uint32_t base = lds0 + slot * kT64Bytes + wave * 1024;
+        if constexpr (REBASE) {
+            const Rsrc r = live ? rows_view(A, lda, static_cast<int>(k0)) : ry;
+#pragma unroll
+            for (int j = j0; j < j1; ++j) dma16(r, my.vo[j], live ? 0u : kPastView, base + j * NW * 1024);
+            return;
+        }
 #pragma unroll
         for (int j = j0; j < j1; ++j) {
             const uint32_t at = base + j * NW * 1024;
@@ -318,12 +339,12 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
 }
 
 // One block per tile (hardware block b runs on XCD b % 8).
-template <int MODE, int EPI, int NW>
+template <int MODE, int EPI, int NW, bool REBASE = false>
 __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
     __shared__ __align__(1024) uint8_t lds[kLdsSlotsBytes];
     Tile t;
     if (find_tile<MODE>(p, x_per_tile<EPI>(), kTile, blockIdx.x, &t) != kTileOk) return;
-    gg_bf16_tile<MODE, EPI, NW>(p, t, lds);
+    gg_bf16_tile<MODE, EPI, NW, REBASE>(p, t, lds);
 }
 
 // ------------------------------------------------------------------ generic kernel (any dtype)
@@ -407,33 +428,49 @@ struct Job {
     int cus_per_xcd;  // CUs per XCD of the device the launch runs on
 };
 
+// Blocks of a launch: an upper bound of its tiles.  Row-grouped products:
+// groups that share one row buffer (rows_from_offsets) hold rows_cap rows
+// together, so their row tiles number at most rows_cap / tile + G; groups
+// with a buffer each (shared experts) hold up to rows_cap rows each.
+template <int MODE>
+int64_t row_grouped_blocks(const Params& p, int64_t rows_cap, int tile_rows, int64_t xt) {
+    if (MODE == kWgrad) return wgrad_blocks(p.G, xt * ((p.Mo + tile_rows - 1) / tile_rows));
+    const int64_t row_tiles = (rows_cap + tile_rows - 1) / tile_rows;
+    return (p.rows_from_offsets ? row_tiles + p.G : row_tiles * p.G) * xt;
+}
+
 template <int MODE, int EPI>
-unsigned mfma_blocks(const Params& p, int64_t rows_cap) {
-    const int64_t xt = (p.N + x_per_tile<EPI>() - 1) / x_per_tile<EPI>();
-    if (MODE == kWgrad) return static_cast<unsigned>(wgrad_blocks(p.G, xt * ((p.Mo + kTile - 1) / kTile)));
-    return static_cast<unsigned>(((rows_cap + kTile - 1) / kTile + p.G) * xt);
+int64_t mfma_blocks(const Params& p, int64_t rows_cap) {
+    return row_grouped_blocks<MODE>(p, rows_cap, kTile, (p.N + x_per_tile<EPI>() - 1) / x_per_tile<EPI>());
 }
 
 template <int MODE>
-unsigned simt_blocks(const Params& p, int64_t rows_cap) {
-    const int64_t xt = (p.N + kSimtTile - 1) / kSimtTile;
-    if (MODE == kWgrad) return static_cast<unsigned>(wgrad_blocks(p.G, xt * ((p.Mo + kSimtTile - 1) / kSimtTile)));
-    return static_cast<unsigned>(((rows_cap + kSimtTile - 1) / kSimtTile + p.G) * xt);
+int64_t simt_blocks(const Params& p, int64_t rows_cap) {
+    return row_grouped_blocks<MODE>(p, rows_cap, kSimtTile, (p.N + kSimtTile - 1) / kSimtTile);
 }
 
 template <int MODE, int EPI>
 void launch_one(const Job& j, const Params& p, hipStream_t s) {
     if (j.mfma) {
-        unsigned nb = mfma_blocks<MODE, EPI>(p, j.rows_cap);
+        int64_t nb = mfma_blocks<MODE, EPI>(p, j.rows_cap);
         if (!nb) return;
         // A K split adds at most one round of pieces to each XCD's items.
-        if (MODE != kWgrad && p.split_cap > 1)
-            nb = kXcds * ((nb + kXcds - 1) / kXcds + static_cast<unsigned>(p.cu_per_xcd));
+        if (MODE != kWgrad && p.split_cap > 1) nb = kXcds * ((nb + kXcds - 1) / kXcds + p.cu_per_xcd);
         constexpr int nw = MODE == kFwd ? 4 : kWaves;
-        hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, nw>), dim3(nb), dim3(64 * nw), 0, s, p);
+        if constexpr (MODE == kWgrad) {
+            // Per-step views cost 15-20 % of a weight-gradient product; they are needed only where a
+            // group's rows may span 2 GiB of an operand (rows_cap rows of the wider one).
+            const int64_t widest = std::max(j.lda, j.ldb);
+            if (j.rows_cap * widest * 2 >= (int64_t(1) << 31) - (int64_t(1) << 20)) {
+                hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, nw, true>), dim3(static_cast<unsigned>(nb)),
+                                   dim3(64 * nw), 0, s, p);
+                return;
+            }
+        }
+        hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, nw>), dim3(static_cast<unsigned>(nb)), dim3(64 * nw), 0, s, p);
         return;
     }
-    const unsigned nb = simt_blocks<MODE>(p, j.rows_cap);
+    const unsigned nb = static_cast<unsigned>(simt_blocks<MODE>(p, j.rows_cap));
     if (!nb) return;
     if (j.dtype == RHP_BF16)
         hipLaunchKernelGGL((gg_simt_kernel<bf16, MODE, EPI>), dim3(nb), dim3(256), 0, s, p);
@@ -460,6 +497,14 @@ void launch(const Job& j, const Params& p, hipStream_t s) {
 int run(const Job& job, const char* what, hipStream_t s) {
     Job j = job;
     j.cus_per_xcd = cus_per_xcd();
+    {
+        // Every launch's grid (an upper bound of its tiles, plus a K split's extra round) fits in 31 bits.
+        const int64_t tr = j.mfma ? kTile : kSimtTile, tx = j.mfma ? 128 : kSimtTile;
+        const int64_t g = std::min(j.G, kMaxG), xt = (j.N + tx - 1) / tx;
+        const int64_t bound = j.mode == kWgrad ? wgrad_blocks(g, xt * ((j.Mo + tr - 1) / tr))
+                                               : ((j.rows_cap + tr - 1) / tr + 1) * g * xt + kXcds * kSplitMaxCus;
+        if (bound >= (int64_t(1) << 31)) return fail(std::string(what) + ": too many tiles for one launch");
+    }
     for (int g0 = 0; g0 < j.G; g0 += kMaxG) {
         const int gn = std::min(kMaxG, j.G - g0);
         Params p{};
@@ -526,15 +571,26 @@ int check_common(const char* fn, int G, const int32_t* offsets, int64_t rows_cap
     return 0;
 }
 
-// The MFMA kernel reads and writes through buffer views whose byte extent is a
-// 31-bit number: every row buffer and weight must stay below 2 GiB, and so
-// must kTile rows of the widest matrix (an epilogue's view).
-bool mfma_ok(int dtype, int h, int f, int act, int64_t rows_cap) {
+// The MFMA kernel reads and writes through buffer views with 31-bit byte
+// offsets.  Row operands get a view per tile (row-grouped products) or per K
+// step (weight gradients), so only a weight (read whole) and kTile rows of
+// the widest matrix (an epilogue's view) must stay below 2 GiB; the number
+// of rows is free.
+bool mfma_shape_ok(int dtype, int h, int f, int act) {
     const int64_t F1 = act == RHP_ACT_SWIGLU ? 2 * static_cast<int64_t>(f) : f;
     const int64_t widest = std::max<int64_t>(h, F1);
     const int64_t limit = int64_t(1) << 31;
-    return dtype == RHP_BF16 && h % 64 == 0 && f % 64 == 0 && rows_cap * widest * 2 < limit && F1 * h * 2 < limit &&
-           kTile * widest * 2 < limit;
+    return dtype == RHP_BF16 && h % 64 == 0 && f % 64 == 0 && F1 * h * 2 < limit && kTile * widest * 2 < limit;
+}
+
+// Kernel of a call: the MFMA kernel for bfloat16 shapes it takes, the generic
+// one otherwise.  bfloat16 operands the MFMA kernel would take but whose
+// pointers are not 16-byte aligned are an error, not a silent fallback.
+int choose_kernel(const char* fn, int dtype, int h, int f, int act, bool aligned, bool* mfma) {
+    *mfma = mfma_shape_ok(dtype, h, f, act);
+    if (*mfma && !aligned)
+        return fail(std::string(fn) + ": bfloat16 operands must be 16-byte aligned (every row and weight pointer)");
+    return 0;
 }
 
 }  // namespace
@@ -543,6 +599,29 @@ bool mfma_ok(int dtype, int h, int f, int act, int64_t rows_cap) {
 using namespace rhp;
 
 extern "C" size_t rhp_expert_split_workspace_bytes(void) { return kSplitBytes; }
+
+namespace rhp {
+namespace {
+__global__ void split_reset_kernel(int32_t* cnt, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) cnt[i] = 0;
+}
+}  // namespace
+}  // namespace rhp
+
+extern "C" int rhp_expert_split_workspace_reset(void* split_ws, size_t split_ws_bytes, hipStream_t stream) {
+    clear_error();
+    RHP_REQUIRE(split_ws != nullptr, "rhp_expert_split_workspace_reset: null workspace");
+    if (int rc = check_split_ws("rhp_expert_split_workspace_reset", split_ws, split_ws_bytes)) return rc;
+    int32_t* cnt = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(split_ws) + kSplitPartBytes);
+    const int n = static_cast<int>(kSplitSlots);
+    hipLaunchKernelGGL(split_reset_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, cnt, n);
+    return check_launch("rhp_expert_split_workspace_reset");
+}
+
+extern "C" int rhp_expert_gemm_kernel(int dtype, int act, int h, int f) {
+    return mfma_shape_ok(dtype, h, f, act) ? RHP_GEMM_KERNEL_MFMA : RHP_GEMM_KERNEL_GENERIC;
+}
 
 extern "C" int rhp_expert_fc1_fwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype,
                                   int act, int h, int f, const void* const* xp, const void* const* w1,
@@ -560,8 +639,11 @@ extern "C" int rhp_expert_fc1_fwd(int G, const int32_t* offsets, int rows_from_o
     j.mode = kFwd;
     j.epi = swiglu ? kEpiSwigluFwd : kEpiGeluFwd;
     j.dtype = dtype;
-    j.mfma = mfma_ok(dtype, h, f, act, rows_cap) && all_aligned(xp, G) && all_aligned(w1, G) &&
-             all_aligned((const void* const*)hpre, G) && all_aligned((const void* const*)act_out, G);
+    if (int rc = choose_kernel("rhp_expert_fc1_fwd", dtype, h, f, act,
+                               all_aligned(xp, G) && all_aligned(w1, G) && all_aligned((const void* const*)hpre, G) &&
+                                   all_aligned((const void* const*)act_out, G),
+                               &j.mfma))
+        return rc;
     j.G = G;
     j.offsets = offsets;
     j.rows_from_offsets = rows_from_offsets;
@@ -593,8 +675,10 @@ extern "C" int rhp_expert_fc2_fwd(int G, const int32_t* offsets, int rows_from_o
     j.mode = kFwd;
     j.epi = kEpiStore;
     j.dtype = dtype;
-    j.mfma = mfma_ok(dtype, h, f, RHP_ACT_GELU, rows_cap) && all_aligned(act_in, G) && all_aligned(w2, G) &&
-             all_aligned((const void* const*)y, G);
+    if (int rc = choose_kernel("rhp_expert_fc2_fwd", dtype, h, f, RHP_ACT_GELU,
+                               all_aligned(act_in, G) && all_aligned(w2, G) && all_aligned((const void* const*)y, G),
+                               &j.mfma))
+        return rc;
     j.G = G;
     j.offsets = offsets;
     j.rows_from_offsets = rows_from_offsets;
@@ -632,7 +716,7 @@ extern "C" int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_o
     d.mode = kDgrad;
     d.epi = swiglu ? kEpiSwigluBwd : kEpiGeluBwd;
     d.dtype = dtype;
-    d.mfma = mfma_ok(dtype, h, f, act, rows_cap) && aligned;
+    if (int rc = choose_kernel("rhp_expert_fc2_bwd", dtype, h, f, act, aligned, &d.mfma)) return rc;
     d.G = G;
     d.offsets = offsets;
     d.rows_from_offsets = rows_from_offsets;
@@ -684,7 +768,8 @@ extern "C" int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_o
     const int F1 = act == RHP_ACT_SWIGLU ? 2 * f : f;
     const bool aligned = all_aligned(dhpre, G) && all_aligned(xp, G) && all_aligned(w1, G) &&
                          all_aligned((const void* const*)dw1, G) && all_aligned((const void* const*)dxp, G);
-    const bool mfma = mfma_ok(dtype, h, f, act, rows_cap) && aligned;
+    bool mfma = false;
+    if (int rc = choose_kernel("rhp_expert_fc1_bwd", dtype, h, f, act, aligned, &mfma)) return rc;
     if (dxp) {
         RHP_REQUIRE(all_set((const void* const*)dxp, G), "rhp_expert_fc1_bwd: null dxp entry");
         // dxp = dhpre @ w1

@@ -257,6 +257,50 @@ def router_wgrad(dl: torch.Tensor, perm: torch.Tensor, offsets: torch.Tensor, x:
     return dw
 
 
+# ----------------------------------------------------------------------------- received rows
+
+
+@dataclass
+class RecvPlan:
+    """Expert-major grouping of a source-major received buffer (all int32 device tensors)."""
+
+    offsets: torch.Tensor      # [L + 1] group offsets of the expert-major rows
+    sort_row: torch.Tensor     # [rows]: expert-major row r holds received row sort_row[r]
+    unsort_row: torch.Tensor   # [rows]: received row q is expert-major row unsort_row[q]
+    rows: int
+
+
+def recv_plan(recv_counts: torch.Tensor) -> RecvPlan:
+    """Plan of a received buffer from its per-(source, local expert) counts ``[n_src, L]``.
+
+    The row count is the counts' sum, read on the host (as the reference reads its split sizes,
+    resihp/runtime/moe.py:210-211), so the two row maps are exact inverses of each other.
+    """
+    dev = _need_cuda(recv_counts)
+    _expect(recv_counts.dtype == torch.int32 and recv_counts.dim() == 2, "recv_counts must be int32 [n_src, L]")
+    _expect(bool((recv_counts >= 0).all()), "recv_counts must be non-negative")
+    n_src, L = recv_counts.shape
+    rows = int(recv_counts.sum().item())
+    offsets = torch.empty(L + 1, dtype=torch.int32, device=dev)
+    sort_row = torch.empty(max(1, rows), dtype=torch.int32, device=dev)
+    unsort_row = torch.empty(max(1, rows), dtype=torch.int32, device=dev)
+    _call("rhp_recv_plan", dev, _ptr(recv_counts), n_src, L, rows, _ptr(offsets), _ptr(sort_row), _ptr(unsort_row))
+    return RecvPlan(offsets, sort_row[:rows], unsort_row[:rows], rows)
+
+
+def gather_rows(src: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[r] = src[idx[r]] (whole rows; an index outside src's rows gives a zero row)."""
+    dev = _need_cuda(src, idx, out)
+    _expect(src.dim() == 2 and idx.dtype == torch.int32 and idx.dim() == 1, "src must be [rows, h], idx int32 [n]")
+    rows, h = idx.numel(), src.shape[1]
+    if out is None:
+        out = torch.empty(rows, h, dtype=src.dtype, device=dev)
+    _expect(out.dtype == src.dtype and tuple(out.shape) == (rows, h), f"out must be {src.dtype} [{rows}, {h}]")
+    if rows:
+        _call("rhp_gather_rows", dev, _ptr(src), dtype_code(src), src.shape[0], h, _ptr(idx), rows, _ptr(out))
+    return out
+
+
 # ----------------------------------------------------------------------------- expert GEMMs
 
 
@@ -281,33 +325,66 @@ def _check_offsets(offsets: torch.Tensor, G: int) -> None:
     _expect(offsets.dtype == torch.int32 and offsets.numel() == G + 1, f"offsets must be int32 with {G + 1} entries")
 
 
-def _shared_rows(rows_from_offsets: bool, rows_cap: int) -> int | None:
-    # Routed experts share one buffer indexed by the offsets: it must hold rows_cap rows.
-    return rows_cap if rows_from_offsets else None
+def _shared_rows(rows_from_offsets: bool, rows_cap: int) -> int:
+    # Routed experts share one buffer indexed by the offsets, shared experts have a buffer each:
+    # either way every buffer must hold rows_cap rows.
+    return rows_cap
 
 
-_split_ws_cache: dict[int, torch.Tensor] = {}
+def gemm_kernel(dtype: torch.dtype, act: str, h: int, f: int) -> str:
+    """Which kernel the expert GEMMs run for these operands: ``"mfma"`` or ``"generic"``."""
+    code = C.lib().rhp_expert_gemm_kernel(dtype_code_of(dtype), act_code(act), h, f)
+    return "mfma" if code == C.GEMM_KERNEL_MFMA else "generic"
 
 
-def split_workspace(dev: torch.device) -> torch.Tensor:
-    """The K-split workspace of the expert GEMMs on ``dev``: allocated (zeroed) once per device.
+def dtype_code_of(dtype: torch.dtype) -> int:
+    try:
+        return _DT[dtype]
+    except KeyError:
+        raise KernelArgumentError(f"unsupported dtype {dtype}") from None
 
-    Its arrival counters must be zero before a call, and every call leaves them zero; the
-    GEMM calls that use it are stream-ordered on the current stream.
+
+# K-split workspaces, one per (device, stream): its arrival counters are shared by every launch that
+# uses it, so launches on two streams must not share one.
+_split_ws_cache: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def split_workspace(dev: torch.device, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """The K-split workspace of the expert GEMMs for ``stream`` (default: the current stream of ``dev``).
+
+    Allocated and zeroed once per (device, stream).  Its arrival counters must be zero before a call;
+    every call that completes leaves them zero, and a call that fails resets them.
     """
     idx = torch.device(dev).index if torch.device(dev).index is not None else torch.cuda.current_device()
-    ws = _split_ws_cache.get(idx)
+    stream = stream if stream is not None else torch.cuda.current_stream(idx)
+    key = (idx, stream.cuda_stream)
+    ws = _split_ws_cache.get(key)
     if ws is None:
-        ws = torch.zeros(C.lib().rhp_expert_split_workspace_bytes(), dtype=torch.uint8, device=f"cuda:{idx}")
-        _split_ws_cache[idx] = ws
+        with torch.cuda.stream(stream):
+            ws = torch.zeros(C.lib().rhp_expert_split_workspace_bytes(), dtype=torch.uint8, device=f"cuda:{idx}")
+        _split_ws_cache[key] = ws
     return ws
 
 
-def _split_args(dev: torch.device, split: bool) -> tuple:
+def reset_split_workspace(ws: torch.Tensor, stream: torch.cuda.Stream | None = None) -> None:
+    """Zeroes a K-split workspace's arrival counters on ``stream`` (a fill kernel)."""
+    stream = stream if stream is not None else torch.cuda.current_stream(ws.device)
+    with torch.cuda.device(ws.device):
+        C.call("rhp_expert_split_workspace_reset", _ptr(ws), ws.numel(), stream.cuda_stream)
+
+
+def _split_call(name: str, dev: torch.device, split: bool, *args) -> None:
+    """Calls a GEMM entry point with the K-split workspace of the current stream (or none)."""
     if not split:
-        return None, 0
+        _call(name, dev, *args, None, 0)
+        return
     ws = split_workspace(dev)
-    return _ptr(ws), ws.numel()
+    try:
+        _call(name, dev, *args, _ptr(ws), ws.numel())
+    except RuntimeError:
+        # A call that did not complete may have left arrival counters set.
+        reset_split_workspace(ws)
+        raise
 
 
 def expert_fc1_fwd(xs: list[torch.Tensor], offsets: torch.Tensor, rows_from_offsets: bool, rows_cap: int,
@@ -322,8 +399,8 @@ def expert_fc1_fwd(xs: list[torch.Tensor], offsets: torch.Tensor, rows_from_offs
     _check_groups("x", xs, G, dt, h, rows)
     _check_groups("hpre", hpre, G, dt, F1, rows)
     _check_groups("act", act_out, G, dt, f, rows)
-    _call("rhp_expert_fc1_fwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w1[0]),
-          act_code(act), h, f, _arr(xs), _arr(w1), _arr(hpre), _arr(act_out), *_split_args(dev, split))
+    _split_call("rhp_expert_fc1_fwd", dev, split, G, _ptr(offsets), int(rows_from_offsets), rows_cap,
+                dtype_code(w1[0]), act_code(act), h, f, _arr(xs), _arr(w1), _arr(hpre), _arr(act_out))
 
 
 def expert_fc2_fwd(acts: list[torch.Tensor], offsets: torch.Tensor, rows_from_offsets: bool, rows_cap: int,
@@ -335,8 +412,8 @@ def expert_fc2_fwd(acts: list[torch.Tensor], offsets: torch.Tensor, rows_from_of
     _check_groups("w2", w2, G, dt, f, exact_shape=(h, f))
     _check_groups("act", acts, G, dt, f, rows)
     _check_groups("y", ys, G, dt, h, rows)
-    _call("rhp_expert_fc2_fwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w2[0]), h, f,
-          _arr(acts), _arr(w2), _arr(ys), *_split_args(dev, split))
+    _split_call("rhp_expert_fc2_fwd", dev, split, G, _ptr(offsets), int(rows_from_offsets), rows_cap,
+                dtype_code(w2[0]), h, f, _arr(acts), _arr(w2), _arr(ys))
 
 
 def expert_fc2_bwd(dys: list[torch.Tensor], acts: list[torch.Tensor], hpres: list[torch.Tensor],
@@ -353,9 +430,9 @@ def expert_fc2_bwd(dys: list[torch.Tensor], acts: list[torch.Tensor], hpres: lis
     _check_groups("act", acts, G, dt, f, rows)
     _check_groups("hpre", hpres, G, dt, F1, rows)
     _check_groups("dhpre", dhpre, G, dt, F1, rows)
-    _call("rhp_expert_fc2_bwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w2[0]),
-          act_code(act), h, f, _arr(dys), _arr(acts), _arr(hpres), _arr(w2), _arr(dhpre), _arr(dw2),
-          *_split_args(dev, split))
+    _split_call("rhp_expert_fc2_bwd", dev, split, G, _ptr(offsets), int(rows_from_offsets), rows_cap,
+                dtype_code(w2[0]), act_code(act), h, f, _arr(dys), _arr(acts), _arr(hpres), _arr(w2), _arr(dhpre),
+                _arr(dw2))
 
 
 def expert_fc1_bwd(dhpre: list[torch.Tensor], xs: list[torch.Tensor], offsets: torch.Tensor,
@@ -372,9 +449,9 @@ def expert_fc1_bwd(dhpre: list[torch.Tensor], xs: list[torch.Tensor], offsets: t
     _check_groups("x", xs, G, dt, h, rows)
     if dxs:
         _check_groups("dx", dxs, G, dt, h, rows)
-    _call("rhp_expert_fc1_bwd", dev, G, _ptr(offsets), int(rows_from_offsets), rows_cap, dtype_code(w1[0]),
-          act_code(act), h, f, _arr(dhpre), _arr(xs), _arr(w1), _arr(dxs) if dxs else None, _arr(dw1),
-          *_split_args(dev, split))
+    _split_call("rhp_expert_fc1_bwd", dev, split, G, _ptr(offsets), int(rows_from_offsets), rows_cap,
+                dtype_code(w1[0]), act_code(act), h, f, _arr(dhpre), _arr(xs), _arr(w1), _arr(dxs) if dxs else None,
+                _arr(dw1))
 
 
 # ----------------------------------------------------------------------------- optimizer

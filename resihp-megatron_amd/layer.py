@@ -204,6 +204,78 @@ class _MoELayerFn(torch.autograd.Function):
         return (None, None, dx, dwr, None, *dw1, *dw2, *sdw1, *sdw2)
 
 
+class _ExpertChunksFn(torch.autograd.Function):
+    """The receiving side of expert parallelism: the expert FFN over a source-major received buffer.
+
+    resihp/runtime/moe.py:213-224 runs ``expert_ffn`` on every (source, expert) chunk of the received
+    rows in order and returns the outputs in that order.  Here the chunks are regrouped expert-major
+    (a row gather), every local expert is one group of the grouped GEMMs, and the outputs are gathered
+    back into the received order.  The backward mirrors it: the output gradient rows arrive in the
+    received order, are regrouped, run through the expert backward, and the input gradient leaves in
+    the received order again.
+    """
+
+    @staticmethod
+    def forward(ctx, act, f, recv_counts, recv, *weights):
+        G = len(weights) // 2
+        fc1s, fc2s = list(weights[:G]), list(weights[G:])
+        plan = K.recv_plan(recv_counts)
+        P, h = plan.rows, recv.shape[1]
+        if recv.shape[0] != P:
+            raise K.KernelArgumentError(f"the received buffer has {recv.shape[0]} rows, the counts {P}")
+        F1 = _fc1_rows(act, f)
+        xs = K.gather_rows(recv, plan.sort_row)
+        hpre = recv.new_empty(P, F1)
+        a = recv.new_empty(P, f)
+        y = recv.new_empty(P, h)
+        if P > 0:
+            K.expert_fc1_fwd([xs] * G, plan.offsets, True, P, fc1s, f, act, [hpre] * G, [a] * G)
+            K.expert_fc2_fwd([a] * G, plan.offsets, True, P, fc2s, [y] * G)
+        ctx.act, ctx.f, ctx.P = act, f, P
+        ctx.save_for_backward(plan.offsets, plan.sort_row, plan.unsort_row, xs, hpre, a, *fc1s, *fc2s)
+        return K.gather_rows(y, plan.unsort_row)
+
+    @staticmethod
+    def backward(ctx, dy_recv):
+        offsets, sort_row, unsort_row, xs, hpre, a, *ws = ctx.saved_tensors
+        G = len(ws) // 2
+        fc1s, fc2s = ws[:G], ws[G:]
+        act, f, P = ctx.act, ctx.f, ctx.P
+        dw1 = [torch.empty_like(w) for w in fc1s]
+        dw2 = [torch.empty_like(w) for w in fc2s]
+        drecv = None
+        if P > 0:
+            dy = K.gather_rows(dy_recv.contiguous(), sort_row)
+            dhpre = torch.empty_like(hpre)
+            K.expert_fc2_bwd([dy] * G, [a] * G, [hpre] * G, offsets, True, P, list(fc2s), act, [dhpre] * G, dw2)
+            need_x = ctx.needs_input_grad[3]
+            dxp = torch.empty_like(xs) if need_x else None
+            K.expert_fc1_bwd([dhpre] * G, [xs] * G, offsets, True, P, list(fc1s), f, act,
+                             [dxp] * G if need_x else None, dw1)
+            if need_x:
+                drecv = K.gather_rows(dxp, unsort_row)
+        else:
+            for w in (*dw1, *dw2):
+                w.zero_()
+            drecv = torch.zeros_like(xs)
+        return (None, None, None, drecv, *dw1, *dw2)
+
+
+def expert_chunks(recv: torch.Tensor, recv_counts: torch.Tensor, fc1s: list[torch.Tensor],
+                  fc2s: list[torch.Tensor], act: str = "swiglu") -> torch.Tensor:
+    """Expert outputs of a received buffer, in the received order (with autograd).
+
+    ``recv`` holds the rows the all-to-all delivered, source-major: chunk (s, i) of
+    ``recv_counts[s, i]`` rows for local expert i (``fc1s[i]``, ``fc2s[i]``), rows in the sender's
+    (token, slot) order, as resihp/runtime/moe.py:199-212 builds and exchanges them.
+    ``recv_counts`` is an int32 ``[n_src, L]`` device tensor.
+    """
+    if len(fc1s) != len(fc2s) or recv_counts.dim() != 2 or recv_counts.shape[1] != len(fc1s):
+        raise ValueError("need one fc1 and one fc2 weight per column of recv_counts")
+    f = fc2s[0].shape[1]
+    return _ExpertChunksFn.apply(act, f, recv_counts.contiguous(), recv.contiguous(), *fc1s, *fc2s)
+
+
 def moe_layer(meta: LayerMeta, x: torch.Tensor, router_w: torch.Tensor, bias: torch.Tensor | None,
               fc1s: list[torch.Tensor], fc2s: list[torch.Tensor], shared_fc1s: list[torch.Tensor] = (),
               shared_fc2s: list[torch.Tensor] = (), fp8: Fp8State | None = None) -> tuple[torch.Tensor, torch.Tensor]:

@@ -28,7 +28,7 @@ from dataclasses import dataclass
 import torch
 
 from . import kernels as K
-from .layer import LayerMeta, moe_layer
+from .layer import LayerMeta, expert_chunks, moe_layer
 from .placement import ExpertPlacement, expert_dp_groups, smooth_weighted_round_robin
 from .rng import generator
 from .state import FULL, GroupSpec, Holdings, TensorSpec
@@ -353,15 +353,39 @@ class EPRuntime:
         self.tokens_per_expert = counts[:E].to(torch.float64)
         return out
 
-    def global_loads(self) -> list[float]:
-        """Tokens routed to each expert in the last forward, summed over all data-parallel ranks."""
-        loads = self.tokens_per_expert.detach().cpu().clone()
-        group = self.comms.group("dp") if self.comms is not None else None
-        if group is not None:
-            import torch.distributed as dist
+    def expert_outputs(self, recv: torch.Tensor, recv_counts: torch.Tensor) -> torch.Tensor:
+        """The receiving side of the expert-parallel exchange (moe.py:213-224) for this device's experts.
 
-            self.wait(dist.all_reduce(loads, group=group, async_op=True))
-        return loads.tolist()
+        ``recv`` holds the rows the dispatch all-to-all delivered, source-major, and ``recv_counts``
+        ``[n_src, E]`` the exchanged counts (moe.py:209): chunk (s, e) holds ``recv_counts[s, e]``
+        rows for expert e.  Returns the expert outputs in the received order, the order in which the
+        reverse all-to-all sends them back (moe.py:224).  Rows for an expert this device does not
+        host raise RuntimeError, as in the reference (moe.py:218-219).
+        """
+        cfg, E = self.cfg, self.cfg.num_experts
+        counts = torch.as_tensor(recv_counts).detach().to("cpu", torch.int64)
+        if counts.dim() != 2 or counts.shape[1] != E:
+            raise ValueError(f"recv_counts must be [n_src, {E}]")
+        local = sorted(self.local_experts)
+        for e in range(E):
+            if e not in local and bool((counts[:, e] != 0).any()):
+                raise RuntimeError(f"{self.me} received tokens for expert {e} it does not host")
+        local_counts = counts[:, local].to(torch.int32).to(recv.device).contiguous()
+        fc1s = [self.params[f"experts.{e}.fc1.weight"] for e in local]
+        fc2s = [self.params[f"experts.{e}.fc2.weight"] for e in local]
+        return expert_chunks(recv, local_counts, fc1s, fc2s, cfg.act)
+
+    def _single_device(self, name: str) -> None:
+        """Collectives are not part of this build: a group with more than one device raises."""
+        if self.comms is not None and self.comms.group(name) is not None:
+            raise NotImplementedError(f"cross-GPU reductions over group {name!r} are not part of this build; "
+                                      "every group must be a single device")
+
+    def global_loads(self) -> list[float]:
+        """Tokens routed to each expert in the last forward (moe.py:228-234).  On a single device the
+        data-parallel group is the device itself, so the global loads are the local ones."""
+        self._single_device("dp")
+        return self.tokens_per_expert.detach().cpu().tolist()
 
     def finish_iteration(self) -> None:
         """Aux-loss-free bias update from the global loads (moe.py:236-240)."""
@@ -371,34 +395,12 @@ class EPRuntime:
             update_expert_bias(self.cfg, bias, loads)
 
     def sync_grads(self) -> None:
-        """moe.py:242-265: all-reduce router grads over dp and expert grads over their holder groups."""
-        if self.comms is None:
-            return
-        import torch.distributed as dist
-
-        def flat(keys):
-            return torch.cat([(self.params[k].grad if self.params[k].grad is not None
-                               else torch.zeros_like(self.params[k])).reshape(-1) for k in keys])
-
-        def unflat(buf, keys):
-            off = 0
-            for k in keys:
-                p = self.params[k]
-                p.grad = buf[off:off + p.numel()].view_as(p).clone()
-                off += p.numel()
-
-        jobs = [("dp", ["router.weight"])]
-        for holders, experts in sorted(expert_dp_groups(self.placement).items()):
+        """moe.py:242-265 on a single device: the router's data-parallel group and every expert's
+        holder group are this device alone, so there is nothing to reduce."""
+        self._single_device("dp")
+        for holders in expert_dp_groups(self.placement):
             if self.me in holders and len(holders) > 1:
-                keys = [f"experts.{e}.{n}" for e in experts for n in ("fc1.weight", "fc2.weight")]
-                jobs.append((edp_group_name(holders), keys))
-        for name, keys in jobs:
-            group = self.comms.group(name)
-            if group is None:
-                continue
-            buf = flat(keys)
-            self.wait(dist.all_reduce(buf, group=group, async_op=True))
-            unflat(buf, keys)
+                self._single_device(edp_group_name(holders))
 
 
 __all__ = ["MoEConfig", "moe_specs", "expert_of", "init_param", "update_expert_bias", "batch", "route", "expert_ffn",

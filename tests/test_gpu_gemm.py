@@ -102,24 +102,46 @@ def test_grouped_expert_gemms(case, act):
         assert rel_err(c64(dw1[g]), dh_g[r0:r1].t() @ xs) <= bar, ("dw1", g)
 
 
-def test_per_group_buffers_shared_expert_mode():
-    """rows_from_offsets = 0: each group reads its own buffer from row 0 (shared experts)."""
-    dt, h, f, T, S = torch.bfloat16, 256, 128, 200, 2
-    offs = torch.arange(S + 1, dtype=torch.int32) * T
+@pytest.mark.parametrize("T", [200, 513, 2048])
+def test_per_group_buffers_shared_expert_mode(T):
+    """rows_from_offsets = 0: each group reads and writes its own buffer from row 0 (shared experts).
+
+    The grid must cover every group's row tiles: with two groups of T rows each that is 2 ceil(T / 256)
+    row tiles, more than ceil(T / 256) + 2 once T exceeds 512 (2048: 16 against 10).  Every output and
+    gradient of both groups is checked, forward and backward.
+    """
+    dt, h, f, S, act = torch.bfloat16, 256, 128, 2, "swiglu"
+    offs = (torch.arange(S + 1, dtype=torch.int32) * T).to(DEV)
     xs = [seeded((T, h), 5 + s, 1.0, dt) for s in range(S)]
     w1 = [seeded((2 * f, h), 50 + s, 0.05, dt) for s in range(S)]
     w2 = [seeded((h, f), 60 + s, 0.05, dt) for s in range(S)]
-    say("gemm shared-expert buffers")
+    dys = [seeded((T, h), 70 + s, 1.0, dt) for s in range(S)]
+    d = lambda ts: [t.to(DEV) for t in ts]  # noqa: E731
+    xs_d, w1_d, w2_d, dys_d = d(xs), d(w1), d(w2), d(dys)
+    say(f"gemm shared-expert buffers T={T}")
     hs = [torch.empty(T, 2 * f, dtype=dt, device=DEV) for _ in range(S)]
     as_ = [torch.empty(T, f, dtype=dt, device=DEV) for _ in range(S)]
     ys = [torch.empty(T, h, dtype=dt, device=DEV) for _ in range(S)]
-    K.expert_fc1_fwd([x.to(DEV) for x in xs], offs.to(DEV), False, T, [w.to(DEV) for w in w1], f, "swiglu", hs, as_)
-    K.expert_fc2_fwd(as_, offs.to(DEV), False, T, [w.to(DEV) for w in w2], ys)
+    K.expert_fc1_fwd(xs_d, offs, False, T, w1_d, f, act, hs, as_)
+    K.expert_fc2_fwd(as_, offs, False, T, w2_d, ys)
+    dh = [torch.empty(T, 2 * f, dtype=dt, device=DEV) for _ in range(S)]
+    dw2 = [torch.empty_like(w) for w in w2_d]
+    K.expert_fc2_bwd(dys_d, as_, hs, offs, False, T, w2_d, act, dh, dw2)
+    dx = [torch.empty(T, h, dtype=dt, device=DEV) for _ in range(S)]
+    dw1 = [torch.empty_like(w) for w in w1_d]
+    K.expert_fc1_bwd(dh, xs_d, offs, False, T, w1_d, f, act, dx, dw1)
     torch.cuda.synchronize()
+    c64 = lambda t: t.detach().cpu().double()  # noqa: E731
     for s in range(S):
-        ref = (F.silu(xs[s].double() @ w1[s].double()[:f].t()) * (xs[s].double() @ w1[s].double()[f:].t()))
-        assert rel_err(as_[s], ref) <= 1e-2
-        assert rel_err(ys[s], as_[s].cpu().double() @ w2[s].double().t()) <= 1e-2
+        x64, a64, h64, dh64, dy64 = c64(xs[s]), c64(as_[s]), c64(hs[s]), c64(dh[s]), c64(dys[s])
+        ref_h = x64 @ c64(w1[s]).t()
+        assert rel_err(h64, ref_h) <= 1e-2, ("hpre", s)
+        assert rel_err(a64, _act(act, ref_h, f)) <= 1e-2, ("act", s)
+        assert rel_err(ys[s], a64 @ c64(w2[s]).t()) <= 1e-2, ("y", s)
+        assert rel_err(dh64, _act_bwd(act, dy64 @ c64(w2[s]), h64, f)) <= 1e-2, ("dhpre", s)
+        assert rel_err(dw2[s], dy64.t() @ a64) <= 1e-2, ("dw2", s)
+        assert rel_err(dx[s], dh64 @ c64(w1[s])) <= 1e-2, ("dx", s)
+        assert rel_err(dw1[s], dh64.t() @ x64) <= 1e-2, ("dw1", s)
 
 
 def test_gemm_deterministic():
@@ -193,3 +215,118 @@ def test_k_split_tiles(case):
         ref_dx = c64(dh[sel]) @ c64(w1[g])
         assert rel_err(c64(y_s[sel]), ref_y) <= 1e-2, ("y", g)
         assert rel_err(c64(dx_s[sel]), ref_dx) <= 1e-2, ("dxp", g)
+
+
+def test_mixtral_shape_beyond_2gib_buffers():
+    """Row buffers past 2 GiB on the MFMA kernel: the Mixtral hidden/ffn sizes with 40960 routed pairs
+    (20480 tokens at top-2), pre-activations [40960, 28672] bf16 = 2.35 GB.  One hot expert holds 38000
+    rows, so its weight-gradient reduction runs past 2 GiB of its own pre-activation gradient rows (37449
+    rows of 57 KB).  Sampled rows of every output and sampled elements of both weight gradients are
+    checked against float64 on the kernel's own inputs."""
+    dt, h, f, act = torch.bfloat16, 4096, 14336, "swiglu"
+    counts = [38000, 2960]
+    G, F1 = len(counts), 2 * f
+    assert K.gemm_kernel(dt, act, h, f) == "mfma"
+    offs = torch.tensor([0] + list(torch.tensor(counts).cumsum(0).tolist()), dtype=torch.int32)
+    P = int(offs[-1])
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    rnd = lambda *s, std=1.0: (torch.randn(*s, generator=gen, device=DEV) * std).to(dt)  # noqa: E731
+    xp, dy = rnd(P, h), rnd(P, h)
+    w1 = [rnd(F1, h, std=0.02) for _ in range(G)]
+    w2 = [rnd(h, f, std=0.02) for _ in range(G)]
+    offs_d = offs.to(DEV)
+    say(f"gemm beyond 2 GiB: P={P} counts={counts}")
+    hpre = torch.empty(P, F1, dtype=dt, device=DEV)
+    a = torch.empty(P, f, dtype=dt, device=DEV)
+    y = torch.empty(P, h, dtype=dt, device=DEV)
+    K.expert_fc1_fwd([xp] * G, offs_d, True, P, w1, f, act, [hpre] * G, [a] * G)
+    K.expert_fc2_fwd([a] * G, offs_d, True, P, w2, [y] * G)
+    dhpre = torch.empty(P, F1, dtype=dt, device=DEV)
+    dw2 = [torch.empty_like(w) for w in w2]
+    K.expert_fc2_bwd([dy] * G, [a] * G, [hpre] * G, offs_d, True, P, w2, act, [dhpre] * G, dw2)
+    dxp = torch.empty(P, h, dtype=dt, device=DEV)
+    dw1 = [torch.empty_like(w) for w in w1]
+    K.expert_fc1_bwd([dhpre] * G, [xp] * G, offs_d, True, P, w1, f, act, [dxp] * G, dw1)
+    torch.cuda.synchronize()
+    assert hpre.numel() * 2 > 2 ** 31
+    c64 = lambda t: t.detach().cpu().double()  # noqa: E731
+    g8 = torch.Generator().manual_seed(3)
+    for g in range(G):
+        r0, r1 = int(offs[g]), int(offs[g + 1])
+        # 16 rows of the group, always including its first and last
+        rows = torch.cat([torch.tensor([r0, r1 - 1]), torch.randint(r0, r1, (14,), generator=g8)]).to(DEV)
+        x64, dy64, h64, a64, dh64 = (c64(t[rows]) for t in (xp, dy, hpre, a, dhpre))
+        ref_h = x64 @ c64(w1[g]).t()
+        assert rel_err(h64, ref_h) <= 1e-2, ("hpre", g)
+        assert rel_err(a64, _act(act, ref_h, f)) <= 1e-2, ("act", g)
+        assert rel_err(c64(y[rows]), a64 @ c64(w2[g]).t()) <= 1e-2, ("y", g)
+        assert rel_err(dh64, _act_bwd(act, dy64 @ c64(w2[g]), h64, f)) <= 1e-2, ("dhpre", g)
+        assert rel_err(c64(dxp[rows]), dh64 @ c64(w1[g])) <= 1e-2, ("dxp", g)
+        # weight gradients: 16 x 64 sampled elements, each a sum over all of the group's rows
+        o2 = torch.randint(0, h, (16,), generator=g8)
+        i2 = torch.randint(0, f, (64,), generator=g8)
+        ref2 = c64(dy[r0:r1][:, o2.to(DEV)]).t() @ c64(a[r0:r1][:, i2.to(DEV)])
+        assert rel_err(c64(dw2[g])[o2][:, i2], ref2) <= 1e-2, ("dw2", g)
+        o1 = torch.cat([torch.tensor([0, F1 - 1]), torch.randint(0, F1, (14,), generator=g8)])
+        i1 = torch.randint(0, h, (64,), generator=g8)
+        ref1 = c64(dhpre[r0:r1][:, o1.to(DEV)]).t() @ c64(xp[r0:r1][:, i1.to(DEV)])
+        assert rel_err(c64(dw1[g])[o1][:, i1], ref1) <= 1e-2, ("dw1", g)
+
+
+def test_kernel_choice_and_alignment():
+    """bfloat16 shapes the MFMA kernel takes run on it (any row count); an unaligned bfloat16 operand
+    is an error, not a silent switch to the generic kernel; other shapes and dtypes take the generic one."""
+    assert K.gemm_kernel(torch.bfloat16, "swiglu", 4096, 14336) == "mfma"
+    assert K.gemm_kernel(torch.bfloat16, "gelu", 40, 24) == "generic"
+    assert K.gemm_kernel(torch.float32, "swiglu", 4096, 14336) == "generic"
+    assert K.gemm_kernel(torch.float64, "gelu", 64, 128) == "generic"
+    dt, h, f, P = torch.bfloat16, 256, 128, 300
+    offs = torch.tensor([0, P], dtype=torch.int32, device=DEV)
+    flat = torch.zeros(P * h + 1, dtype=dt, device=DEV)
+    xp = flat[1:].view(P, h)      # 2 bytes past a 16-byte boundary
+    w1 = [seeded((2 * f, h), 1, 0.05, dt).to(DEV)]
+    hp = torch.empty(P, 2 * f, dtype=dt, device=DEV)
+    a = torch.empty(P, f, dtype=dt, device=DEV)
+    say("gemm unaligned operand")
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        K.expert_fc1_fwd([xp], offs, True, P, w1, f, "swiglu", [hp], [a])
+
+
+def test_k_split_workspace_per_stream():
+    """Each stream gets its own K-split workspace, so split products on two streams at once do not
+    share arrival counters: both give the bits of the same product run alone.  A reset leaves the
+    counters zero and the next call correct."""
+    dt, h, f, counts = torch.bfloat16, 512, 8192, [300, 40]
+    G = len(counts)
+    offs = torch.tensor([0, 300, 340], dtype=torch.int32, device=DEV)
+    P = 340
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    a = [(torch.randn(P, f, generator=gen, device=DEV)).to(dt) for _ in range(2)]
+    w2 = [(torch.randn(h, f, generator=gen, device=DEV) * 0.02).to(dt) for _ in range(G)]
+    say("gemm k-split workspace per stream")
+    alone = []
+    for i in range(2):
+        y = torch.empty(P, h, dtype=dt, device=DEV)
+        K.expert_fc2_fwd([a[i]] * G, offs, True, P, w2, [y] * G)
+        alone.append(y)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=DEV)
+    main = torch.cuda.current_stream(DEV)
+    assert K.split_workspace(torch.device(DEV), side).data_ptr() != K.split_workspace(torch.device(DEV), main).data_ptr()
+    side.wait_stream(main)
+    outs = [torch.empty(P, h, dtype=dt, device=DEV) for _ in range(2)]
+    for _ in range(3):
+        with torch.cuda.stream(side):
+            K.expert_fc2_fwd([a[1]] * G, offs, True, P, w2, [outs[1]] * G)
+        K.expert_fc2_fwd([a[0]] * G, offs, True, P, w2, [outs[0]] * G)
+    main.wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], alone[0]) and torch.equal(outs[1], alone[1])
+    ws = K.split_workspace(torch.device(DEV))
+    K.reset_split_workspace(ws)
+    y = torch.empty(P, h, dtype=dt, device=DEV)
+    K.expert_fc2_fwd([a[0]] * G, offs, True, P, w2, [y] * G)
+    torch.cuda.synchronize()
+    assert torch.equal(y, alone[0])
+    counters = ws[K.C.lib().rhp_expert_split_workspace_bytes() - 4 * 256:].view(torch.int32)
+    assert int(counters.abs().sum()) == 0
