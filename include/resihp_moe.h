@@ -92,6 +92,21 @@ int rhp_dispatch(const int32_t* topi, int64_t T, int k, int E, int e0, int e1, i
                  size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * rhp_dispatch without a workspace argument and without allocating: the same
+ * plan, bit for bit, with a fixed 4 MiB device array of the library (one per
+ * GPU, kept until the process ends) as its workspace.  No counterpart in the
+ * reference: an entry point for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Sizes whose rhp_dispatch_workspace_bytes() exceeds 4 MiB are
+ * rejected.  The stream's device must be current.  All calls on one GPU share
+ * its array, so calls that overlap on one GPU (different streams without
+ * ordering) race; stream-ordered calls are safe, since every call writes each
+ * scratch entry it reads.
+ */
+int rhp_dispatch_noalloc(const int32_t* topi, int64_t T, int k, int E, int e0, int e1, int n_src, int32_t* counts,
+                         int32_t* offsets, int32_t* src_counts, int32_t* perm, int32_t* pair_row, hipStream_t stream);
+
+/*
  * Aux-loss-free bias update: bias[e] += rate * sign(mean(counts) - counts[e]).
  * Replaces update_expert_bias (moe.py:64-66).  bias: [E] r_dtype; counts: int32 [E].
  */

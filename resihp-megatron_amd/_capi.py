@@ -31,6 +31,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "rhp_route": (_i, [_p, _i, _p, _i, _p, _i64, _i, _i, _i, _i, _i, _d, _p, _p, _p, _p]),
     "rhp_dispatch_workspace_bytes": (_sz, [_i64, _i, _i, _i]),
     "rhp_dispatch": (_i, [_p, _i64, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _sz, _p]),
+    "rhp_dispatch_noalloc": (_i, [_p, _i64, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p]),
     "rhp_update_expert_bias": (_i, [_p, _i, _p, _i, _d, _p]),
     "rhp_permute": (_i, [_p, _i, _i64, _i, _i, _p, _p, _p]),
     "rhp_combine": (_i, [_p, _p, _p, _i, _p, _p, _pp, _i, _i, _i64, _i, _i, _p, _p]),

@@ -11,6 +11,8 @@
 #pragma clang fp contract(off)
 
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 #include "rhp_common.h"
 
@@ -677,18 +679,25 @@ extern "C" size_t rhp_dispatch_workspace_bytes(int64_t T, int k, int E, int n_sr
     return static_cast<size_t>(nblk) * (2 * static_cast<size_t>(E) + 2) * sizeof(int32_t) + 256;
 }
 
-extern "C" int rhp_dispatch(const int32_t* topi, int64_t T, int k, int E, int e0, int e1, int n_src,
-                            int32_t* counts, int32_t* offsets, int32_t* src_counts, int32_t* perm, int32_t* pair_row,
-                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    clear_error();
-    RHP_REQUIRE(T >= 0 && k >= 1 && E >= 1 && E <= kMaxE, "rhp_dispatch: need T >= 0, k >= 1, 1 <= E <= 1024");
-    RHP_REQUIRE(0 <= e0 && e0 < e1 && e1 <= E, "rhp_dispatch: need 0 <= e0 < e1 <= E");
-    RHP_REQUIRE(n_src >= 1 && n_src <= (1 << 20), "rhp_dispatch: need 1 <= n_src <= 2^20");
-    RHP_REQUIRE(T * k < (int64_t(1) << 31), "rhp_dispatch: T * k must fit in int32");
+namespace rhp {
+namespace {
+
+// The dispatch plan with its workspace: argument checks, then the count,
+// scan and scatter kernels.  Every launch writes each workspace entry it
+// reads (per-block histograms, sources and base rows), so the workspace
+// needs no clearing.
+int dispatch_run(const char* fn, const int32_t* topi, int64_t T, int k, int E, int e0, int e1, int n_src,
+                 int32_t* counts, int32_t* offsets, int32_t* src_counts, int32_t* perm, int32_t* pair_row,
+                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    const std::string f(fn);
+    RHP_REQUIRE(T >= 0 && k >= 1 && E >= 1 && E <= kMaxE, f + ": need T >= 0, k >= 1, 1 <= E <= 1024");
+    RHP_REQUIRE(0 <= e0 && e0 < e1 && e1 <= E, f + ": need 0 <= e0 < e1 <= E");
+    RHP_REQUIRE(n_src >= 1 && n_src <= (1 << 20), f + ": need 1 <= n_src <= 2^20");
+    RHP_REQUIRE(T * k < (int64_t(1) << 31), f + ": T * k must fit in int32");
     RHP_REQUIRE(workspace_bytes >= rhp_dispatch_workspace_bytes(T, k, E, n_src),
-                "rhp_dispatch: workspace smaller than rhp_dispatch_workspace_bytes()");
-    RHP_REQUIRE(counts && offsets && src_counts && workspace, "rhp_dispatch: null pointer");
-    RHP_REQUIRE(T == 0 || (topi && perm && pair_row), "rhp_dispatch: null pointer");
+                f + ": workspace smaller than rhp_dispatch_workspace_bytes()");
+    RHP_REQUIRE(counts && offsets && src_counts && workspace, f + ": null pointer");
+    RHP_REQUIRE(T == 0 || (topi && perm && pair_row), f + ": null pointer");
     DispatchShape d;
     d.T = T;
     d.k = k;
@@ -715,6 +724,66 @@ extern "C" int rhp_dispatch(const int32_t* topi, int64_t T, int k, int E, int e0
         if (int rc = check_launch("dispatch_scatter_kernel")) return rc;
     }
     return 0;
+}
+
+}  // namespace
+}  // namespace rhp
+
+extern "C" int rhp_dispatch(const int32_t* topi, int64_t T, int k, int E, int e0, int e1, int n_src,
+                            int32_t* counts, int32_t* offsets, int32_t* src_counts, int32_t* perm, int32_t* pair_row,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    return dispatch_run("rhp_dispatch", topi, T, k, E, e0, e1, n_src, counts, offsets, src_counts, perm, pair_row,
+                        workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------- dispatch without allocation
+
+// The workspace of rhp_dispatch_noalloc: a fixed device array, one per GPU,
+// held until the process ends.  In host code its name is not a device
+// address; the address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace rhp {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's scratch array (the current device's).
+int scratch_of_current_device(const char* fn, void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(std::string(fn) + ": no current HIP device");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return fail(std::string(fn) + ": hipGetSymbolAddress of the scratch array failed: " + hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+}  // namespace rhp
+
+extern "C" int rhp_dispatch_noalloc(const int32_t* topi, int64_t T, int k, int E, int e0, int e1, int n_src,
+                                    int32_t* counts, int32_t* offsets, int32_t* src_counts, int32_t* perm,
+                                    int32_t* pair_row, hipStream_t stream) {
+    clear_error();
+    RHP_REQUIRE(T >= 0 && k >= 1 && E >= 1 && n_src >= 1, "rhp_dispatch_noalloc: need T >= 0, k >= 1, E >= 1, n_src >= 1");
+    const size_t need = rhp_dispatch_workspace_bytes(T, k, E, n_src);
+    RHP_REQUIRE(need <= kScratchBytes, "rhp_dispatch_noalloc: these sizes need " + std::to_string(need) +
+                                           " bytes of scratch, more than the library's 4 MiB; use rhp_dispatch");
+    void* ws = nullptr;
+    if (int rc = scratch_of_current_device("rhp_dispatch_noalloc", &ws)) return rc;
+    return dispatch_run("rhp_dispatch_noalloc", topi, T, k, E, e0, e1, n_src, counts, offsets, src_counts, perm,
+                        pair_row, ws, kScratchBytes, stream);
 }
 
 extern "C" int rhp_update_expert_bias(void* bias, int r_dtype, const int32_t* counts, int E, double rate,
