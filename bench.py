@@ -48,6 +48,9 @@ WORKLOADS = {
     "ep128-share": (32768, 2048, 768, 128, 8, "softmax", 0, (0, 16), 8, "zipf", False),
     "mixtral-fp8": (16384, 4096, 14336, 8, 2, "softmax", 0, None, 1, None, True),
 }
+# Workloads that start from a received buffer (the receiving side of the expert exchange) instead of
+# routing their own tokens through the whole layer.
+RECEIVED = {"ep128-share"}
 
 GEMM_CALLS = ("rhp_expert_fc1_fwd", "rhp_expert_fc2_fwd", "rhp_expert_fc2_bwd", "rhp_expert_fc1_bwd", "rhp_fp8_gemm",
               "rhp_fp8_gemm_cast")
@@ -122,6 +125,41 @@ def build_workload(name: str, dev: torch.device):
                 fc2=fc2, s1=s1, s2=s2, bias=bias, x=x, dout=dout, fp8=st)
 
 
+def build_received(pkg, w, dev):
+    """The received buffer of the GPU holding the local window: the workload's tokens are split into
+    n_src sources (even_split), routed once, and every source's rows for the local experts are laid out
+    source-major, expert-major within a source, (token, slot) ascending within an expert -- the order
+    the reference's dispatch exchange delivers (resihp/runtime/moe.py:193-212).  Built once, before
+    timing (it stands for what the all-to-all delivers)."""
+    import importlib
+
+    K = importlib.import_module(f"{pkg.__name__}.kernels")
+    T, k, E, e0, e1, n_src = w["T"], w["k"], w["E"], w["e0"], w["e1"], w["n_src"]
+    with torch.no_grad():
+        _, topi, _ = K.route(w["x"].detach(), w["router"].detach(), w["bias"], k, w["score"])
+        plan = K.dispatch(topi, E, e0, e1, n_src)
+        P = int(plan.offsets[-1].item())
+        pairs = plan.perm[:P].long()
+        tok = pairs // k
+        expert = topi.reshape(-1).long()[pairs] - e0
+        bounds = torch.tensor([(T // n_src) * (s + 1) + min(s + 1, T % n_src) for s in range(n_src)], device=dev)
+        src = torch.searchsorted(bounds, tok, right=True)
+        order = torch.sort(src * (e1 - e0) + expert, stable=True).indices
+        recv = w["x"].detach()[tok[order]].contiguous().requires_grad_(True)
+    g = torch.Generator(device=dev).manual_seed(99)
+    dy = (torch.randn(P, w["h"], generator=g, device=dev)).to(torch.bfloat16)
+    return recv, plan.src_counts.contiguous(), dy
+
+
+def recv_step(pkg, w):
+    """The receiving side of the expert exchange: expert outputs of the received rows, then the backward
+    from their gradient (resihp/runtime/moe.py:213-224 and its autograd)."""
+    for p in (w["recv"], *w["fc1"], *w["fc2"]):
+        p.grad = None
+    y = pkg.layer.expert_chunks(w["recv"], w["recv_counts"], w["fc1"], w["fc2"], "swiglu", rows=w["recv"].shape[0])
+    y.backward(w["recv_dy"])
+
+
 def gpu_step(pkg, w, meta):
     for p in (w["x"], w["router"], *w["fc1"], *w["fc2"], *w["s1"], *w["s2"]):
         p.grad = None
@@ -133,24 +171,64 @@ def gpu_step(pkg, w, meta):
     return counts
 
 
-def cpu_baseline(name: str, sample_tokens: int, reps: int = 3) -> dict:
-    """The float32 CPU restatement of the reference layer (oracle), fwd + bwd on a token sample."""
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(name: str, sample_tokens: int, reps: int = 3, received_rows: int | None = None) -> dict:
+    """The float32 CPU restatement of the reference layer (oracle), fwd + bwd on a token sample.
+
+    For a received-buffer workload (``received_rows`` = the P rows one step processes) the sample is
+    the reference's receiving side instead: expert_ffn chunk by chunk (resihp/runtime/moe.py:213-223)
+    over 8 sources x 16 rows of each local expert, scaled to source tokens per second by T / P.
+    """
     if str(ROOT) not in sys.path:
         sys.path.insert(0, str(ROOT))
     from oracle import moe_ref as M
 
-    T, h, f, E, k, score, S = WORKLOADS[name][:7]
+    T, h, f, E, k, score, S, window, n_src = WORKLOADS[name][:9]
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(5)
+    times = []
+    if received_rows:
+        L = window[1] - window[0]
+        w1 = [torch.empty(2 * f, h).normal_(0.0, 0.02, generator=g).requires_grad_(True) for _ in range(L)]
+        w2 = [torch.empty(h, f).normal_(0.0, 0.02, generator=g).requires_grad_(True) for _ in range(L)]
+        chunk = 16
+        rows = n_src * L * chunk
+        x = torch.randn(rows, h, generator=g).requires_grad_(True)
+        dy = torch.randn(rows, h, generator=g)
+        for i in range(reps + 1):
+            for p in (x, *w1, *w2):
+                p.grad = None
+            t0 = time.perf_counter()
+            outs = [M.expert_ffn(x[c * chunk:(c + 1) * chunk], w1[c % L], w2[c % L], "swiglu")
+                    for c in range(n_src * L)]
+            torch.cat(outs).backward(dy)
+            dt = time.perf_counter() - t0
+            if i:
+                times.append(dt)
+        med = sorted(times)[len(times) // 2]
+        return {"value": rows / med * T / received_rows, "unit": "tokens/s", "cores": cores, "kind": "port",
+                "cpu": cpu_model(),
+                "sample": f"{rows} of the {received_rows} received rows ({n_src} sources x {L} experts x {chunk} "
+                          f"rows), float32 torch CPU restatement of the reference's per-chunk expert_ffn, fwd+bwd, "
+                          f"median of {reps} after 1 warm-up, scaled by {T} source tokens / {received_rows} rows; "
+                          f"torch {torch.__version__}"}
     cfg = M.OracleConfig(hidden=h, ffn=f, num_experts=E, top_k=k, tokens=sample_tokens, act="swiglu", score=score,
                          num_shared=S, shared_ffn=f if S else 0, dtype=torch.float32)
-    g = torch.Generator().manual_seed(5)
     params = {}
     for key, (shape, _) in M.param_shapes(cfg).items():
         params[key] = torch.empty(shape, dtype=torch.float32).normal_(0.0, 0.02, generator=g).requires_grad_(True)
     x = torch.randn(sample_tokens, h, generator=g).requires_grad_(True)
     dout = torch.randn(sample_tokens, h, generator=g)
-    times = []
     for i in range(reps + 1):
         for p in (x, *params.values()):
             p.grad = None
@@ -160,7 +238,7 @@ def cpu_baseline(name: str, sample_tokens: int, reps: int = 3) -> dict:
         if i:
             times.append(dt)
     med = sorted(times)[len(times) // 2]
-    return {"value": sample_tokens / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+    return {"value": sample_tokens / med, "unit": "tokens/s", "cores": cores, "kind": "port", "cpu": cpu_model(),
             "sample": f"{sample_tokens} of {T} tokens, float32 torch CPU restatement of the reference layer, "
                       f"fwd+bwd, median of {reps} after 1 warm-up; torch {torch.__version__}"}
 
@@ -238,6 +316,7 @@ def adam_bench(args) -> int:
                 times.append(time.perf_counter() - c0)
         med = sorted(times)[len(times) // 2]
         result["cpu_baseline"] = {"value": n / med, "unit": "parameters/s", "cores": 1, "kind": "port",
+                                  "cpu": cpu_model(),
                                   "sample": f"{n} bf16 parameters, C oracle of the same update (one thread), "
                                             f"median of 3 after 1 warm-up"}
     print(json.dumps(result), flush=True)
@@ -295,19 +374,27 @@ def main() -> int:
     meta = pkg.layer.LayerMeta(num_experts=E, top_k=k, ffn=f, act="swiglu", score=w["score"],
                                num_shared=w["S"], shared_ffn=f if w["S"] else 0, e0=w["e0"], e1=w["e1"],
                                n_src=w["n_src"])
+    received = args.workload in RECEIVED
+    if received:
+        w["recv"], w["recv_counts"], w["recv_dy"] = build_received(pkg, w, dev)
+        step = lambda: recv_step(pkg, w)  # noqa: E731
+        P = w["recv"].shape[0]
+    else:
+        step = lambda: gpu_step(pkg, w, meta)  # noqa: E731
     counts = None
     for _ in range(args.warmup):
-        counts = gpu_step(pkg, w, meta)
+        counts = step()
     torch.cuda.synchronize()
-    # Routed pairs on this GPU (the routing is the same every step: same tokens and router).
-    P = int(counts[w["e0"]:w["e1"]].sum().item()) if counts is not None else T * k
+    if not received:
+        # Routed pairs on this GPU (the routing is the same every step: same tokens and router).
+        P = int(counts[w["e0"]:w["e1"]].sum().item()) if counts is not None else T * k
 
     timer = EventTimer()
     kernels.set_timer(timer)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        gpu_step(pkg, w, meta)
+        step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     kernels.set_timer(None)
@@ -320,12 +407,15 @@ def main() -> int:
     gemm_ms = sum(per.get(n, (0.0, 0))[0] for n in GEMM_CALLS)
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
     s = 2  # bf16 bytes
-    row_bytes = {  # algorithmic HBM bytes per step of the row kernels (token-major permute)
-        "rhp_permute": T * h * s + P * h * s + 4 * P,
-        "rhp_combine": P * h * s + 2 * T * h * s + 8 * P + S * T * h * s,
-        "rhp_combine_bwd": T * h * s + 2 * P * h * s + 8 * P,
-        "rhp_token_bwd": 2 * T * h * s + P * h * s + 12 * P + S * T * h * s,
-    }
+    if received:   # four row gathers per step: rows in, outputs back, output gradients in, input gradients back
+        row_bytes = {"rhp_gather_rows": 4 * (2 * P * h * s + 4 * P)}
+    else:          # algorithmic HBM bytes per step of the row kernels (token-major permute)
+        row_bytes = {
+            "rhp_permute": T * h * s + P * h * s + 4 * P,
+            "rhp_combine": P * h * s + 2 * T * h * s + 8 * P + S * T * h * s,
+            "rhp_combine_bwd": T * h * s + 2 * P * h * s + 8 * P,
+            "rhp_token_bwd": 2 * T * h * s + P * h * s + 12 * P + S * T * h * s,
+        }
     row_ms = sum(per.get(n, (0.0, 0))[0] for n in row_bytes)
     row_gbps = sum(row_bytes.values()) / (row_ms * 1e-3) / 1e9 if row_ms else None
     ms_step = elapsed * 1e3 / args.steps
@@ -343,22 +433,31 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "fp8 (e4m3 fwd, e5m2 grads) with bf16 outputs" if fp8 else "bf16",
         "data": "synthetic (N(0,1) tokens, random N(0,0.02) weights of the layer shape, drawn on device)",
-        "config": {"workload": f"{args.workload} MoE layer: tokens={T}, hidden={h}, ffn={f} SwiGLU, experts={E}, "
-                               f"local experts [{w['e0']}, {w['e1']}), top_k={k} {w['score']} router (fp32), "
-                               f"shared experts={S}, {'fp8 experts' if fp8 else 'bf16'}, fwd+bwd",
+        "config": {"workload": (f"{args.workload}: the local experts [{w['e0']}, {w['e1']}) of a {E}-expert top-{k} "
+                                f"layer (hidden={h}, ffn={f} SwiGLU, bf16) on the {P} rows received from "
+                                f"{w['n_src']} sources of {T // w['n_src']} tokens ({T} source tokens, {w['score']} "
+                                f"router with a Zipf(1.1) selection prior): regroup, expert FFN, return, fwd+bwd")
+                   if received else
+                   (f"{args.workload} MoE layer: tokens={T}, hidden={h}, ffn={f} SwiGLU, experts={E}, "
+                    f"local experts [{w['e0']}, {w['e1']}), top_k={k} {w['score']} router (fp32), "
+                    f"shared experts={S}, {'fp8 experts' if fp8 else 'bf16'}, fwd+bwd"),
                    "tokens": T, "hidden": h, "ffn": f, "experts": E, "top_k": k, "local_experts": w["e1"] - w["e0"],
                    "routed_pairs": P, "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": gemm_tflops, "peak": peak, "unit": "TFLOP/s",
                      "frac": gemm_tflops / peak, "traffic": gemm_traffic(args.workload),
+                     "traffic_source": f"profiled constant: rocprofv3 FETCH_SIZE + WRITE_SIZE of the same launches, "
+                                       f"copy-calibrated, from profiles/gemm_traffic_{args.workload}.json (not "
+                                       f"measured in this run)" if gemm_traffic(args.workload) else None,
                      "kernel": "grouped expert GEMMs (fc1/fc2 fwd, dgrad, wgrad)",
                      "algorithmic": f"18*(P + S*T)*h*f = {gemm_flops:.4g} FLOP per step, P = {P} routed pairs"},
         "rows_roofline": {"bound": "hbm", "achieved": row_gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                           "frac": (row_gbps / PEAK_HBM_GBPS) if row_gbps else None,
-                          "kernel": "permute + combine + combine_bwd + token_bwd"},
+                          "kernel": "four row gathers (received rows in, outputs back, gradients in and back)"
+                          if received else "permute + combine + combine_bwd + token_bwd"},
         "breakdown_ms": {n: round(v[0], 4) for n, v in sorted(per.items())},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.workload, args.cpu_sample)
+        result["cpu_baseline"] = cpu_baseline(args.workload, args.cpu_sample, received_rows=P if received else None)
     print(json.dumps(result), flush=True)
     return 0
 

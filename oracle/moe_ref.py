@@ -394,3 +394,80 @@ def quantize(x: torch.Tensor, scale: float, fmt: str) -> torch.Tensor:
     m = FP8_MAX[fmt]
     y = (x.to(torch.float32) * torch.tensor(scale, dtype=torch.float32)).clamp(-m, m)
     return y.to(FP8_DTYPE[fmt]).to(torch.float64)
+
+
+def fp8_layer_emulation(x, router, fc1s, fc2s, topi, dout, scales, quantize_on: bool = True,
+                        round_bf16: bool = True, amax: dict | None = None, act: str = "swiglu") -> dict[str, torch.Tensor]:
+    """Float64 emulation of the layer with fp8 SwiGLU or GELU experts (softmax top-k gates, no shared experts):
+    forward and backward, every quantised tensor cast with its delayed scale, every bf16 intermediate
+    the GPU stores rounded to bf16.  An extension of resihp/runtime/moe.py:90-101 (the reference has no
+    fp8 math; its amax state is reference_model.py:204-216).
+
+    ``scales``: the scale (fp8_max / max(history)) of "x", "act" (e4m3), "dy", "dh" (e5m2) and the lists
+    "w1", "w2" (e4m3) per expert.  With ``quantize_on=False, round_bf16=False`` every cast and rounding is
+    the identity and the result is the float64 layer itself (the structure check of the tests).
+    ``amax``, if given, receives the largest magnitude of every tensor before its cast (what one
+    iteration records into the histories).  Returns out, dx, router (weight gradient), fc1 and fc2
+    (lists of weight gradients).
+    """
+    f64 = torch.float64
+
+    def q(v, s, fmt, name=None):
+        if amax is not None and name is not None and v.numel():
+            amax[name] = max(amax.get(name, 0.0), float(v.abs().max()))
+        if not quantize_on:
+            return v
+        return quantize(v, s, fmt) / torch.tensor(s, dtype=torch.float32).to(f64)
+
+    def bf(v):
+        return v.to(torch.bfloat16).to(f64) if round_bf16 else v
+
+    x, router, dout = x.to(f64), router.to(f64), dout.to(f64)
+    T, h = x.shape
+    E, k = router.shape[0], topi.shape[1]
+    logits = x @ router.t()
+    sel = logits.gather(-1, topi)
+    gates = torch.softmax(sel, dim=-1)
+    out = x.clone()
+    dx = dout.clone()
+    dgates = torch.zeros(T, k, dtype=f64)
+    dw1, dw2 = [], []
+    ys = {}
+    for e in range(E):
+        rows, slots = (topi == e).nonzero(as_tuple=True)
+        w1, w2 = fc1s[e].to(f64), fc2s[e].to(f64)
+        f = w2.shape[1]
+        w1q, w2q = q(w1, scales["w1"][e], "e4m3", ("w1", e)), q(w2, scales["w2"][e], "e4m3", ("w2", e))
+        if rows.numel() == 0:
+            dw1.append(torch.zeros_like(w1))
+            dw2.append(torch.zeros_like(w2))
+            continue
+        xq = q(x[rows], scales["x"], "e4m3", "x")
+        hp = xq @ w1q.t()
+        a = bf(F.silu(hp[:, :f]) * hp[:, f:] if act == "swiglu" else F.gelu(hp))
+        aq = q(a, scales["act"], "e4m3", "act")
+        y = bf(aq @ w2q.t())
+        g = gates[rows, slots].unsqueeze(1)
+        out.index_add_(0, rows, g * y)
+        dgates[rows, slots] = (dout[rows] * y).sum(1)
+        dy = bf(g * dout[rows])
+        dyq = q(dy, scales["dy"], "e5m2", "dy")
+        hpb = bf(hp)
+        dact = dyq @ w2q
+        if act == "swiglu":
+            gg, uu = hpb[:, :f], hpb[:, f:]
+            sg = torch.sigmoid(gg)
+            dh = bf(torch.cat([dact * uu * sg * (1 + gg * (1 - sg)), dact * gg * sg], 1))
+        else:
+            phi = torch.exp(-0.5 * hpb * hpb) / math.sqrt(2 * math.pi)
+            dh = bf(dact * (0.5 * (1 + torch.erf(hpb / math.sqrt(2))) + hpb * phi))
+        dhq = q(dh, scales["dh"], "e5m2", "dh")
+        dw2.append(dyq.t() @ aq)
+        dw1.append(dhq.t() @ xq)
+        dx.index_add_(0, rows, bf(dhq @ w1q))
+        ys[e] = y
+    # softmax over the k selected logits: d sel = g * (dg - sum_j g dg)
+    dsel = gates * (dgates - (gates * dgates).sum(1, keepdim=True))
+    dlogits = torch.zeros(T, E, dtype=f64).scatter_add_(1, topi, dsel)
+    dx += dlogits @ router
+    return {"out": out, "dx": dx, "router": dlogits.t() @ x, "fc1": dw1, "fc2": dw2}

@@ -270,17 +270,19 @@ class RecvPlan:
     rows: int
 
 
-def recv_plan(recv_counts: torch.Tensor) -> RecvPlan:
+def recv_plan(recv_counts: torch.Tensor, rows: int | None = None) -> RecvPlan:
     """Plan of a received buffer from its per-(source, local expert) counts ``[n_src, L]``.
 
-    The row count is the counts' sum, read on the host (as the reference reads its split sizes,
-    resihp/runtime/moe.py:210-211), so the two row maps are exact inverses of each other.
+    ``rows`` is the counts' sum.  Without it the counts are read on the host (as the reference reads
+    its split sizes, resihp/runtime/moe.py:210-211) and checked; a caller that already holds the sum
+    passes it and saves the synchronisation.  With the true sum the two row maps are exact inverses.
     """
     dev = _need_cuda(recv_counts)
     _expect(recv_counts.dtype == torch.int32 and recv_counts.dim() == 2, "recv_counts must be int32 [n_src, L]")
-    _expect(bool((recv_counts >= 0).all()), "recv_counts must be non-negative")
     n_src, L = recv_counts.shape
-    rows = int(recv_counts.sum().item())
+    if rows is None:
+        _expect(bool((recv_counts >= 0).all()), "recv_counts must be non-negative")
+        rows = int(recv_counts.sum().item())
     offsets = torch.empty(L + 1, dtype=torch.int32, device=dev)
     sort_row = torch.empty(max(1, rows), dtype=torch.int32, device=dev)
     unsort_row = torch.empty(max(1, rows), dtype=torch.int32, device=dev)

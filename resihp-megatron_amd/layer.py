@@ -216,10 +216,10 @@ class _ExpertChunksFn(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, act, f, recv_counts, recv, *weights):
+    def forward(ctx, act, f, rows, recv_counts, recv, *weights):
         G = len(weights) // 2
         fc1s, fc2s = list(weights[:G]), list(weights[G:])
-        plan = K.recv_plan(recv_counts)
+        plan = K.recv_plan(recv_counts, rows)
         P, h = plan.rows, recv.shape[1]
         if recv.shape[0] != P:
             raise K.KernelArgumentError(f"the received buffer has {recv.shape[0]} rows, the counts {P}")
@@ -248,7 +248,7 @@ class _ExpertChunksFn(torch.autograd.Function):
             dy = K.gather_rows(dy_recv.contiguous(), sort_row)
             dhpre = torch.empty_like(hpre)
             K.expert_fc2_bwd([dy] * G, [a] * G, [hpre] * G, offsets, True, P, list(fc2s), act, [dhpre] * G, dw2)
-            need_x = ctx.needs_input_grad[3]
+            need_x = ctx.needs_input_grad[4]
             dxp = torch.empty_like(xs) if need_x else None
             K.expert_fc1_bwd([dhpre] * G, [xs] * G, offsets, True, P, list(fc1s), f, act,
                              [dxp] * G if need_x else None, dw1)
@@ -258,22 +258,23 @@ class _ExpertChunksFn(torch.autograd.Function):
             for w in (*dw1, *dw2):
                 w.zero_()
             drecv = torch.zeros_like(xs)
-        return (None, None, None, drecv, *dw1, *dw2)
+        return (None, None, None, None, drecv, *dw1, *dw2)
 
 
 def expert_chunks(recv: torch.Tensor, recv_counts: torch.Tensor, fc1s: list[torch.Tensor],
-                  fc2s: list[torch.Tensor], act: str = "swiglu") -> torch.Tensor:
+                  fc2s: list[torch.Tensor], act: str = "swiglu", rows: int | None = None) -> torch.Tensor:
     """Expert outputs of a received buffer, in the received order (with autograd).
 
     ``recv`` holds the rows the all-to-all delivered, source-major: chunk (s, i) of
     ``recv_counts[s, i]`` rows for local expert i (``fc1s[i]``, ``fc2s[i]``), rows in the sender's
     (token, slot) order, as resihp/runtime/moe.py:199-212 builds and exchanges them.
-    ``recv_counts`` is an int32 ``[n_src, L]`` device tensor.
+    ``recv_counts`` is an int32 ``[n_src, L]`` device tensor; ``rows``, its sum, may be given to spare
+    reading the counts on the host.
     """
     if len(fc1s) != len(fc2s) or recv_counts.dim() != 2 or recv_counts.shape[1] != len(fc1s):
         raise ValueError("need one fc1 and one fc2 weight per column of recv_counts")
     f = fc2s[0].shape[1]
-    return _ExpertChunksFn.apply(act, f, recv_counts.contiguous(), recv.contiguous(), *fc1s, *fc2s)
+    return _ExpertChunksFn.apply(act, f, rows, recv_counts.contiguous(), recv.contiguous(), *fc1s, *fc2s)
 
 
 def moe_layer(meta: LayerMeta, x: torch.Tensor, router_w: torch.Tensor, bias: torch.Tensor | None,

@@ -186,3 +186,35 @@ def test_quantize_saturates_and_rounds_to_nearest_even():
     q = M.quantize(x, 1.0, "e4m3")
     # e4m3 spacing in [1, 2) is 1/8: 1.0625 ties to 1.0 (even), 1.1875 ties to 1.25.
     assert q.tolist() == [448.0, -448.0, 1.0, 1.25, 0.0]
+
+
+def test_shared_expert_term_known_answer():
+    """One token, top-1 (gate 1), GELU experts with h = f = 1: out = x + 2 gelu(1) (routed) + 3 gelu(1)
+    (shared, gate 1, added after the routed sum).  gelu(1) = 0.8413447460685429."""
+    cfg = M.OracleConfig(hidden=1, ffn=1, num_experts=2, top_k=1, tokens=1, act="gelu", num_shared=1, shared_ffn=1)
+    one = lambda v: torch.tensor([[v]], dtype=torch.float64)  # noqa: E731
+    params = {"router.weight": torch.tensor([[0.0], [1.0]], dtype=torch.float64),
+              "experts.0.fc1.weight": one(7.0), "experts.0.fc2.weight": one(7.0),
+              "experts.1.fc1.weight": one(1.0), "experts.1.fc2.weight": one(2.0),
+              "shared_experts.0.fc1.weight": one(1.0), "shared_experts.0.fc2.weight": one(3.0)}
+    out = M.layer_forward(cfg, params, one(1.0))
+    assert out.item() == pytest.approx(1.0 + 5.0 * 0.8413447460685429, rel=1e-15)
+    # the shared expert's weight follows its own key: scaling it moves only its term
+    params["shared_experts.0.fc2.weight"] = one(30.0)
+    assert M.layer_forward(cfg, params, one(1.0)).item() == pytest.approx(1.0 + 32.0 * 0.8413447460685429, rel=1e-15)
+
+
+def test_sigmoid_gates_unnormalised_and_scaled_known_answer():
+    """logits [0, ln 3] score sigmoid [1/2, 3/4]: top-1 unnormalised gate 3/4; times gate_scale 2.5 = 15/8;
+    top-2 normalised [3/4, 1/2] / (5/4) = [3/5, 2/5], times 2.5 = [3/2, 1], slots in descending score."""
+    x = torch.ones(1, 1, dtype=torch.float64)
+    w = torch.tensor([[0.0], [math.log(3.0)]], dtype=torch.float64)
+    c1 = M.OracleConfig(hidden=1, num_experts=2, top_k=1, score="sigmoid", normalize=False)
+    topi, g = M.route(c1, x, w)
+    assert topi.tolist() == [[1]] and g.item() == pytest.approx(0.75, rel=1e-15)
+    c2 = M.OracleConfig(hidden=1, num_experts=2, top_k=1, score="sigmoid", normalize=False, gate_scale=2.5)
+    assert M.route(c2, x, w)[1].item() == pytest.approx(1.875, rel=1e-15)
+    c3 = M.OracleConfig(hidden=1, num_experts=2, top_k=2, score="sigmoid", normalize=True, gate_scale=2.5)
+    topi, g = M.route(c3, x, w)
+    assert topi.tolist() == [[1, 0]]
+    assert g[0].tolist() == pytest.approx([1.5, 1.0], rel=1e-15)
