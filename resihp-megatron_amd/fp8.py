@@ -63,6 +63,41 @@ class Fp8State:
             h[i] = (a * (1 + spread * u)).float()
         self.history.copy_(h)
 
+    # Layer-wide tensors of the state, by key (the expert weights' rows go by expert id).
+    LAYER_KEYS = (("fp8.expert_input", X), ("fp8.activation", ACT), ("fp8.grad_output", DY),
+                  ("fp8.grad_preactivation", DH))
+
+    def state_tensors(self, experts: list[int]) -> dict[str, torch.Tensor]:
+        """The state by key, for live re-placement: histories and pending amaxes of the layer-wide tensors,
+        and of every local expert's two weights under ``experts.{e}.fc1`` / ``experts.{e}.fc2`` (``experts``
+        lists the expert id of each local slot).  The reference migrates its amax buffer with its layer
+        and restores it on rollback (resihp/runtime/reference_model.py:44-46; transaction.py:41-43, 59-65);
+        the values returned are views of this state."""
+        if len(experts) != self.G:
+            raise ValueError(f"need the expert id of each of the {self.G} local slots")
+        rows = [(k, i) for k, i in self.LAYER_KEYS]
+        for g, e in enumerate(experts):
+            rows += [(f"experts.{e}.fc1", self.w1(g)), (f"experts.{e}.fc2", self.w2(g))]
+        out = {}
+        for key, i in rows:
+            out[f"{key}.amax_history"] = self.history[i]
+            out[f"{key}.amax"] = self.amax[i:i + 1]
+        return out
+
+    def load_state_tensors(self, tensors: dict[str, torch.Tensor], experts: list[int]) -> None:
+        """Copies a keyed state (``state_tensors`` of any holder) into this one, whose local slots hold
+        ``experts``; a missing key or a wrong shape raises and leaves this state unchanged."""
+        mine = self.state_tensors(experts)
+        missing = [k for k in mine if k not in tensors]
+        if missing:
+            raise KeyError(f"fp8 state misses {missing[0]}")
+        for k, dst in mine.items():
+            if tuple(tensors[k].shape) != tuple(dst.shape):
+                raise ValueError(f"{k} has shape {tuple(tensors[k].shape)}, expected {tuple(dst.shape)}")
+        with torch.no_grad():
+            for k, dst in mine.items():
+                dst.copy_(tensors[k].to(dst.device, dst.dtype))
+
     def finish_iteration(self) -> None:
         """Prepend every pending amax to its history and reset it (reference_model.py:212-216)."""
         K.fp8_amax_roll(self.history, self.amax)
