@@ -275,6 +275,9 @@ int rhp_expert_fc2_fwd(int G, const int32_t* offsets, int rows_from_offsets, int
  * Backward through fc2 and the activation:
  *   dact = dy @ w2;  dhpre = activation backward of dact at hpre  ([M_g, F1])
  *   dw2[g] = dy_g^T @ act_g  ([h, f])      (written, not accumulated)
+ * dhpre may be NULL to skip the input-gradient product (then hpre and w2 are
+ * not read), or dw2 NULL to skip the weight gradient, not both.  The two
+ * products are independent, so a caller may run them on two streams.
  */
 int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,
                        int h, int f, const void* const* dy, const void* const* act_in, const void* const* hpre,
@@ -284,7 +287,8 @@ int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_offsets, int
 /*
  * Backward through fc1:
  *   dxp = dhpre @ w1  ([M_g, h]);   dw1[g] = dhpre_g^T @ xp_g  ([F1, h])   (written, not accumulated)
- * dxp may be NULL to skip the input gradient.
+ * dxp may be NULL to skip the input gradient, or dw1 NULL to skip the weight
+ * gradient, not both; the two products may run on two streams.
  */
 int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,
                        int h, int f, const void* const* dhpre, const void* const* xp, const void* const* w1,

@@ -703,43 +703,50 @@ extern "C" int rhp_expert_fc2_bwd(int G, const int32_t* offsets, int rows_from_o
     clear_error();
     if (int rc = check_common("rhp_expert_fc2_bwd", G, offsets, rows_cap, dtype, act, h, f)) return rc;
     if (int rc = check_split_ws("rhp_expert_fc2_bwd", split_ws, split_ws_bytes)) return rc;
-    RHP_REQUIRE(all_set(dy, G) && all_set(act_in, G) && all_set(hpre, G) && all_set(w2, G) &&
-                    all_set((const void* const*)dhpre, G) && all_set((const void* const*)dw2, G),
+    RHP_REQUIRE(dhpre || dw2, "rhp_expert_fc2_bwd: nothing to compute (dhpre and dw2 both null)");
+    RHP_REQUIRE(all_set(dy, G) && (!dhpre || (all_set(hpre, G) && all_set(w2, G) &&
+                                               all_set((const void* const*)dhpre, G))) &&
+                    (!dw2 || (all_set(act_in, G) && all_set((const void* const*)dw2, G))),
                 "rhp_expert_fc2_bwd: null pointer");
     const bool swiglu = act == RHP_ACT_SWIGLU;
     const int F1 = swiglu ? 2 * f : f;
-    const bool aligned = all_aligned(dy, G) && all_aligned(act_in, G) && all_aligned(hpre, G) &&
-                         all_aligned(w2, G) && all_aligned((const void* const*)dhpre, G) &&
-                         all_aligned((const void* const*)dw2, G);
-    // dact = dy @ w2, then the activation backward at hpre.
-    Job d{};
-    d.mode = kDgrad;
-    d.epi = swiglu ? kEpiSwigluBwd : kEpiGeluBwd;
-    d.dtype = dtype;
-    if (int rc = choose_kernel("rhp_expert_fc2_bwd", dtype, h, f, act, aligned, &d.mfma)) return rc;
-    d.G = G;
-    d.offsets = offsets;
-    d.rows_from_offsets = rows_from_offsets;
-    d.rows_cap = rows_cap;
-    d.N = f;
-    d.K = h;
-    d.lda = h;
-    d.ldb = f;
-    d.ldc = F1;
-    d.ldaux = F1;
-    d.f = f;
-    d.a = dy;
-    d.b = w2;
-    d.c = dhpre;
-    d.aux = hpre;
-    d.split_ws = split_ws;
-    if (int rc = run(d, "expert_fc2_dgrad", stream)) return rc;
+    const bool aligned = all_aligned(dy, G) && (!dhpre || (all_aligned(hpre, G) && all_aligned(w2, G) &&
+                                                           all_aligned((const void* const*)dhpre, G))) &&
+                         (!dw2 || (all_aligned(act_in, G) && all_aligned((const void* const*)dw2, G)));
+    bool mfma = false;
+    if (int rc = choose_kernel("rhp_expert_fc2_bwd", dtype, h, f, act, aligned, &mfma)) return rc;
+    if (dhpre) {
+        // dact = dy @ w2, then the activation backward at hpre.
+        Job d{};
+        d.mode = kDgrad;
+        d.epi = swiglu ? kEpiSwigluBwd : kEpiGeluBwd;
+        d.dtype = dtype;
+        d.mfma = mfma;
+        d.G = G;
+        d.offsets = offsets;
+        d.rows_from_offsets = rows_from_offsets;
+        d.rows_cap = rows_cap;
+        d.N = f;
+        d.K = h;
+        d.lda = h;
+        d.ldb = f;
+        d.ldc = F1;
+        d.ldaux = F1;
+        d.f = f;
+        d.a = dy;
+        d.b = w2;
+        d.c = dhpre;
+        d.aux = hpre;
+        d.split_ws = split_ws;
+        if (int rc = run(d, "expert_fc2_dgrad", stream)) return rc;
+    }
+    if (!dw2) return 0;
     // dw2[g] = dy_g^T @ act_g
     Job w{};
     w.mode = kWgrad;
     w.epi = kEpiStore;
     w.dtype = dtype;
-    w.mfma = d.mfma;
+    w.mfma = mfma;
     w.G = G;
     w.offsets = offsets;
     w.rows_from_offsets = rows_from_offsets;
@@ -763,10 +770,12 @@ extern "C" int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_o
     clear_error();
     if (int rc = check_common("rhp_expert_fc1_bwd", G, offsets, rows_cap, dtype, act, h, f)) return rc;
     if (int rc = check_split_ws("rhp_expert_fc1_bwd", split_ws, split_ws_bytes)) return rc;
-    RHP_REQUIRE(all_set(dhpre, G) && all_set(xp, G) && all_set(w1, G) && all_set((const void* const*)dw1, G),
+    RHP_REQUIRE(dxp || dw1, "rhp_expert_fc1_bwd: nothing to compute (dxp and dw1 both null)");
+    RHP_REQUIRE(all_set(dhpre, G) && (!dxp || all_set(w1, G)) && (!dw1 || (all_set(xp, G) &&
+                                                                         all_set((const void* const*)dw1, G))),
                 "rhp_expert_fc1_bwd: null pointer");
     const int F1 = act == RHP_ACT_SWIGLU ? 2 * f : f;
-    const bool aligned = all_aligned(dhpre, G) && all_aligned(xp, G) && all_aligned(w1, G) &&
+    const bool aligned = all_aligned(dhpre, G) && (!dxp || all_aligned(w1, G)) && all_aligned(xp, G) &&
                          all_aligned((const void* const*)dw1, G) && all_aligned((const void* const*)dxp, G);
     bool mfma = false;
     if (int rc = choose_kernel("rhp_expert_fc1_bwd", dtype, h, f, act, aligned, &mfma)) return rc;
@@ -794,6 +803,7 @@ extern "C" int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_o
         d.split_ws = split_ws;
         if (int rc = run(d, "expert_fc1_dgrad", stream)) return rc;
     }
+    if (!dw1) return 0;
     // dw1[g] = dhpre_g^T @ xp_g
     Job w{};
     w.mode = kWgrad;

@@ -68,6 +68,11 @@ def _need_cuda(*ts: torch.Tensor | None) -> torch.device:
     return dev
 
 
+def need_device(*ts: torch.Tensor | None) -> torch.device:
+    """The HIP device all of ``ts`` are on; raises RuntimeError for host tensors or mixed devices."""
+    return _need_cuda(*ts)
+
+
 class KernelArgumentError(RuntimeError):
     """Arguments the kernels cannot take.  A RuntimeError, like every failure of the layer, so the
     resilient trainer (resihp/train/resilient_loop.py:28) treats it as it treats the reference's."""
@@ -420,40 +425,49 @@ def expert_fc2_fwd(acts: list[torch.Tensor], offsets: torch.Tensor, rows_from_of
 
 def expert_fc2_bwd(dys: list[torch.Tensor], acts: list[torch.Tensor], hpres: list[torch.Tensor],
                    offsets: torch.Tensor, rows_from_offsets: bool, rows_cap: int, w2: list[torch.Tensor], act: str,
-                   dhpre: list[torch.Tensor], dw2: list[torch.Tensor], split: bool = True) -> None:
-    dev = _need_cuda(offsets, *dys, *acts, *hpres, *w2, *dhpre, *dw2)
+                   dhpre: list[torch.Tensor] | None, dw2: list[torch.Tensor] | None, split: bool = True) -> None:
+    """Input-gradient product into ``dhpre`` and weight gradient into ``dw2``; either may be None (not
+    both), so the two independent products can run on two streams.  ``w2`` gives the shapes either way."""
+    _expect(dhpre is not None or dw2 is not None, "expert_fc2_bwd: nothing to compute")
+    dev = _need_cuda(offsets, *dys, *acts, *hpres, *w2, *(dhpre or []), *(dw2 or []))
     G, dt, (h, f) = len(w2), w2[0].dtype, tuple(w2[0].shape)
     F1 = 2 * f if act == "swiglu" else f
     rows = _shared_rows(rows_from_offsets, rows_cap)
     _check_offsets(offsets, G)
     _check_groups("w2", w2, G, dt, f, exact_shape=(h, f))
-    _check_groups("dw2", dw2, G, dt, f, exact_shape=(h, f))
     _check_groups("dy", dys, G, dt, h, rows)
-    _check_groups("act", acts, G, dt, f, rows)
-    _check_groups("hpre", hpres, G, dt, F1, rows)
-    _check_groups("dhpre", dhpre, G, dt, F1, rows)
+    if dw2 is not None:
+        _check_groups("dw2", dw2, G, dt, f, exact_shape=(h, f))
+        _check_groups("act", acts, G, dt, f, rows)
+    if dhpre is not None:
+        _check_groups("hpre", hpres, G, dt, F1, rows)
+        _check_groups("dhpre", dhpre, G, dt, F1, rows)
     _split_call("rhp_expert_fc2_bwd", dev, split, G, _ptr(offsets), int(rows_from_offsets), rows_cap,
-                dtype_code(w2[0]), act_code(act), h, f, _arr(dys), _arr(acts), _arr(hpres), _arr(w2), _arr(dhpre),
-                _arr(dw2))
+                dtype_code(w2[0]), act_code(act), h, f, _arr(dys), _arr(acts) if dw2 is not None else None,
+                _arr(hpres) if dhpre is not None else None, _arr(w2), _arr(dhpre) if dhpre is not None else None,
+                _arr(dw2) if dw2 is not None else None)
 
 
 def expert_fc1_bwd(dhpre: list[torch.Tensor], xs: list[torch.Tensor], offsets: torch.Tensor,
                    rows_from_offsets: bool, rows_cap: int, w1: list[torch.Tensor], f: int, act: str,
-                   dxs: list[torch.Tensor] | None, dw1: list[torch.Tensor], split: bool = True) -> None:
-    dev = _need_cuda(offsets, *dhpre, *xs, *w1, *(dxs or []), *dw1)
+                   dxs: list[torch.Tensor] | None, dw1: list[torch.Tensor] | None, split: bool = True) -> None:
+    """Input gradient into ``dxs`` and weight gradient into ``dw1``; either may be None (not both)."""
+    _expect(bool(dxs) or dw1 is not None, "expert_fc1_bwd: nothing to compute")
+    dev = _need_cuda(offsets, *dhpre, *xs, *w1, *(dxs or []), *(dw1 or []))
     G, dt, h = len(w1), w1[0].dtype, w1[0].shape[1]
     F1 = 2 * f if act == "swiglu" else f
     rows = _shared_rows(rows_from_offsets, rows_cap)
     _check_offsets(offsets, G)
     _check_groups("w1", w1, G, dt, h, exact_shape=(F1, h))
-    _check_groups("dw1", dw1, G, dt, h, exact_shape=(F1, h))
     _check_groups("dhpre", dhpre, G, dt, F1, rows)
-    _check_groups("x", xs, G, dt, h, rows)
+    if dw1 is not None:
+        _check_groups("dw1", dw1, G, dt, h, exact_shape=(F1, h))
+        _check_groups("x", xs, G, dt, h, rows)
     if dxs:
         _check_groups("dx", dxs, G, dt, h, rows)
     _split_call("rhp_expert_fc1_bwd", dev, split, G, _ptr(offsets), int(rows_from_offsets), rows_cap,
-                dtype_code(w1[0]), act_code(act), h, f, _arr(dhpre), _arr(xs), _arr(w1), _arr(dxs) if dxs else None,
-                _arr(dw1))
+                dtype_code(w1[0]), act_code(act), h, f, _arr(dhpre), _arr(xs) if dw1 is not None else None, _arr(w1),
+                _arr(dxs) if dxs else None, _arr(dw1) if dw1 is not None else None)
 
 
 # ----------------------------------------------------------------------------- optimizer

@@ -51,6 +51,59 @@ def _fc1_rows(act: str, f: int) -> int:
     return 2 * f if act == "swiglu" else f
 
 
+# The backward's input-gradient and weight-gradient products are independent.  Run concurrently, the
+# weight gradients go to a second stream of the device (default priority), so their tiles fill the CUs
+# the input-gradient products leave idle: every CU reaches a tile's epilogue at the same time, so the
+# epilogues' HBM traffic comes in bursts, and the last round of a launch leaves CUs empty.  That pays
+# for short reductions (measured: dsv2lite +1.4 %, the EP-128 share +2.7 %); input-gradient products
+# whose reduction is long enough for the K split of their last round (h or the fc1 rows >= 8192) fill
+# that round themselves and lose L2 locality to a concurrent launch (Mixtral shape: -4 %), so they keep
+# the GPU to themselves.  "auto" chooses by that rule; True / False force it.
+CONCURRENT_BACKWARD: bool | str = "auto"
+SPLIT_MIN_K = 8192   # the reduction length from which the input-gradient products split their last round
+
+
+def _concurrent(h: int, F1: int) -> bool:
+    if CONCURRENT_BACKWARD == "auto":
+        return max(h, F1) < SPLIT_MIN_K
+    return bool(CONCURRENT_BACKWARD)
+_side_streams: dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    st = _side_streams.get(idx)
+    if st is None:
+        st = torch.cuda.Stream(device=idx)
+        _side_streams[idx] = st
+    return st
+
+
+def expert_backward(dys, acts, hpres, offsets, rows_from_offsets: bool, rows_cap: int, fc1s, fc2s, f: int,
+                    act: str, dhpre, xs, dxs, dw1, dw2) -> None:
+    """The expert FFN backward (fc2 then fc1, input and weight gradients) of a group launch.
+
+    The weight gradients go to the side stream when the products run concurrently (CONCURRENT_BACKWARD);
+    the current stream waits for them before returning, so every output is ordered on it as usual."""
+    fc1s, fc2s = list(fc1s), list(fc2s)
+    if not _concurrent(fc1s[0].shape[1], fc1s[0].shape[0]):
+        K.expert_fc2_bwd(dys, acts, hpres, offsets, rows_from_offsets, rows_cap, fc2s, act, dhpre, dw2)
+        K.expert_fc1_bwd(dhpre, xs, offsets, rows_from_offsets, rows_cap, fc1s, f, act, dxs, dw1)
+        return
+    main = torch.cuda.current_stream(offsets.device)
+    side = _side_stream(offsets.device)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        K.expert_fc2_bwd(dys, acts, hpres, offsets, rows_from_offsets, rows_cap, fc2s, act, None, dw2)
+    K.expert_fc2_bwd(dys, acts, hpres, offsets, rows_from_offsets, rows_cap, fc2s, act, dhpre, None)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        K.expert_fc1_bwd(dhpre, xs, offsets, rows_from_offsets, rows_cap, fc1s, f, act, None, dw1)
+    if dxs:
+        K.expert_fc1_bwd(dhpre, xs, offsets, rows_from_offsets, rows_cap, fc1s, f, act, dxs, None)
+    main.wait_stream(side)
+
+
 def _fp8_forward(st: Fp8State, meta: LayerMeta, offsets, P, xp, fc1s, fc2s, hpre, y):
     """Expert FFN forward in fp8; returns what the backward needs (codes and transposed copies).
 
@@ -120,6 +173,24 @@ class _MoELayerFn(torch.autograd.Function):
         sfc1s, sfc2s = list(weights[2 * G:2 * G + S]), list(weights[2 * G + S:2 * G + 2 * S])
         T, h = x.shape
         k, f = meta.top_k, meta.ffn
+        fs = meta.shared_ffn or f
+        shared_off = shared_h = shared_a = shared_y = None
+        K.need_device(x, router_w, *weights)
+        main = torch.cuda.current_stream(x.device)
+        # Shared experts need only x: concurrently with the routing and the routed experts on a side
+        # stream where the products run concurrently, else after them.
+        shared_side = S > 0 and T > 0 and _concurrent(h, _fc1_rows(meta.act, fs))
+        if S:
+            shared_off = torch.arange(S + 1, dtype=torch.int32, device=x.device) * T
+            shared_h = [x.new_empty(T, _fc1_rows(meta.act, fs)) for _ in range(S)]
+            shared_a = [x.new_empty(T, fs) for _ in range(S)]
+            shared_y = [x.new_empty(T, h) for _ in range(S)]
+        if shared_side:
+            side = _side_stream(x.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                K.expert_fc1_fwd([x] * S, shared_off, False, T, sfc1s, fs, meta.act, shared_h, shared_a)
+                K.expert_fc2_fwd(shared_a, shared_off, False, T, sfc2s, shared_y)
         logits, topi, gates = K.route(x, router_w, bias, k, meta.score, meta.normalize, meta.gate_scale)
         plan = K.dispatch(topi, meta.num_experts, e0, e1, meta.n_src)
         # The reference materialises counts on the host here too (moe.py:210-211);
@@ -136,16 +207,11 @@ class _MoELayerFn(torch.autograd.Function):
         elif P > 0:
             K.expert_fc1_fwd([xp] * G, plan.offsets, True, P, fc1s, f, meta.act, [hpre] * G, [act] * G)
             K.expert_fc2_fwd([act] * G, plan.offsets, True, P, fc2s, [y] * G)
-        shared_off = shared_h = shared_a = shared_y = None
-        if S:
-            fs = meta.shared_ffn or f
-            shared_off = torch.arange(S + 1, dtype=torch.int32, device=x.device) * T
-            shared_h = [x.new_empty(T, _fc1_rows(meta.act, fs)) for _ in range(S)]
-            shared_a = [x.new_empty(T, fs) for _ in range(S)]
-            shared_y = [x.new_empty(T, h) for _ in range(S)]
-            if T > 0:
-                K.expert_fc1_fwd([x] * S, shared_off, False, T, sfc1s, fs, meta.act, shared_h, shared_a)
-                K.expert_fc2_fwd(shared_a, shared_off, False, T, sfc2s, shared_y)
+        if S and T > 0 and not shared_side:
+            K.expert_fc1_fwd([x] * S, shared_off, False, T, sfc1s, fs, meta.act, shared_h, shared_a)
+            K.expert_fc2_fwd(shared_a, shared_off, False, T, sfc2s, shared_y)
+        if shared_side:
+            main.wait_stream(_side_stream(x.device))
         out = K.combine(y, x, gates, topi, plan.pair_row, shared_y or [])
         ctx.meta = meta
         ctx.fp8 = (fp8, q8)
@@ -165,8 +231,25 @@ class _MoELayerFn(torch.autograd.Function):
         sfc1s, sfc2s = ws[2 * G:2 * G + S], ws[2 * G + S:]
         shared_off, shared_h, shared_a = ctx.shared
         f = meta.ffn
+        fs = meta.shared_ffn or f
         dout = dout.contiguous()
         need_x = ctx.needs_input_grad[2]
+        main = torch.cuda.current_stream(x.device)
+        sdw1 = [torch.empty_like(w) for w in sfc1s]
+        sdw2 = [torch.empty_like(w) for w in sfc2s]
+        shared_dx = []
+        shared_side = S > 0 and T > 0 and _concurrent(h, _fc1_rows(meta.act, fs))
+        if S and T > 0:
+            dh = [x.new_empty(T, _fc1_rows(meta.act, fs)) for _ in range(S)]
+            shared_dx = [x.new_empty(T, h) for _ in range(S)] if need_x else []
+        if shared_side:
+            # The shared experts' whole backward (it needs only dout) on the side stream, ahead of the
+            # routed experts' weight gradients that expert_backward queues there.
+            side = _side_stream(x.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                K.expert_fc2_bwd([dout] * S, shared_a, shared_h, shared_off, False, T, list(sfc2s), meta.act, dh, sdw2)
+                K.expert_fc1_bwd(dh, [x] * S, shared_off, False, T, list(sfc1s), fs, meta.act, shared_dx or None, sdw1)
         dy, dgates = K.combine_bwd(dout, y, gates, pair_row, P)
         dw2 = [torch.empty_like(w) for w in fc2s]
         dw1 = [torch.empty_like(w) for w in fc1s]
@@ -176,21 +259,16 @@ class _MoELayerFn(torch.autograd.Function):
             _fp8_backward(fp8, q8, meta, offsets, P, dy, hpre, dxp, dw1, dw2)
         elif P > 0:
             dhpre = x.new_empty(P, _fc1_rows(meta.act, f))
-            K.expert_fc2_bwd([dy] * G, [act] * G, [hpre] * G, offsets, True, P, fc2s, meta.act, [dhpre] * G, dw2)
-            K.expert_fc1_bwd([dhpre] * G, [xp] * G, offsets, True, P, fc1s, f, meta.act,
-                             [dxp] * G if need_x else None, dw1)
+            expert_backward([dy] * G, [act] * G, [hpre] * G, offsets, True, P, fc1s, fc2s, f, meta.act, [dhpre] * G,
+                            [xp] * G, [dxp] * G if need_x else None, dw1, dw2)
         else:
             for w in (*dw1, *dw2):
                 w.zero_()
-        sdw1 = [torch.empty_like(w) for w in sfc1s]
-        sdw2 = [torch.empty_like(w) for w in sfc2s]
-        shared_dx = []
-        if S and T > 0:
-            fs = meta.shared_ffn or f
-            dh = [x.new_empty(T, _fc1_rows(meta.act, fs)) for _ in range(S)]
-            K.expert_fc2_bwd([dout] * S, shared_a, shared_h, shared_off, False, T, list(sfc2s), meta.act, dh, sdw2)
-            shared_dx = [x.new_empty(T, h) for _ in range(S)] if need_x else []
-            K.expert_fc1_bwd(dh, [x] * S, shared_off, False, T, list(sfc1s), fs, meta.act, shared_dx or None, sdw1)
+        if S and T > 0 and not shared_side:
+            expert_backward([dout] * S, shared_a, shared_h, shared_off, False, T, sfc1s, sfc2s, fs, meta.act, dh,
+                            [x] * S, shared_dx or None, sdw1, sdw2)
+        if shared_side:
+            main.wait_stream(_side_stream(x.device))
         dl = K.route_bwd(dgates, gates, logits, topi, meta.score, meta.normalize, meta.gate_scale)
         dx = K.token_bwd(dout, dxp, pair_row, dl, topi, router_w, shared_dx) if need_x else None
         dwr = None
@@ -247,11 +325,10 @@ class _ExpertChunksFn(torch.autograd.Function):
         if P > 0:
             dy = K.gather_rows(dy_recv.contiguous(), sort_row)
             dhpre = torch.empty_like(hpre)
-            K.expert_fc2_bwd([dy] * G, [a] * G, [hpre] * G, offsets, True, P, list(fc2s), act, [dhpre] * G, dw2)
             need_x = ctx.needs_input_grad[4]
             dxp = torch.empty_like(xs) if need_x else None
-            K.expert_fc1_bwd([dhpre] * G, [xs] * G, offsets, True, P, list(fc1s), f, act,
-                             [dxp] * G if need_x else None, dw1)
+            expert_backward([dy] * G, [a] * G, [hpre] * G, offsets, True, P, fc1s, fc2s, f, act, [dhpre] * G,
+                            [xs] * G, [dxp] * G if need_x else None, dw1, dw2)
             if need_x:
                 drecv = K.gather_rows(dxp, unsort_row)
         else:
