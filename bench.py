@@ -53,7 +53,8 @@ WORKLOADS = {
 RECEIVED = {"ep128-share"}
 
 GEMM_CALLS = ("rhp_expert_fc1_fwd", "rhp_expert_fc2_fwd", "rhp_expert_fc2_bwd", "rhp_expert_fc1_bwd", "rhp_fp8_gemm",
-              "rhp_fp8_gemm_cast")
+              "rhp_fp8_gemm_cast", "rhp_expert_fc1_fwd_gather", "rhp_expert_fc2_fwd_scatter",
+              "rhp_expert_fc2_dgrad_gather", "rhp_expert_fc1_dgrad_scatter")
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 
 
@@ -424,8 +425,9 @@ def main() -> int:
     gemm_ms = timer.union_ms(GEMM_CALLS) / args.steps
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
     s = 2  # bf16 bytes
-    if received:   # four row gathers per step: rows in, outputs back, output gradients in, input gradients back
-        row_bytes = {"rhp_gather_rows": 4 * (2 * P * h * s + 4 * P)}
+    if received:   # the products read and write received rows through the plan's row map; two row gathers a
+        # step make the expert-major copies the weight gradients read (inputs, output gradients)
+        row_bytes = {"rhp_gather_rows": 2 * (2 * P * h * s + 4 * P)}
     else:          # algorithmic HBM bytes per step of the row kernels (token-major permute)
         row_bytes = {
             "rhp_permute": T * h * s + P * h * s + 4 * P,
@@ -469,7 +471,7 @@ def main() -> int:
                      "algorithmic": f"18*(P + S*T)*h*f = {gemm_flops:.4g} FLOP per step, P = {P} routed pairs"},
         "rows_roofline": {"bound": "hbm", "achieved": row_gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                           "frac": (row_gbps / PEAK_HBM_GBPS) if row_gbps else None,
-                          "kernel": "four row gathers (received rows in, outputs back, gradients in and back)"
+                          "kernel": "two row gathers (expert-major inputs and output gradients, side stream)"
                           if received else "permute + combine + combine_bwd + token_bwd"},
         "breakdown_ms": {n: round(v[0], 4) for n, v in sorted(per.items())},
     }

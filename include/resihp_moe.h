@@ -295,6 +295,40 @@ int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_offsets, int
                        void* const* dxp, void* const* dw1, void* split_ws, size_t split_ws_bytes,
                        hipStream_t stream);
 
+/*
+ * The same products on received rows (moe.py:213-226): the expert FFN of the
+ * rows a GPU received from its sources, which arrive source-major, (src, e)
+ * chunks (moe.py:211-212), and return in the same order (moe.py:224).  With
+ * the rhp_recv_plan maps, expert-major row r (the grouped order of offsets)
+ * is received row sort_row[r]; the products below read or write received rows
+ * directly through such a map, so no regrouped copy is made:
+ *   fc1_fwd_gather:    row r of the grouped product reads src[src_idx[r]]
+ *   fc2_fwd_scatter:   y[y_idx[r]] = act[r] @ w2^T (rows of y no index names are not written)
+ *   fc2_dgrad_gather:  the input-gradient product of rhp_expert_fc2_bwd on dy[dy_idx[r]]
+ *   fc1_dgrad_scatter: dx[dx_idx[r]] = dhpre[r] @ w1
+ * Index arrays hold rows_cap int32 entries (rows_cap >= offsets[G]); an index
+ * outside [0, src_rows) reads a zero row, one outside [0, y_rows) drops the
+ * row.  Grouped-order operands (hpre, act, dhpre) are single buffers of
+ * rows_cap rows.  The results equal those of rhp_gather_rows followed by the
+ * plain product, bit for bit.  On the MFMA kernel a mapped buffer must be
+ * 16-byte aligned and hold fewer than 2^31 / (2 ld) - 1 rows (ld = h), which
+ * is an error otherwise.  No reference counterpart as entry points: they fuse
+ * the regrouping gathers of moe.py:213-226 into the products.
+ */
+int rhp_expert_fc1_fwd_gather(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int act, int h, int f,
+                              const void* src, int64_t src_rows, const int32_t* src_idx, const void* const* w1,
+                              void* hpre, void* act_out, void* split_ws, size_t split_ws_bytes, hipStream_t stream);
+int rhp_expert_fc2_fwd_scatter(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int h, int f,
+                               const void* act_in, const void* const* w2, void* y, int64_t y_rows,
+                               const int32_t* y_idx, void* split_ws, size_t split_ws_bytes, hipStream_t stream);
+int rhp_expert_fc2_dgrad_gather(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int act, int h, int f,
+                                const void* dy, int64_t dy_rows, const int32_t* dy_idx, const void* hpre,
+                                const void* const* w2, void* dhpre, void* split_ws, size_t split_ws_bytes,
+                                hipStream_t stream);
+int rhp_expert_fc1_dgrad_scatter(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int act, int h, int f,
+                                 const void* dhpre, const void* const* w1, void* dx, int64_t dx_rows,
+                                 const int32_t* dx_idx, void* split_ws, size_t split_ws_bytes, hipStream_t stream);
+
 /* ------------------------------------------------------------------ optimizer step */
 
 /*

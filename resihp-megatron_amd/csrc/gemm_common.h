@@ -62,6 +62,14 @@ struct Params {
     uint32_t* q_amax;
     float* q_scale_inv;
     int q_ld, q_L, q_margin;
+    // Row maps of the row-grouped modes (kernels instantiated with MAP): row r
+    // of the grouped order reads row a_idx[r] of the token-row buffer a[g]
+    // (a_rows rows; an index outside them reads zeros), and the plain-store
+    // epilogue writes its row r to row c_idx[r] of c[g] (c_rows rows; an index
+    // outside them drops the row).  Null: row r itself.
+    const int32_t* a_idx;
+    const int32_t* c_idx;
+    int64_t a_rows, c_rows;
 };
 
 // ------------------------------------------------------------------ activations
@@ -468,11 +476,40 @@ __device__ __forceinline__ void unpack_bf16x4(uint2 v, float* o) {
 // columns).  Stores go through views of the tile's valid rows, so that a
 // piece's address is one add from the previous one's and pieces of rows past
 // the tile drop out in the memory unit.
-template <int MODE, int EPI, int NT>
+// Destination rows of a half under a scatter map: lane n of a wave holds the
+// c_idx row of the wave's n-th row of the half (rows r0 + wave + (NT / 64) n),
+// or -1 past the tile's valid rows.
+template <int NT>
+__device__ __forceinline__ int32_t scatter_rows_half(const Params& p, const Tile& t, int r0) {
+    constexpr int kN = kEpRows * 64 / NT;
+    const int lane = threadIdx.x & 63, r = r0 + (threadIdx.x >> 6) + (NT / 64) * lane;
+    if (lane >= kN || r >= t.y_lim) return -1;
+    const int32_t d = p.c_idx[t.row0 + t.y0 + r];
+    return d >= 0 && d < p.c_rows ? d : -1;
+}
+
+template <int MODE, int EPI, int NT, bool MAP = false>
 __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, const float* ep, int r0,
-                                              const AuxHalf<EPI, NT>& aux) {
+                                              const AuxHalf<EPI, NT>& aux, int32_t dst_rows = -1) {
     const int g = t.g;
     const int64_t first = tile_first_row<MODE>(t);
+    if constexpr (MAP && EPI == kEpiStore) {
+        if (p.c_idx != nullptr) {
+            // Scattered rows: the view spans the whole output; each row's offset comes from the map.
+            const __amdgpu_buffer_rsrc_t ov = __builtin_amdgcn_make_buffer_rsrc(
+                p.c[g], 0, static_cast<int>(p.c_rows * p.ldc * 2), 0x00020000);
+            const int x = (threadIdx.x & 63) * 4;
+            const bool ok = x < t.x_lim;
+#pragma unroll
+            for (int n = 0; n < kEpRows * 64 / NT; ++n) {
+                const int32_t d = __builtin_amdgcn_readlane(dst_rows, n);
+                const uint32_t off = ok && d >= 0 ? static_cast<uint32_t>((d * p.ldc + t.x0 + x) * 2) : kOutOfRange;
+                const float4 v = lds_f4(ep, (threadIdx.x >> 6) + n * (NT / 64), x);
+                view_store_bf16x4(ov, off, 0, v.x, v.y, v.z, v.w);
+            }
+            return;
+        }
+    }
     if (EPI == kEpiSwigluFwd) {
         // X columns of the tile are [gate 64 | up 64] for each half of 128
         // activation columns; thread t covers activation columns 4 (t % 32) ..
@@ -723,12 +760,15 @@ struct SplitSum {
 
 // One half of the epilogue (rows [HALF * 128, +128) of the tile): load the
 // half's aux values, stage the fp32 results in LDS, then write the half.
-template <int HALF, int MODE, int EPI, int NT, int WY, int QF>
+template <int HALF, int MODE, int EPI, int NT, int WY, int QF, bool MAP>
 __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, float* ep, f32x16_t (&acc)[4][WY / 32],
                                               int wx, int wy, int lane, float mul, const SplitSum& split, QuantAcc& qa) {
     constexpr int FY = WY / 32;
     AuxHalf<EPI, NT> aux;
     load_aux_half<MODE, EPI, NT>(p, t, HALF * kEpRows, aux);
+    int32_t dst_rows = -1;
+    if constexpr (MAP && EPI == kEpiStore && QF < 0)
+        if (p.c_idx != nullptr) dst_rows = scatter_rows_half<NT>(p, t, HALF * kEpRows);
     lds_barrier();
     if ((wy * WY) / kEpRows == HALF) {
         if (split.pieces) {
@@ -780,7 +820,7 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
     if constexpr (QF >= 0)
         epilogue_half_q<MODE, EPI, NT, QF>(p, t, ep, HALF * kEpRows, aux, qa);
     else
-        epilogue_half<MODE, EPI, NT>(p, t, ep, HALF * kEpRows, aux);
+        epilogue_half<MODE, EPI, NT, MAP>(p, t, ep, HALF * kEpRows, aux, dst_rows);
 }
 
 // Epilogue, in two halves of 128 Y rows.  The pre-activation values a
@@ -796,8 +836,9 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
 // load into the LDS buffer has completed.  With a K split, the staged values
 // are the sum of the pieces' partial tiles instead of acc.  QF >= 0 (an fp8
 // format) makes the epilogue quantising (the Params q fields): each wave
-// raises the amax once, after both halves.
-template <int MODE, int EPI, int NT = kThreadsMfma, int WY = kWaveY, int QF = -1>
+// raises the amax once, after both halves.  MAP: a plain-store epilogue
+// writes its rows through the c_idx scatter map when one is given.
+template <int MODE, int EPI, int NT = kThreadsMfma, int WY = kWaveY, int QF = -1, bool MAP = false>
 __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][WY / 32],
                                          int wx, int wy, int lane, float mul = 1.0f,
                                          SplitSum split = SplitSum{nullptr, 0, 0}) {
@@ -805,8 +846,8 @@ __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t
     float* ep = reinterpret_cast<float*>(lds);
     QuantAcc qa{1.0f, 0.0f};
     if constexpr (QF >= 0) qa.scale = history_scale(p.q_hist, p.q_L, fp8_max(QF), p.q_margin);
-    epilogue_pass<0, MODE, EPI, NT, WY, QF>(p, t, ep, acc, wx, wy, lane, mul, split, qa);
-    epilogue_pass<1, MODE, EPI, NT, WY, QF>(p, t, ep, acc, wx, wy, lane, mul, split, qa);
+    epilogue_pass<0, MODE, EPI, NT, WY, QF, MAP>(p, t, ep, acc, wx, wy, lane, mul, split, qa);
+    epilogue_pass<1, MODE, EPI, NT, WY, QF, MAP>(p, t, ep, acc, wx, wy, lane, mul, split, qa);
     if constexpr (QF >= 0) {
         // Wave maximum, then one atomic per wave; non-negative floats order like
         // their bits, and a maximum not above the value read (possibly stale,

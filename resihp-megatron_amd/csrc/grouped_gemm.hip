@@ -23,6 +23,7 @@
 // output column block, then by row block, and block ids are remapped so each
 // XCD runs a contiguous range of that order.
 #include <type_traits>
+#include <vector>
 
 #include "gemm_common.h"
 
@@ -105,7 +106,9 @@ constexpr uint32_t kPastView = 0x7ffffff0u;   // soffset that puts every lane pa
 // piece of a K-split tile, the hand-over to the piece that finishes last).
 // REBASE (weight gradients whose group rows may pass 2 GiB of one operand):
 // every K step's loads go through a view based at the step's first row.
-template <int MODE, int EPI, int NW, bool REBASE = false>
+// MAP (row-grouped products): token rows are gathered through a_idx and a
+// plain-store epilogue scatters its rows through c_idx (the Params row maps).
+template <int MODE, int EPI, int NW, bool REBASE = false, bool MAP = false>
 __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* lds) {
     // NW waves: wave w owns X rows [128 (w % 2), +128) and Y rows [WY (w / 2), +WY).
     constexpr int WY = kTile / (NW / 2), FY = WY / 32;
@@ -144,9 +147,22 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
         d64_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
         d64_mnmaj(my, lda, t.y0, t.y_lim, wy * WY, FY);
     } else {
-        ry = make_dma_rsrc(A + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda * 2);
         const int y_last = t.y_lim - 1;
-        d64_kmaj(my, lda, wy * WY, FY, [&](int r) { return r < t.y_lim ? r : y_last; });
+        if (MAP && p.a_idx != nullptr) {
+            // Gathered token rows: tile row r is row a_idx[row0 + y0 + r] of A, through a view of
+            // all of A (below 2 GiB, checked by the host); an index outside it maps to the row just
+            // past the view, which reads zeros.
+            ry = make_dma_rsrc(A, p.a_rows * p.lda * 2);
+            const int32_t* ix = p.a_idx + t.row0 + t.y0;
+            const uint32_t n_rows = static_cast<uint32_t>(p.a_rows);
+            d64_kmaj(my, lda, wy * WY, FY, [&](int r) {
+                const uint32_t src = static_cast<uint32_t>(ix[r < t.y_lim ? r : y_last]);
+                return src < n_rows ? src : n_rows;
+            });
+        } else {
+            ry = make_dma_rsrc(A + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda * 2);
+            d64_kmaj(my, lda, wy * WY, FY, [&](int r) { return r < t.y_lim ? r : y_last; });
+        }
         if (MODE == kFwd) {
             rx = make_dma_rsrc(B, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb * 2);
             d64_kmaj(mx, ldb, wx * 128, 4, [&](int r) {
@@ -332,19 +348,19 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
     }
     if (MODE != kWgrad && t.pieces > 1) {
         if (!split_arrive<64 * NW, FY>(p, t, acc, lds)) return;
-        epilogue<MODE, EPI, 64 * NW, WY>(p, t, lds, acc, wx, wy, lane, 1.0f, split_sum_of(p, t));
+        epilogue<MODE, EPI, 64 * NW, WY, -1, MAP>(p, t, lds, acc, wx, wy, lane, 1.0f, split_sum_of(p, t));
         return;
     }
-    epilogue<MODE, EPI, 64 * NW, WY>(p, t, lds, acc, wx, wy, lane);
+    epilogue<MODE, EPI, 64 * NW, WY, -1, MAP>(p, t, lds, acc, wx, wy, lane);
 }
 
 // One block per tile (hardware block b runs on XCD b % 8).
-template <int MODE, int EPI, int NW, bool REBASE = false>
+template <int MODE, int EPI, int NW, bool REBASE = false, bool MAP = false>
 __global__ __launch_bounds__(64 * NW) void gg_bf16_kernel(Params p) {
     __shared__ __align__(1024) uint8_t lds[kLdsSlotsBytes];
     Tile t;
     if (find_tile<MODE>(p, x_per_tile<EPI>(), kTile, blockIdx.x, &t) != kTileOk) return;
-    gg_bf16_tile<MODE, EPI, NW, REBASE>(p, t, lds);
+    gg_bf16_tile<MODE, EPI, NW, REBASE, MAP>(p, t, lds);
 }
 
 // ------------------------------------------------------------------ generic kernel (any dtype)
@@ -379,8 +395,18 @@ __global__ __launch_bounds__(256) void gg_simt_kernel(Params p) {
             continue;
         }
         const int64_t row = t.row0 + t.y0 + y;
+        // Row maps: the token row read (a_idx) and the output row written (c_idx); -1 = none.
+        int64_t arow = row, crow = row;
+        if (p.a_idx) {
+            const int32_t s = p.a_idx[row];
+            arow = s >= 0 && s < p.a_rows ? s : -1;
+        }
+        if (p.c_idx) {
+            const int32_t s = p.c_idx[row];
+            crow = s >= 0 && s < p.c_rows ? s : -1;
+        }
         for (int kk = 0; kk < p.K; ++kk) {
-            const A av = Elem<S>::ld(Ap, row * p.lda + kk);
+            const A av = arow >= 0 ? Elem<S>::ld(Ap, arow * p.lda + kk) : A(0);
             if (MODE == kFwd) {
                 acc += av * Elem<S>::ld(Bp, static_cast<int64_t>(col) * p.ldb + kk);
                 if (EPI == kEpiSwigluFwd) acc_up += av * Elem<S>::ld(Bp, static_cast<int64_t>(p.f + col) * p.ldb + kk);
@@ -389,7 +415,7 @@ __global__ __launch_bounds__(256) void gg_simt_kernel(Params p) {
             }
         }
         if (EPI == kEpiStore) {
-            Elem<S>::st(C, row * p.ldc + col, acc);
+            if (crow >= 0) Elem<S>::st(C, crow * p.ldc + col, acc);
         } else if (EPI == kEpiSwigluFwd) {
             Elem<S>::st(C, row * p.ldc + col, acc);
             Elem<S>::st(C, row * p.ldc + p.f + col, acc_up);
@@ -426,6 +452,9 @@ struct Job {
     const void* const* aux;
     void* split_ws;   // K-split workspace (rhp_expert_split_workspace_bytes), or null
     int cus_per_xcd;  // CUs per XCD of the device the launch runs on
+    const int32_t* a_idx;   // row maps (Params::a_idx, c_idx), or null
+    const int32_t* c_idx;
+    int64_t a_rows, c_rows;
 };
 
 // Blocks of a launch: an upper bound of its tiles.  Row-grouped products:
@@ -457,6 +486,13 @@ void launch_one(const Job& j, const Params& p, hipStream_t s) {
         // A K split adds at most one round of pieces to each XCD's items.
         if (MODE != kWgrad && p.split_cap > 1) nb = kXcds * ((nb + kXcds - 1) / kXcds + p.cu_per_xcd);
         constexpr int nw = MODE == kFwd ? 4 : kWaves;
+        if constexpr (MODE != kWgrad) {
+            if (j.a_idx || j.c_idx) {
+                hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, nw, false, true>), dim3(static_cast<unsigned>(nb)),
+                                   dim3(64 * nw), 0, s, p);
+                return;
+            }
+        }
         if constexpr (MODE == kWgrad) {
             // Per-step views cost 15-20 % of a weight-gradient product; they are needed only where a
             // group's rows may span 2 GiB of an operand (rows_cap rows of the wider one).
@@ -528,6 +564,10 @@ int run(const Job& job, const char* what, hipStream_t s) {
         p.ldaux = j.ldaux;
         p.f = j.f;
         p.rows_cap = static_cast<int>(j.rows_cap);
+        p.a_idx = j.a_idx;
+        p.c_idx = j.c_idx;
+        p.a_rows = j.a_rows;
+        p.c_rows = j.c_rows;
         // Only reductions long enough to be split get the split (and its larger
         // grid: the extra, mostly empty blocks cost about 1 % of a short product).
         if (j.split_ws && j.mfma && j.mode != kWgrad && j.K >= kSplitMinK) {
@@ -824,4 +864,191 @@ extern "C" int rhp_expert_fc1_bwd(int G, const int32_t* offsets, int rows_from_o
     w.b = xp;
     w.c = dw1;
     return run(w, "expert_fc1_wgrad", stream);
+}
+
+// ------------------------------------------------------------------ products on received rows (row maps)
+
+namespace rhp {
+namespace {
+
+// Views of a gathered or scattered buffer must stay below 2 GiB on the MFMA
+// kernel, with one row to spare (the zero row an invalid index maps to).
+constexpr int64_t kMapViewBytes = 0x7ffffff0;
+
+int check_map(const char* fn, const Job& j, const void* buf, int64_t rows, const int32_t* idx, int ld) {
+    RHP_REQUIRE(buf != nullptr && idx != nullptr, std::string(fn) + ": null row buffer or row map");
+    RHP_REQUIRE(rows >= 0 && rows < (int64_t(1) << 31), std::string(fn) + ": row count out of range");
+    if (j.mfma) {
+        RHP_REQUIRE(aligned16(buf), std::string(fn) + ": bfloat16 operands must be 16-byte aligned");
+        RHP_REQUIRE((rows + 1) * ld * 2 <= kMapViewBytes,
+                    std::string(fn) + ": the mapped row buffer must stay below 2 GiB (gather it with "
+                                      "rhp_gather_rows and call the plain product instead)");
+    }
+    return 0;
+}
+
+int map_common(const char* fn, int G, const int32_t* offsets, int64_t rows_cap, int dtype, int act, int h, int f,
+               const void* split_ws, size_t split_ws_bytes, const void* const* w) {
+    if (int rc = check_common(fn, G, offsets, rows_cap, dtype, act, h, f)) return rc;
+    if (int rc = check_split_ws(fn, split_ws, split_ws_bytes)) return rc;
+    RHP_REQUIRE(all_set(w, G), std::string(fn) + ": null weight pointer");
+    return 0;
+}
+
+}  // namespace
+}  // namespace rhp
+
+extern "C" int rhp_expert_fc1_fwd_gather(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int act, int h,
+                                         int f, const void* src, int64_t src_rows, const int32_t* src_idx,
+                                         const void* const* w1, void* hpre, void* act_out, void* split_ws,
+                                         size_t split_ws_bytes, hipStream_t stream) {
+    clear_error();
+    const char* fn = "rhp_expert_fc1_fwd_gather";
+    if (int rc = map_common(fn, G, offsets, rows_cap, dtype, act, h, f, split_ws, split_ws_bytes, w1)) return rc;
+    RHP_REQUIRE(hpre && act_out, "rhp_expert_fc1_fwd_gather: null output");
+    const bool swiglu = act == RHP_ACT_SWIGLU;
+    const int F1 = swiglu ? 2 * f : f;
+    Job j{};
+    j.mode = kFwd;
+    j.epi = swiglu ? kEpiSwigluFwd : kEpiGeluFwd;
+    j.dtype = dtype;
+    if (int rc = choose_kernel(fn, dtype, h, f, act, all_aligned(w1, G) && aligned16(hpre) && aligned16(act_out),
+                               &j.mfma))
+        return rc;
+    if (int rc = check_map(fn, j, src, src_rows, src_idx, h)) return rc;
+    std::vector<const void*> a(G, src);
+    std::vector<void*> c(G, hpre), c2(G, act_out);
+    j.G = G;
+    j.offsets = offsets;
+    j.rows_from_offsets = 1;
+    j.rows_cap = rows_cap;
+    j.N = f;
+    j.K = h;
+    j.lda = h;
+    j.ldb = h;
+    j.ldc = F1;
+    j.ldc2 = f;
+    j.f = f;
+    j.a = a.data();
+    j.b = w1;
+    j.c = c.data();
+    j.c2 = c2.data();
+    j.split_ws = split_ws;
+    j.a_idx = src_idx;
+    j.a_rows = src_rows;
+    return run(j, "expert_fc1_fwd_gather", stream);
+}
+
+extern "C" int rhp_expert_fc2_fwd_scatter(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int h, int f,
+                                          const void* act_in, const void* const* w2, void* y, int64_t y_rows,
+                                          const int32_t* y_idx, void* split_ws, size_t split_ws_bytes,
+                                          hipStream_t stream) {
+    clear_error();
+    const char* fn = "rhp_expert_fc2_fwd_scatter";
+    if (int rc = map_common(fn, G, offsets, rows_cap, dtype, RHP_ACT_GELU, h, f, split_ws, split_ws_bytes, w2))
+        return rc;
+    RHP_REQUIRE(act_in != nullptr, "rhp_expert_fc2_fwd_scatter: null act_in");
+    Job j{};
+    j.mode = kFwd;
+    j.epi = kEpiStore;
+    j.dtype = dtype;
+    if (int rc = choose_kernel(fn, dtype, h, f, RHP_ACT_GELU, all_aligned(w2, G) && aligned16(act_in), &j.mfma))
+        return rc;
+    if (int rc = check_map(fn, j, y, y_rows, y_idx, h)) return rc;
+    std::vector<const void*> a(G, act_in);
+    std::vector<void*> c(G, y);
+    j.G = G;
+    j.offsets = offsets;
+    j.rows_from_offsets = 1;
+    j.rows_cap = rows_cap;
+    j.N = h;
+    j.K = f;
+    j.lda = f;
+    j.ldb = f;
+    j.ldc = h;
+    j.f = f;
+    j.a = a.data();
+    j.b = w2;
+    j.c = c.data();
+    j.split_ws = split_ws;
+    j.c_idx = y_idx;
+    j.c_rows = y_rows;
+    return run(j, "expert_fc2_fwd_scatter", stream);
+}
+
+extern "C" int rhp_expert_fc2_dgrad_gather(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int act, int h,
+                                           int f, const void* dy, int64_t dy_rows, const int32_t* dy_idx,
+                                           const void* hpre, const void* const* w2, void* dhpre, void* split_ws,
+                                           size_t split_ws_bytes, hipStream_t stream) {
+    clear_error();
+    const char* fn = "rhp_expert_fc2_dgrad_gather";
+    if (int rc = map_common(fn, G, offsets, rows_cap, dtype, act, h, f, split_ws, split_ws_bytes, w2)) return rc;
+    RHP_REQUIRE(hpre && dhpre, "rhp_expert_fc2_dgrad_gather: null hpre or dhpre");
+    const bool swiglu = act == RHP_ACT_SWIGLU;
+    const int F1 = swiglu ? 2 * f : f;
+    Job d{};
+    d.mode = kDgrad;
+    d.epi = swiglu ? kEpiSwigluBwd : kEpiGeluBwd;
+    d.dtype = dtype;
+    if (int rc = choose_kernel(fn, dtype, h, f, act, all_aligned(w2, G) && aligned16(hpre) && aligned16(dhpre),
+                               &d.mfma))
+        return rc;
+    if (int rc = check_map(fn, d, dy, dy_rows, dy_idx, h)) return rc;
+    std::vector<const void*> a(G, dy), aux(G, hpre);
+    std::vector<void*> c(G, dhpre);
+    d.G = G;
+    d.offsets = offsets;
+    d.rows_from_offsets = 1;
+    d.rows_cap = rows_cap;
+    d.N = f;
+    d.K = h;
+    d.lda = h;
+    d.ldb = f;
+    d.ldc = F1;
+    d.ldaux = F1;
+    d.f = f;
+    d.a = a.data();
+    d.b = w2;
+    d.c = c.data();
+    d.aux = aux.data();
+    d.split_ws = split_ws;
+    d.a_idx = dy_idx;
+    d.a_rows = dy_rows;
+    return run(d, "expert_fc2_dgrad_gather", stream);
+}
+
+extern "C" int rhp_expert_fc1_dgrad_scatter(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int act,
+                                            int h, int f, const void* dhpre, const void* const* w1, void* dx,
+                                            int64_t dx_rows, const int32_t* dx_idx, void* split_ws,
+                                            size_t split_ws_bytes, hipStream_t stream) {
+    clear_error();
+    const char* fn = "rhp_expert_fc1_dgrad_scatter";
+    if (int rc = map_common(fn, G, offsets, rows_cap, dtype, act, h, f, split_ws, split_ws_bytes, w1)) return rc;
+    RHP_REQUIRE(dhpre != nullptr, "rhp_expert_fc1_dgrad_scatter: null dhpre");
+    const int F1 = act == RHP_ACT_SWIGLU ? 2 * f : f;
+    Job d{};
+    d.mode = kDgrad;
+    d.epi = kEpiStore;
+    d.dtype = dtype;
+    if (int rc = choose_kernel(fn, dtype, h, f, act, all_aligned(w1, G) && aligned16(dhpre), &d.mfma)) return rc;
+    if (int rc = check_map(fn, d, dx, dx_rows, dx_idx, h)) return rc;
+    std::vector<const void*> a(G, dhpre);
+    std::vector<void*> c(G, dx);
+    d.G = G;
+    d.offsets = offsets;
+    d.rows_from_offsets = 1;
+    d.rows_cap = rows_cap;
+    d.N = h;
+    d.K = F1;
+    d.lda = F1;
+    d.ldb = h;
+    d.ldc = h;
+    d.f = f;
+    d.a = a.data();
+    d.b = w1;
+    d.c = c.data();
+    d.split_ws = split_ws;
+    d.c_idx = dx_idx;
+    d.c_rows = dx_rows;
+    return run(d, "expert_fc1_dgrad_scatter", stream);
 }

@@ -470,6 +470,74 @@ def expert_fc1_bwd(dhpre: list[torch.Tensor], xs: list[torch.Tensor], offsets: t
                 _arr(dxs) if dxs else None, _arr(dw1) if dw1 is not None else None)
 
 
+def _check_map(what: str, idx: torch.Tensor, rows_cap: int) -> None:
+    _expect(idx.dtype == torch.int32 and idx.dim() == 1 and idx.is_contiguous() and idx.numel() >= rows_cap,
+            f"{what}: the row map must be a contiguous int32 vector of at least {rows_cap} entries")
+
+
+def expert_fc1_fwd_gather(src: torch.Tensor, src_idx: torch.Tensor, offsets: torch.Tensor, rows_cap: int,
+                          w1: list[torch.Tensor], f: int, act: str, hpre: torch.Tensor, act_out: torch.Tensor,
+                          split: bool = True) -> None:
+    """expert_fc1_fwd on rows gathered from ``src``: grouped row r is ``src[src_idx[r]]`` (no copy)."""
+    dev = _need_cuda(offsets, src, src_idx, *w1, hpre, act_out)
+    G, dt, h = len(w1), w1[0].dtype, w1[0].shape[1]
+    F1 = 2 * f if act == "swiglu" else f
+    _check_offsets(offsets, G)
+    _check_map("src_idx", src_idx, rows_cap)
+    _check_groups("w1", w1, G, dt, h, exact_shape=(F1, h))
+    _check_groups("src", [src], 1, dt, h)
+    _check_groups("hpre", [hpre], 1, dt, F1, rows_cap)
+    _check_groups("act", [act_out], 1, dt, f, rows_cap)
+    _split_call("rhp_expert_fc1_fwd_gather", dev, split, G, _ptr(offsets), rows_cap, dtype_code(w1[0]),
+                act_code(act), h, f, _ptr(src), src.shape[0], _ptr(src_idx), _arr(w1), _ptr(hpre), _ptr(act_out))
+
+
+def expert_fc2_fwd_scatter(act_in: torch.Tensor, offsets: torch.Tensor, rows_cap: int, w2: list[torch.Tensor],
+                           y: torch.Tensor, y_idx: torch.Tensor, split: bool = True) -> None:
+    """expert_fc2_fwd writing grouped row r to ``y[y_idx[r]]`` (no copy)."""
+    dev = _need_cuda(offsets, act_in, y, y_idx, *w2)
+    G, dt, (h, f) = len(w2), w2[0].dtype, tuple(w2[0].shape)
+    _check_offsets(offsets, G)
+    _check_map("y_idx", y_idx, rows_cap)
+    _check_groups("w2", w2, G, dt, f, exact_shape=(h, f))
+    _check_groups("act", [act_in], 1, dt, f, rows_cap)
+    _check_groups("y", [y], 1, dt, h)
+    _split_call("rhp_expert_fc2_fwd_scatter", dev, split, G, _ptr(offsets), rows_cap, dtype_code(w2[0]), h, f,
+                _ptr(act_in), _arr(w2), _ptr(y), y.shape[0], _ptr(y_idx))
+
+
+def expert_fc2_dgrad_gather(dy: torch.Tensor, dy_idx: torch.Tensor, offsets: torch.Tensor, rows_cap: int,
+                            w2: list[torch.Tensor], act: str, hpre: torch.Tensor, dhpre: torch.Tensor,
+                            split: bool = True) -> None:
+    """The input-gradient product of expert_fc2_bwd on output-gradient rows ``dy[dy_idx[r]]`` (no copy)."""
+    dev = _need_cuda(offsets, dy, dy_idx, hpre, dhpre, *w2)
+    G, dt, (h, f) = len(w2), w2[0].dtype, tuple(w2[0].shape)
+    F1 = 2 * f if act == "swiglu" else f
+    _check_offsets(offsets, G)
+    _check_map("dy_idx", dy_idx, rows_cap)
+    _check_groups("w2", w2, G, dt, f, exact_shape=(h, f))
+    _check_groups("dy", [dy], 1, dt, h)
+    _check_groups("hpre", [hpre], 1, dt, F1, rows_cap)
+    _check_groups("dhpre", [dhpre], 1, dt, F1, rows_cap)
+    _split_call("rhp_expert_fc2_dgrad_gather", dev, split, G, _ptr(offsets), rows_cap, dtype_code(w2[0]),
+                act_code(act), h, f, _ptr(dy), dy.shape[0], _ptr(dy_idx), _ptr(hpre), _arr(w2), _ptr(dhpre))
+
+
+def expert_fc1_dgrad_scatter(dhpre: torch.Tensor, offsets: torch.Tensor, rows_cap: int, w1: list[torch.Tensor],
+                             f: int, act: str, dx: torch.Tensor, dx_idx: torch.Tensor, split: bool = True) -> None:
+    """The input-gradient product of expert_fc1_bwd writing grouped row r to ``dx[dx_idx[r]]`` (no copy)."""
+    dev = _need_cuda(offsets, dhpre, dx, dx_idx, *w1)
+    G, dt, h = len(w1), w1[0].dtype, w1[0].shape[1]
+    F1 = 2 * f if act == "swiglu" else f
+    _check_offsets(offsets, G)
+    _check_map("dx_idx", dx_idx, rows_cap)
+    _check_groups("w1", w1, G, dt, h, exact_shape=(F1, h))
+    _check_groups("dhpre", [dhpre], 1, dt, F1, rows_cap)
+    _check_groups("dx", [dx], 1, dt, h)
+    _split_call("rhp_expert_fc1_dgrad_scatter", dev, split, G, _ptr(offsets), rows_cap, dtype_code(w1[0]),
+                act_code(act), h, f, _ptr(dhpre), _arr(w1), _ptr(dx), dx.shape[0], _ptr(dx_idx))
+
+
 # ----------------------------------------------------------------------------- optimizer
 
 

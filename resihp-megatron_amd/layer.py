@@ -286,11 +286,13 @@ class _ExpertChunksFn(torch.autograd.Function):
     """The receiving side of expert parallelism: the expert FFN over a source-major received buffer.
 
     resihp/runtime/moe.py:213-224 runs ``expert_ffn`` on every (source, expert) chunk of the received
-    rows in order and returns the outputs in that order.  Here the chunks are regrouped expert-major
-    (a row gather), every local expert is one group of the grouped GEMMs, and the outputs are gathered
-    back into the received order.  The backward mirrors it: the output gradient rows arrive in the
-    received order, are regrouped, run through the expert backward, and the input gradient leaves in
-    the received order again.
+    rows in order and returns the outputs in that order.  Here every local expert is one group of the
+    grouped GEMMs over the chunks' expert-major order (the recv plan), and the products read and write
+    received rows through the plan's row map: fc1 gathers its input rows, fc2 scatters its outputs
+    back into the received order, and in the backward fc2's input-gradient product gathers the output
+    gradient rows and fc1's scatters the input gradient.  Only the weight gradients need expert-major
+    copies (of the inputs and of the output gradients); those gathers run on the side stream, beside
+    the products.
     """
 
     @staticmethod
@@ -302,35 +304,62 @@ class _ExpertChunksFn(torch.autograd.Function):
         if recv.shape[0] != P:
             raise K.KernelArgumentError(f"the received buffer has {recv.shape[0]} rows, the counts {P}")
         F1 = _fc1_rows(act, f)
-        xs = K.gather_rows(recv, plan.sort_row)
+        xs = recv.new_empty(P, h)
         hpre = recv.new_empty(P, F1)
         a = recv.new_empty(P, f)
         y = recv.new_empty(P, h)
         if P > 0:
-            K.expert_fc1_fwd([xs] * G, plan.offsets, True, P, fc1s, f, act, [hpre] * G, [a] * G)
-            K.expert_fc2_fwd([a] * G, plan.offsets, True, P, fc2s, [y] * G)
+            main = torch.cuda.current_stream(recv.device)
+            side = _side_stream(recv.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                K.gather_rows(recv, plan.sort_row, out=xs)   # expert-major inputs, for the fc1 weight gradient
+            K.expert_fc1_fwd_gather(recv, plan.sort_row, plan.offsets, P, fc1s, f, act, hpre, a)
+            K.expert_fc2_fwd_scatter(a, plan.offsets, P, fc2s, y, plan.sort_row)
+            main.wait_stream(side)
         ctx.act, ctx.f, ctx.P = act, f, P
-        ctx.save_for_backward(plan.offsets, plan.sort_row, plan.unsort_row, xs, hpre, a, *fc1s, *fc2s)
-        return K.gather_rows(y, plan.unsort_row)
+        ctx.save_for_backward(plan.offsets, plan.sort_row, xs, hpre, a, *fc1s, *fc2s)
+        return y
 
     @staticmethod
     def backward(ctx, dy_recv):
-        offsets, sort_row, unsort_row, xs, hpre, a, *ws = ctx.saved_tensors
+        offsets, sort_row, xs, hpre, a, *ws = ctx.saved_tensors
         G = len(ws) // 2
         fc1s, fc2s = ws[:G], ws[G:]
         act, f, P = ctx.act, ctx.f, ctx.P
         dw1 = [torch.empty_like(w) for w in fc1s]
         dw2 = [torch.empty_like(w) for w in fc2s]
         drecv = None
+        need_x = ctx.needs_input_grad[4]
         if P > 0:
-            dy = K.gather_rows(dy_recv.contiguous(), sort_row)
+            dy_recv = dy_recv.contiguous()
+            h = xs.shape[1]
+            dys = torch.empty_like(xs)          # expert-major output gradients, for the fc2 weight gradient
             dhpre = torch.empty_like(hpre)
-            need_x = ctx.needs_input_grad[4]
-            dxp = torch.empty_like(xs) if need_x else None
-            expert_backward([dy] * G, [a] * G, [hpre] * G, offsets, True, P, fc1s, fc2s, f, act, [dhpre] * G,
-                            [xs] * G, [dxp] * G if need_x else None, dw1, dw2)
-            if need_x:
-                drecv = K.gather_rows(dxp, unsort_row)
+            main = torch.cuda.current_stream(xs.device)
+            if _concurrent(h, hpre.shape[1]):
+                # Weight gradients (and the gather they need) on the side stream, input gradients here.
+                side = _side_stream(xs.device)
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    K.gather_rows(dy_recv, sort_row, out=dys)
+                    K.expert_fc2_bwd([dys] * G, [a] * G, [hpre] * G, offsets, True, P, fc2s, act, None, dw2)
+                K.expert_fc2_dgrad_gather(dy_recv, sort_row, offsets, P, fc2s, act, hpre, dhpre)
+                side.wait_stream(main)
+                with torch.cuda.stream(side):
+                    K.expert_fc1_bwd([dhpre] * G, [xs] * G, offsets, True, P, fc1s, f, act, None, dw1)
+                if need_x:
+                    drecv = torch.empty_like(dy_recv)
+                    K.expert_fc1_dgrad_scatter(dhpre, offsets, P, fc1s, f, act, drecv, sort_row)
+                main.wait_stream(side)
+            else:
+                K.gather_rows(dy_recv, sort_row, out=dys)
+                K.expert_fc2_dgrad_gather(dy_recv, sort_row, offsets, P, fc2s, act, hpre, dhpre)
+                K.expert_fc2_bwd([dys] * G, [a] * G, [hpre] * G, offsets, True, P, fc2s, act, None, dw2)
+                K.expert_fc1_bwd([dhpre] * G, [xs] * G, offsets, True, P, fc1s, f, act, None, dw1)
+                if need_x:
+                    drecv = torch.empty_like(dy_recv)
+                    K.expert_fc1_dgrad_scatter(dhpre, offsets, P, fc1s, f, act, drecv, sort_row)
         else:
             for w in (*dw1, *dw2):
                 w.zero_()

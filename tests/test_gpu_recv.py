@@ -64,6 +64,97 @@ def test_gather_rows_rejects_unaligned_rows():
         K.gather_rows(src, torch.zeros(2, dtype=torch.int32, device=DEV))
 
 
+def _map_case(counts, src_rows, seed, invalid):
+    """Offsets of ragged groups and a row map: distinct received rows (a random subset of src_rows in
+    random order), optionally with a few indices outside the buffer."""
+    rng = np.random.default_rng(seed)
+    P = int(sum(counts))
+    idx = rng.permutation(src_rows)[:P].astype(np.int32)
+    if invalid:
+        bad = rng.choice(P, 5, replace=False)
+        idx[bad[:3]] = -1
+        idx[bad[3:]] = src_rows + np.array([0, 7])
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    return torch.from_numpy(offsets).to(DEV), torch.from_numpy(idx).to(DEV), P
+
+
+@pytest.mark.parametrize("dtype,h,f,invalid", [(torch.bfloat16, 256, 128, False), (torch.bfloat16, 2048, 768, True),
+                                               (torch.bfloat16, 96, 40, True), (torch.float32, 128, 64, True)],
+                         ids=["bf16-mfma", "bf16-mfma-ep128-dims-bad-idx", "bf16-generic", "f32-generic"])
+def test_row_map_products_equal_gather_then_product(dtype, h, f, invalid):
+    """The four products on received rows (gathered inputs, scattered outputs) equal rhp_gather_rows
+    followed by the plain product, bit for bit, on both kernels: ragged groups (one empty), distinct
+    received rows in random order, indices outside the buffer (zero rows in, rows dropped out), and
+    buffer rows that no index names (left untouched)."""
+    counts = [300, 0, 517, 64, 1029] if dtype == torch.bfloat16 and h >= 256 else [33, 0, 70, 5]
+    src_rows = int(sum(counts)) + 41
+    offsets, idx, P = _map_case(counts, src_rows, h + f, invalid)
+    G = len(counts)
+    gen = torch.Generator(device=DEV).manual_seed(h * 7 + f)
+    rnd = lambda *sh, std=1.0: (torch.randn(*sh, generator=gen, device=DEV) * std).to(dtype)  # noqa: E731
+    w1 = [rnd(2 * f, h, std=0.05) for _ in range(G)]
+    w2 = [rnd(h, f, std=0.05) for _ in range(G)]
+    src, dy_src = rnd(src_rows, h), rnd(src_rows, h)
+    kind = K.gemm_kernel(dtype, "swiglu", h, f)
+    assert kind == ("mfma" if dtype == torch.bfloat16 and h % 64 == 0 and f % 64 == 0 else "generic")
+    say(f"row-map products {dtype} h={h} f={f} ({kind}), P={P}, invalid={invalid}")
+    empty = lambda n, c: torch.empty(n, c, dtype=dtype, device=DEV)  # noqa: E731
+    # forward: fc1 on gathered rows
+    xs = K.gather_rows(src, idx)
+    hpre_r, a_r = empty(P, 2 * f), empty(P, f)
+    K.expert_fc1_fwd([xs] * G, offsets, True, P, w1, f, "swiglu", [hpre_r] * G, [a_r] * G)
+    hpre, a = empty(P, 2 * f), empty(P, f)
+    K.expert_fc1_fwd_gather(src, idx, offsets, P, w1, f, "swiglu", hpre, a)
+    # forward: fc2 scattered back
+    y_r = empty(P, h)
+    K.expert_fc2_fwd([a_r] * G, offsets, True, P, w2, [y_r] * G)
+    sentinel = torch.full((src_rows, h), 7.0, dtype=dtype, device=DEV)
+    y = sentinel.clone()
+    K.expert_fc2_fwd_scatter(a_r, offsets, P, w2, y, idx)
+    # backward: fc2 input gradient on gathered output gradients, fc1 input gradient scattered
+    dys = K.gather_rows(dy_src, idx)
+    dh_r = empty(P, 2 * f)
+    K.expert_fc2_bwd([dys] * G, [a_r] * G, [hpre_r] * G, offsets, True, P, w2, "swiglu", [dh_r] * G, None)
+    dh = empty(P, 2 * f)
+    K.expert_fc2_dgrad_gather(dy_src, idx, offsets, P, w2, "swiglu", hpre_r, dh)
+    dx_r = empty(P, h)
+    K.expert_fc1_bwd([dh_r] * G, [xs] * G, offsets, True, P, w1, f, "swiglu", [dx_r] * G, None)
+    dx = sentinel.clone()
+    K.expert_fc1_dgrad_scatter(dh_r, offsets, P, w1, f, "swiglu", dx, idx)
+    torch.cuda.synchronize()
+    assert torch.equal(hpre, hpre_r) and torch.equal(a, a_r)
+    assert torch.equal(dh, dh_r)
+    ix = idx.long()
+    ok = (ix >= 0) & (ix < src_rows)
+    named = torch.zeros(src_rows, dtype=torch.bool, device=DEV)
+    named[ix[ok]] = True
+    for out, ref in ((y, y_r), (dx, dx_r)):
+        assert torch.equal(out[ix[ok]], ref[ok])
+        assert torch.equal(out[~named], sentinel[~named])
+    if invalid:
+        assert not bool(ok.all()) and bool((xs[~ok] == 0).all())
+
+
+def test_row_map_products_reject_bad_maps():
+    h, f = 256, 128
+    w1 = [torch.zeros(2 * f, h, dtype=torch.bfloat16, device=DEV)]
+    w2 = [torch.zeros(h, f, dtype=torch.bfloat16, device=DEV)]
+    offsets = torch.tensor([0, 4], dtype=torch.int32, device=DEV)
+    idx = torch.arange(4, dtype=torch.int32, device=DEV)
+    act = torch.zeros(4, f, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(K.KernelArgumentError, match="row map"):
+        K.expert_fc2_fwd_scatter(act, offsets, 4, w2, torch.zeros(4, h, dtype=torch.bfloat16, device=DEV), idx[:3])
+    with pytest.raises(K.KernelArgumentError, match="row map"):
+        K.expert_fc2_fwd_scatter(act, offsets, 4, w2, torch.zeros(4, h, dtype=torch.bfloat16, device=DEV),
+                                 idx.to(torch.int64))
+    # a mapped buffer of 2 GiB does not fit the MFMA kernel's 31-bit views: an error, not a wrong result
+    big = torch.empty((1 << 31) // (2 * h), h, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="below 2 GiB"):
+        K.expert_fc1_fwd_gather(big, idx, offsets, 4, w1, f, "swiglu",
+                                torch.zeros(4, 2 * f, dtype=torch.bfloat16, device=DEV), act.clone())
+    del big
+
+
 def _ep_share(T: int, window: tuple[int, int], n_src: int = 8):
     """Routing of T source tokens (n_src sources by even_split) over 128 experts, top-8, with the Zipf
     selection prior; the received buffer of the device holding the window, in the reference's order."""
