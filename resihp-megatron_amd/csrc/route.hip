@@ -367,21 +367,41 @@ __device__ __forceinline__ void block_range(const DispatchShape& d, int b, int64
 
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (lane == 0) ? 0ull : ((~0ull) >> (64 - lane)); }
 
-// Lanes of the wave whose key equals mine (among lanes with valid keys).
-__device__ __forceinline__ uint64_t match_any(bool valid, int key) {
-    uint64_t pending = __ballot(valid);
-    uint64_t mine = 0;
-    while (pending) {
-        const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
-        const int lk = __shfl(key, leader, 64);
-        const uint64_t m = __ballot(valid && key == lk);
-        if (valid && key == lk) mine = m;
-        pending &= ~m;
+// Lanes of the wave whose key equals mine (among lanes with valid keys), in
+// nbits ballots: a lane matches when it agrees with mine on every key bit.
+// Keys lie in [0, 2^nbits).
+__device__ __forceinline__ uint64_t match_any(bool valid, int key, int nbits) {
+    uint64_t m = __ballot(valid);
+    for (int i = 0; i < nbits; ++i) {
+        const bool bit = (key >> i) & 1;
+        const uint64_t b = __ballot(valid && bit);
+        m &= bit ? b : ~b;
     }
-    return mine;
+    return valid ? m : 0ull;
 }
 
-// Phase 1: per-block expert histogram with wave-aggregated LDS atomics.
+// Bits of the largest key n - 1 (at least one).
+__host__ __device__ constexpr int key_bits(int n) {
+    int b = 1;
+    while ((1 << b) < n) ++b;
+    return b;
+}
+
+constexpr int kDispatchRounds = kDispatchPairs / kThreads;   // rounds of one pair per thread in a block
+
+// The expert ids of a block's pairs, loaded all at once (one pair per thread
+// and round, pair p0 + r kThreads + thread): every round's load is in flight
+// together, not one at a time.  Entries past the block are not read.
+__device__ __forceinline__ void load_block_ids(const int32_t* topi, int64_t p0, int64_t p1,
+                                               int (&e)[kDispatchRounds]) {
+#pragma unroll
+    for (int r = 0; r < kDispatchRounds; ++r) {
+        const int64_t p = p0 + static_cast<int64_t>(r) * kThreads + threadIdx.x;
+        e[r] = p < p1 ? topi[p] : 0;
+    }
+}
+
+// Phase 1: per-block expert histogram; one LDS atomic per distinct id of a wave and round.
 __global__ __launch_bounds__(kThreads) void dispatch_count_kernel(const int32_t* __restrict__ topi, DispatchShape d,
                                                                   int32_t* __restrict__ block_counts,
                                                                   int32_t* __restrict__ block_src) {
@@ -391,15 +411,16 @@ __global__ __launch_bounds__(kThreads) void dispatch_count_kernel(const int32_t*
     int64_t ts, te;
     int src;
     block_range(d, b, &ts, &te, &src);
+    int ids[kDispatchRounds];
+    load_block_ids(topi, ts * d.k, te * d.k, ids);
     __syncthreads();
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, nbits = key_bits(d.E + 1);
     const int64_t p0 = ts * d.k, p1 = te * d.k;
-    for (int64_t base = p0; base < p1; base += kThreads) {
-        const int64_t p = base + threadIdx.x;
-        const bool valid = p < p1;
-        int e = valid ? topi[p] : 0;
-        if (e < 0 || e >= d.E) e = d.E;
-        const uint64_t m = match_any(valid, e);
+#pragma unroll
+    for (int r = 0; r < kDispatchRounds; ++r) {
+        const bool valid = p0 + static_cast<int64_t>(r) * kThreads + threadIdx.x < p1;
+        const int e = ids[r] < 0 || ids[r] >= d.E ? d.E : ids[r];   // d.E counts ids outside [0, E)
+        const uint64_t m = match_any(valid, e, nbits);
         if (valid && (m & lanemask_lt(lane)) == 0) atomicAdd(&hist[e], __popcll(m));
     }
     __syncthreads();
@@ -408,7 +429,10 @@ __global__ __launch_bounds__(kThreads) void dispatch_count_kernel(const int32_t*
 }
 
 // Phase 2 (one block): totals, local offsets, per-source counts and the base
-// row of every (block, local expert).
+// row of every (block, local expert).  The per-block histograms are staged in
+// LDS first (one load per entry, all in flight together) when they fit.
+constexpr int kScanStage = 16384;   // histogram entries staged in LDS (64 KB)
+
 __global__ __launch_bounds__(1024) void dispatch_scan_kernel(const int32_t* __restrict__ block_counts,
                                                              const int32_t* __restrict__ block_src, DispatchShape d,
                                                              int32_t* __restrict__ counts,
@@ -417,10 +441,17 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(const int32_t* __re
                                                              int32_t* __restrict__ block_base) {
     __shared__ int tot[kMaxE + 1];
     __shared__ int off[kMaxE + 1];
-    const int L = d.e1 - d.e0;
+    __shared__ int stage[kScanStage];
+    const int L = d.e1 - d.e0, W = d.E + 1;
+    const int64_t n = static_cast<int64_t>(d.nblk) * W;
+    const bool staged = n <= kScanStage;
+    if (staged)
+        for (int i = threadIdx.x; i < n; i += blockDim.x) stage[i] = block_counts[i];
+    __syncthreads();
+    auto cnt = [&](int b, int e) { return staged ? stage[b * W + e] : block_counts[static_cast<int64_t>(b) * W + e]; };
     for (int e = threadIdx.x; e <= d.E; e += blockDim.x) {
         int sum = 0;
-        for (int b = 0; b < d.nblk; ++b) sum += block_counts[static_cast<int64_t>(b) * (d.E + 1) + e];
+        for (int b = 0; b < d.nblk; ++b) sum += cnt(b, e);
         tot[e] = sum;
         counts[e] = sum;
     }
@@ -442,7 +473,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(const int32_t* __re
         int run = off[i];
         int cur_src = -1, cur = 0;
         for (int b = 0; b < d.nblk; ++b) {
-            const int c = block_counts[static_cast<int64_t>(b) * (d.E + 1) + e];
+            const int c = cnt(b, e);
             block_base[static_cast<int64_t>(b) * L + i] = run;
             run += c;
             const int s = block_src[b];
@@ -459,7 +490,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(const int32_t* __re
 
 // Phase 3: stable scatter.  Pairs of a block are ranked in ascending p: within
 // a wave by lane order, across the block's waves by wave order, across
-// iterations by a running per-expert count.
+// rounds by a running per-expert count.
 __global__ __launch_bounds__(kThreads) void dispatch_scatter_kernel(const int32_t* __restrict__ topi, DispatchShape d,
                                                                     const int32_t* __restrict__ block_base,
                                                                     int32_t* __restrict__ perm,
@@ -470,29 +501,33 @@ __global__ __launch_bounds__(kThreads) void dispatch_scatter_kernel(const int32_
     const int b = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int i = threadIdx.x; i < L; i += kThreads) {
-        run[i] = 0;
+        run[i] = block_base[static_cast<int64_t>(b) * L + i];
 #pragma unroll
         for (int w = 0; w < kThreads / 64; ++w) wcnt[w][i] = 0;
     }
     int64_t ts, te;
     int src;
     block_range(d, b, &ts, &te, &src);
-    __syncthreads();
     const int64_t p0 = ts * d.k, p1 = te * d.k;
-    for (int64_t base = p0; base < p1; base += kThreads) {
-        const int64_t p = base + threadIdx.x;
+    int ids[kDispatchRounds];
+    load_block_ids(topi, p0, p1, ids);
+    __syncthreads();
+    const int nbits = key_bits(L);
+    for (int r = 0; r < kDispatchRounds; ++r) {
+        const int64_t p = p0 + static_cast<int64_t>(r) * kThreads + threadIdx.x;
+        if (p0 + static_cast<int64_t>(r) * kThreads >= p1) break;   // uniform: no pairs left in the block
         const bool in = p < p1;
-        const int e = in ? topi[p] : -1;
+        const int e = ids[r];
         const bool local = in && e >= d.e0 && e < d.e1;
         const int li = local ? e - d.e0 : 0;
-        const uint64_t m = match_any(local, li);
+        const uint64_t m = match_any(local, li, nbits);
         const int rank = __popcll(m & lanemask_lt(lane));
         if (local && rank == 0) wcnt[wave][li] = __popcll(m);
         __syncthreads();
         if (local) {
             int pre = run[li];
             for (int w = 0; w < wave; ++w) pre += wcnt[w][li];
-            const int row = block_base[static_cast<int64_t>(b) * L + li] + pre + rank;
+            const int row = pre + rank;
             perm[row] = static_cast<int32_t>(p);
             pair_row[p] = row;
         } else if (in) {
