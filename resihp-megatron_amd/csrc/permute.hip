@@ -514,18 +514,16 @@ __global__ __launch_bounds__(kThreads) void combine_bwd_bf16_kernel(const bf16* 
     }
 }
 
+// One token of the bf16 token backward: dx[t] = dout[t] + sum_j dxp[row_j] + sum_j dl_j * router_w[e_j]
+// (+ the shared experts' input gradients), one wave per token.  RW is where the router rows are
+// read: the router matrix in memory or its copy in LDS (same values, same operations).
 template <int KM, int SM, int U>
-__global__ __launch_bounds__(kThreads) void token_bwd_bf16_kernel(const bf16* __restrict__ dout,
-                                                                  const bf16* __restrict__ dxp,
-                                                                  const int32_t* __restrict__ pair_row,
-                                                                  const float* __restrict__ dl,
-                                                                  const int32_t* __restrict__ topi,
-                                                                  const float* __restrict__ router_w,
-                                                                  SharedPtrs shared, int n_shared, int64_t T, int h,
-                                                                  int E, int k, bf16* __restrict__ dx) {
+__device__ __forceinline__ void token_bwd_bf16_row(const bf16* __restrict__ dout, const bf16* __restrict__ dxp,
+                                                   const int32_t* __restrict__ pair_row, const float* __restrict__ dl,
+                                                   const int32_t* __restrict__ topi, const float* rw,
+                                                   const SharedPtrs& shared, int n_shared, int64_t t, int h, int E,
+                                                   int k, bf16* __restrict__ dx) {
     const int lane = threadIdx.x & 63;
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-    if (t >= T) return;
     int32_t rows[KM], ex[KM];
     float d[KM];
 #pragma unroll
@@ -572,11 +570,10 @@ __global__ __launch_bounds__(kThreads) void token_bwd_bf16_kernel(const bf16* __
 #pragma unroll
                     for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
                 }
-            // Router rows are small and stay in L2: loaded here, per chunk.
             float wv[KM][8];
 #pragma unroll
             for (int j = 0; j < KM; ++j)
-                if (ex[j] >= 0) Vec8<float, float>::load(router_w + static_cast<int64_t>(ex[j]) * h + c * 8, wv[j]);
+                if (ex[j] >= 0) Vec8<float, float>::load(rw + static_cast<int64_t>(ex[j]) * h + c * 8, wv[j]);
 #pragma unroll
             for (int j = 0; j < KM; ++j)
                 if (ex[j] >= 0) {
@@ -594,6 +591,43 @@ __global__ __launch_bounds__(kThreads) void token_bwd_bf16_kernel(const bf16* __
             store16(dx + t * h + c * 8, pack_bf16x8(acc));
         }
     }
+}
+
+// Router rows from memory (they are small and stay in L2), one token per wave.
+template <int KM, int SM, int U>
+__global__ __launch_bounds__(kThreads) void token_bwd_bf16_kernel(const bf16* __restrict__ dout,
+                                                                  const bf16* __restrict__ dxp,
+                                                                  const int32_t* __restrict__ pair_row,
+                                                                  const float* __restrict__ dl,
+                                                                  const int32_t* __restrict__ topi,
+                                                                  const float* __restrict__ router_w,
+                                                                  SharedPtrs shared, int n_shared, int64_t T, int h,
+                                                                  int E, int k, bf16* __restrict__ dx) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (t >= T) return;
+    token_bwd_bf16_row<KM, SM, U>(dout, dxp, pair_row, dl, topi, router_w, shared, n_shared, t, h, E, k, dx);
+}
+
+// Router matrix in LDS: a block per CU copies it once and its waves walk the
+// tokens; the router rows of a token (k of them, 4 h bytes each) then come
+// from LDS instead of k more row reads through L2 per token.
+constexpr int kTokenBwdLdsFloats = 32768;   // 128 KB: router matrices of at most this many elements
+constexpr int kTokenBwdLdsThreads = 1024;
+
+template <int KM, int SM, int U>
+__global__ __launch_bounds__(kTokenBwdLdsThreads) void token_bwd_bf16_lds_kernel(
+    const bf16* __restrict__ dout, const bf16* __restrict__ dxp, const int32_t* __restrict__ pair_row,
+    const float* __restrict__ dl, const int32_t* __restrict__ topi, const float* __restrict__ router_w,
+    SharedPtrs shared, int n_shared, int64_t T, int h, int E, int k, bf16* __restrict__ dx) {
+    __shared__ __align__(16) float rw[kTokenBwdLdsFloats];
+    const int n4 = E * h / 4;
+    for (int i = threadIdx.x; i < n4; i += blockDim.x)
+        reinterpret_cast<float4*>(rw)[i] = reinterpret_cast<const float4*>(router_w)[i];
+    __syncthreads();
+    const int nw = blockDim.x >> 6;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * nw + (threadIdx.x >> 6); t < T;
+         t += static_cast<int64_t>(gridDim.x) * nw)
+        token_bwd_bf16_row<KM, SM, U>(dout, dxp, pair_row, dl, topi, rw, shared, n_shared, t, h, E, k, dx);
 }
 
 // Batched bf16 variants by (k, shared experts); larger k or more shared
@@ -900,7 +934,18 @@ extern "C" int rhp_token_bwd(const void* dout, const void* dxp, const int32_t* p
             const float* dlf = static_cast<const float*>(dlogits_sel);
             const float* wf = static_cast<const float*>(router_w);
             bf16* dxb = static_cast<bf16*>(dx);
-            switch (row_variant(k, n_shared)) {
+            // With the router term and a router matrix that fits in LDS: one block per CU keeps it there
+            // (k <= 2 without shared experts: the variant whose registers fit 16 waves a CU).
+            const RowVariant rv = row_variant(k, n_shared);
+            if (dlf != nullptr && static_cast<int64_t>(E) * h <= kTokenBwdLdsFloats && rv == RowVariant::kSmall) {
+                const int64_t per_block = kTokenBwdLdsThreads / 64;   // tokens a block takes at a time
+                const unsigned nb = static_cast<unsigned>(
+                    std::max<int64_t>(1, std::min<int64_t>(device_cus(), (T + per_block - 1) / per_block)));
+                hipLaunchKernelGGL((token_bwd_bf16_lds_kernel<2, 0, 4>), dim3(nb), dim3(kTokenBwdLdsThreads), 0,
+                                   stream, db, xb, pair_row, dlf, topi, wf, sp, n_shared, T, h, E, k, dxb);
+                return check_launch("token_bwd_bf16_lds_kernel");
+            }
+            switch (rv) {
                 case RowVariant::kSmall:
                     hipLaunchKernelGGL((token_bwd_bf16_kernel<2, 0, 4>), grid, block, 0, stream, db, xb, pair_row,
                                        dlf, topi, wf, sp, n_shared, T, h, E, k, dxb);

@@ -50,6 +50,19 @@ inline size_t dtype_bytes(int dt) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Compute units of the current device (cached per device id); 256 if unknown.
+inline int device_cus() {
+    static int cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int c = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+    if (c == 0) {
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) return 256;
+        __atomic_store_n(&cache[dev], c, __ATOMIC_RELAXED);
+    }
+    return c;
+}
+
 // ------------------------------------------------------------------ bfloat16
 
 struct bf16 {

@@ -431,7 +431,8 @@ __global__ __launch_bounds__(kThreads) void dispatch_count_kernel(const int32_t*
 // Phase 2 (one block): totals, local offsets, per-source counts and the base
 // row of every (block, local expert).  The per-block histograms are staged in
 // LDS first (one load per entry, all in flight together) when they fit.
-constexpr int kScanStage = 16384;   // histogram entries staged in LDS (64 KB)
+constexpr int kScanStage = 16384;     // histogram entries staged in LDS (64 KB)
+constexpr int kScanStageSrc = 4096;   // block sources staged in LDS (16 KB)
 
 __global__ __launch_bounds__(1024) void dispatch_scan_kernel(const int32_t* __restrict__ block_counts,
                                                              const int32_t* __restrict__ block_src, DispatchShape d,
@@ -442,13 +443,17 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(const int32_t* __re
     __shared__ int tot[kMaxE + 1];
     __shared__ int off[kMaxE + 1];
     __shared__ int stage[kScanStage];
+    __shared__ int stage_src[kScanStageSrc];
     const int L = d.e1 - d.e0, W = d.E + 1;
     const int64_t n = static_cast<int64_t>(d.nblk) * W;
-    const bool staged = n <= kScanStage;
+    const bool staged = n <= kScanStage, staged_src = d.nblk <= kScanStageSrc;
     if (staged)
         for (int i = threadIdx.x; i < n; i += blockDim.x) stage[i] = block_counts[i];
+    if (staged_src)
+        for (int i = threadIdx.x; i < d.nblk; i += blockDim.x) stage_src[i] = block_src[i];
     __syncthreads();
     auto cnt = [&](int b, int e) { return staged ? stage[b * W + e] : block_counts[static_cast<int64_t>(b) * W + e]; };
+    auto src_of = [&](int b) { return staged_src ? stage_src[b] : block_src[b]; };
     for (int e = threadIdx.x; e <= d.E; e += blockDim.x) {
         int sum = 0;
         for (int b = 0; b < d.nblk; ++b) sum += cnt(b, e);
@@ -476,7 +481,7 @@ __global__ __launch_bounds__(1024) void dispatch_scan_kernel(const int32_t* __re
             const int c = cnt(b, e);
             block_base[static_cast<int64_t>(b) * L + i] = run;
             run += c;
-            const int s = block_src[b];
+            const int s = src_of(b);
             if (s != cur_src) {
                 if (cur_src >= 0) src_counts[cur_src * L + i] = cur;
                 cur_src = s;
