@@ -54,7 +54,7 @@ RECEIVED = {"ep128-share"}
 
 GEMM_CALLS = ("rhp_expert_fc1_fwd", "rhp_expert_fc2_fwd", "rhp_expert_fc2_bwd", "rhp_expert_fc1_bwd", "rhp_fp8_gemm",
               "rhp_fp8_gemm_cast", "rhp_expert_fc1_fwd_gather", "rhp_expert_fc2_fwd_scatter",
-              "rhp_expert_fc2_dgrad_gather", "rhp_expert_fc1_dgrad_scatter")
+              "rhp_expert_fc2_dgrad_gather", "rhp_expert_fc1_dgrad_scatter", "rhp_expert_fc1_dgrad_router")
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 
 

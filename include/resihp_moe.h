@@ -329,6 +329,23 @@ int rhp_expert_fc1_dgrad_scatter(int G, const int32_t* offsets, int64_t rows_cap
                                  const void* dhpre, const void* const* w1, void* dx, int64_t dx_rows,
                                  const int32_t* dx_idx, void* split_ws, size_t split_ws_bytes, hipStream_t stream);
 
+/*
+ * fc1's input-gradient product with the router's term of the token backward
+ * folded into its epilogue: for expert-major row r of group g (expert e0 + g),
+ *   dxp[r] = dhpre[r] @ w1 + dlogits_sel[perm[r]] * router_w[e0 + g]
+ * rounded once to the row dtype.  rhp_token_bwd then runs without dlogits_sel:
+ * sum_j dxp[row_j] holds every slot's router term (moe.py:76-79, 164-167).
+ * Valid only when every expert of the layer is local (all pairs have a row);
+ * with a window the router terms of other devices' pairs would be missing.
+ * router_w: fp32 [E, h]; perm: the dispatch plan's row -> pair map;
+ * dlogits_sel: fp32 [T, k] (rhp_route_bwd).  BF16 or F32 experts.  No reference
+ * counterpart as an entry point: a fusion of two autograd terms.
+ */
+int rhp_expert_fc1_dgrad_router(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int act, int h, int f,
+                                const void* const* dhpre, const void* const* w1, const float* router_w, int e0,
+                                const int32_t* perm, const float* dlogits_sel, void* const* dxp, void* split_ws,
+                                size_t split_ws_bytes, hipStream_t stream);
+
 /* ------------------------------------------------------------------ optimizer step */
 
 /*

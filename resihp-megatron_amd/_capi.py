@@ -53,6 +53,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "rhp_expert_fc2_fwd_scatter": (_i, [_i, _p, _i64, _i, _i, _i, _p, _pp, _p, _i64, _p, _p, _sz, _p]),
     "rhp_expert_fc2_dgrad_gather": (_i, [_i, _p, _i64, _i, _i, _i, _i, _p, _i64, _p, _p, _pp, _p, _p, _sz, _p]),
     "rhp_expert_fc1_dgrad_scatter": (_i, [_i, _p, _i64, _i, _i, _i, _i, _p, _pp, _p, _i64, _p, _p, _sz, _p]),
+    "rhp_expert_fc1_dgrad_router": (_i, [_i, _p, _i64, _i, _i, _i, _i, _pp, _pp, _p, _i, _p, _p, _pp, _p, _sz, _p]),
     "rhp_adam_step": (_i, [_i, _pp, _pp, _pp, _pp, _p, _i, _d, _d, _d, _d, _d, _i64, _p]),
     "rhp_fp8_padded_offsets": (_i, [_p, _i, _i, _p, _p]),
     "rhp_fp8_cast": (_i, [_p, _i, _i64, _i, _i, _p, _p, _i64, _p, _i, _i, _i, _p, _p, _p, _p, _p]),

@@ -16,7 +16,7 @@ namespace {
 constexpr int kMaxG = RHP_MAX_GROUPS_PER_LAUNCH;
 
 enum Mode { kFwd = 0, kDgrad = 1, kWgrad = 2 };
-enum Epi { kEpiStore = 0, kEpiSwigluFwd = 1, kEpiGeluFwd = 2, kEpiSwigluBwd = 3, kEpiGeluBwd = 4 };
+enum Epi { kEpiStore = 0, kEpiSwigluFwd = 1, kEpiGeluFwd = 2, kEpiSwigluBwd = 3, kEpiGeluBwd = 4, kEpiStoreRouter = 5 };
 
 struct Params {
     const void* a[kMaxG];     // FWD/DGRAD: token rows A; WGRAD: gradient rows G
@@ -70,6 +70,14 @@ struct Params {
     const int32_t* a_idx;
     const int32_t* c_idx;
     int64_t a_rows, c_rows;
+    // kEpiStoreRouter (the input-gradient product of fc1 with the router's
+    // term): row r of group g gets rdl[rperm[r]] * rw[(rw_e0 + g) * N + column]
+    // added before it is rounded; rw is the fp32 router matrix, rperm the
+    // dispatch plan's row -> pair map, rdl the selected-logit gradients.
+    const float* rw;
+    const int32_t* rperm;
+    const float* rdl;
+    int rw_e0;
 };
 
 // ------------------------------------------------------------------ activations
@@ -488,11 +496,40 @@ __device__ __forceinline__ int32_t scatter_rows_half(const Params& p, const Tile
     return d >= 0 && d < p.c_rows ? d : -1;
 }
 
+// The router term's row factors of a half: lane n of a wave holds
+// rdl[rperm[row]] of the wave's n-th row (rows r0 + wave + (NT / 64) n), 0 past
+// the tile's valid rows.
+template <int NT>
+__device__ __forceinline__ float router_scale_half(const Params& p, const Tile& t, int r0) {
+    constexpr int kN = kEpRows * 64 / NT;
+    const int lane = threadIdx.x & 63, r = r0 + (threadIdx.x >> 6) + (NT / 64) * lane;
+    if (lane >= kN || r >= t.y_lim) return 0.0f;
+    return p.rdl[p.rperm[t.row0 + t.y0 + r]];
+}
+
 template <int MODE, int EPI, int NT, bool MAP = false>
 __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, const float* ep, int r0,
                                               const AuxHalf<EPI, NT>& aux, int32_t dst_rows = -1) {
     const int g = t.g;
     const int64_t first = tile_first_row<MODE>(t);
+    if constexpr (EPI == kEpiStoreRouter) {
+        // Plain store plus the router term: dst_rows carries the rows' logit gradients (lane n: the
+        // wave's n-th row), the router row's four columns of this thread are loaded once.
+        const __amdgpu_buffer_rsrc_t ov = tile_view(p.c[g], first, p.ldc, t.x0, t.y_lim);
+        const int rr = threadIdx.x >> 6, x = (threadIdx.x & 63) * 4;
+        const bool ok = x < t.x_lim;
+        const float4 w = ok ? *reinterpret_cast<const float4*>(p.rw + static_cast<int64_t>(p.rw_e0 + g) * p.N + t.x0 + x)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        uint32_t off = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc + x) * 2) : kOutOfRange;
+        const uint32_t step = static_cast<uint32_t>((NT / 64) * p.ldc * 2);
+#pragma unroll
+        for (int n = 0; n < kEpRows * 64 / NT; ++n, off += step) {
+            const float d = __int_as_float(__builtin_amdgcn_readlane(dst_rows, n));
+            const float4 v = lds_f4(ep, rr + n * (NT / 64), x);
+            view_store_bf16x4(ov, off, 0, v.x + d * w.x, v.y + d * w.y, v.z + d * w.z, v.w + d * w.w);
+        }
+        return;
+    }
     if constexpr (MAP && EPI == kEpiStore) {
         if (p.c_idx != nullptr) {
             // Scattered rows: the view spans the whole output; each row's offset comes from the map.
@@ -769,6 +806,7 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
     int32_t dst_rows = -1;
     if constexpr (MAP && EPI == kEpiStore && QF < 0)
         if (p.c_idx != nullptr) dst_rows = scatter_rows_half<NT>(p, t, HALF * kEpRows);
+    if constexpr (EPI == kEpiStoreRouter) dst_rows = __float_as_int(router_scale_half<NT>(p, t, HALF * kEpRows));
     lds_barrier();
     if ((wy * WY) / kEpRows == HALF) {
         if (split.pieces) {

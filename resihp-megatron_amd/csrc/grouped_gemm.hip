@@ -416,6 +416,9 @@ __global__ __launch_bounds__(256) void gg_simt_kernel(Params p) {
         }
         if (EPI == kEpiStore) {
             if (crow >= 0) Elem<S>::st(C, crow * p.ldc + col, acc);
+        } else if (EPI == kEpiStoreRouter) {
+            const A w = static_cast<A>(p.rw[static_cast<int64_t>(p.rw_e0 + g) * p.N + col]);
+            Elem<S>::st(C, row * p.ldc + col, acc + static_cast<A>(p.rdl[p.rperm[row]]) * w);
         } else if (EPI == kEpiSwigluFwd) {
             Elem<S>::st(C, row * p.ldc + col, acc);
             Elem<S>::st(C, row * p.ldc + p.f + col, acc_up);
@@ -455,6 +458,10 @@ struct Job {
     const int32_t* a_idx;   // row maps (Params::a_idx, c_idx), or null
     const int32_t* c_idx;
     int64_t a_rows, c_rows;
+    const float* rw;        // router term of kEpiStoreRouter (Params::rw, rperm, rdl, rw_e0)
+    const int32_t* rperm;
+    const float* rdl;
+    int rw_e0;
 };
 
 // Blocks of a launch: an upper bound of its tiles.  Row-grouped products:
@@ -524,6 +531,7 @@ void launch(const Job& j, const Params& p, hipStream_t s) {
         case kDgrad * 8 + kEpiStore: launch_one<kDgrad, kEpiStore>(j, p, s); break;
         case kDgrad * 8 + kEpiSwigluBwd: launch_one<kDgrad, kEpiSwigluBwd>(j, p, s); break;
         case kDgrad * 8 + kEpiGeluBwd: launch_one<kDgrad, kEpiGeluBwd>(j, p, s); break;
+        case kDgrad * 8 + kEpiStoreRouter: launch_one<kDgrad, kEpiStoreRouter>(j, p, s); break;
         case kWgrad * 8 + kEpiStore: launch_one<kWgrad, kEpiStore>(j, p, s); break;
         default: break;
     }
@@ -568,6 +576,10 @@ int run(const Job& job, const char* what, hipStream_t s) {
         p.c_idx = j.c_idx;
         p.a_rows = j.a_rows;
         p.c_rows = j.c_rows;
+        p.rw = j.rw;
+        p.rperm = j.rperm;
+        p.rdl = j.rdl;
+        p.rw_e0 = j.rw_e0 + g0;
         // Only reductions long enough to be split get the split (and its larger
         // grid: the extra, mostly empty blocks cost about 1 % of a short product).
         if (j.split_ws && j.mfma && j.mode != kWgrad && j.K >= kSplitMinK) {
@@ -1051,4 +1063,48 @@ extern "C" int rhp_expert_fc1_dgrad_scatter(int G, const int32_t* offsets, int64
     d.c_idx = dx_idx;
     d.c_rows = dx_rows;
     return run(d, "expert_fc1_dgrad_scatter", stream);
+}
+
+extern "C" int rhp_expert_fc1_dgrad_router(int G, const int32_t* offsets, int64_t rows_cap, int dtype, int act, int h,
+                                           int f, const void* const* dhpre, const void* const* w1,
+                                           const float* router_w, int e0, const int32_t* perm,
+                                           const float* dlogits_sel, void* const* dxp, void* split_ws,
+                                           size_t split_ws_bytes, hipStream_t stream) {
+    clear_error();
+    const char* fn = "rhp_expert_fc1_dgrad_router";
+    if (int rc = check_common(fn, G, offsets, rows_cap, dtype, act, h, f)) return rc;
+    if (int rc = check_split_ws(fn, split_ws, split_ws_bytes)) return rc;
+    RHP_REQUIRE(dtype != RHP_F64, "rhp_expert_fc1_dgrad_router: float64 experts keep the router term in rhp_token_bwd");
+    RHP_REQUIRE(all_set(dhpre, G) && all_set(w1, G) && all_set((const void* const*)dxp, G) && router_w && perm &&
+                    dlogits_sel && e0 >= 0,
+                "rhp_expert_fc1_dgrad_router: null pointer or negative e0");
+    const int F1 = act == RHP_ACT_SWIGLU ? 2 * f : f;
+    Job d{};
+    d.mode = kDgrad;
+    d.epi = kEpiStoreRouter;
+    d.dtype = dtype;
+    if (int rc = choose_kernel(fn, dtype, h, f, act,
+                               all_aligned(dhpre, G) && all_aligned(w1, G) && all_aligned((const void* const*)dxp, G) &&
+                                   aligned16(router_w),
+                               &d.mfma))
+        return rc;
+    d.G = G;
+    d.offsets = offsets;
+    d.rows_from_offsets = 1;
+    d.rows_cap = rows_cap;
+    d.N = h;
+    d.K = F1;
+    d.lda = F1;
+    d.ldb = h;
+    d.ldc = h;
+    d.f = f;
+    d.a = dhpre;
+    d.b = w1;
+    d.c = dxp;
+    d.split_ws = split_ws;
+    d.rw = router_w;
+    d.rperm = perm;
+    d.rdl = dlogits_sel;
+    d.rw_e0 = e0;
+    return run(d, "expert_fc1_dgrad_router", stream);
 }

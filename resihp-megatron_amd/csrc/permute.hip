@@ -947,8 +947,13 @@ extern "C" int rhp_token_bwd(const void* dout, const void* dxp, const int32_t* p
             }
             switch (rv) {
                 case RowVariant::kSmall:
-                    hipLaunchKernelGGL((token_bwd_bf16_kernel<2, 0, 4>), grid, block, 0, stream, db, xb, pair_row,
-                                       dlf, topi, wf, sp, n_shared, T, h, E, k, dxb);
+                    // Without the router term a whole 4096-wide row's loads fit in flight (8 chunks a lane).
+                    if (dlf == nullptr)
+                        hipLaunchKernelGGL((token_bwd_bf16_kernel<2, 0, 8>), grid, block, 0, stream, db, xb, pair_row,
+                                           dlf, topi, wf, sp, n_shared, T, h, E, k, dxb);
+                    else
+                        hipLaunchKernelGGL((token_bwd_bf16_kernel<2, 0, 4>), grid, block, 0, stream, db, xb, pair_row,
+                                           dlf, topi, wf, sp, n_shared, T, h, E, k, dxb);
                     break;
                 case RowVariant::kSmallShared:
                     hipLaunchKernelGGL((token_bwd_bf16_kernel<2, 2, 4>), grid, block, 0, stream, db, xb, pair_row,

@@ -538,6 +538,27 @@ def expert_fc1_dgrad_scatter(dhpre: torch.Tensor, offsets: torch.Tensor, rows_ca
                 act_code(act), h, f, _ptr(dhpre), _arr(w1), _ptr(dx), dx.shape[0], _ptr(dx_idx))
 
 
+def expert_fc1_dgrad_router(dhpre: list[torch.Tensor], offsets: torch.Tensor, rows_cap: int, w1: list[torch.Tensor],
+                            f: int, act: str, router_w: torch.Tensor, e0: int, perm: torch.Tensor, dl: torch.Tensor,
+                            dxs: list[torch.Tensor], split: bool = True) -> None:
+    """fc1's input gradient with the router term added per row: ``dxs[r] = dhpre[r] @ w1 + dl[perm[r]] *
+    router_w[e0 + g]`` (then token_bwd runs without ``dl``).  Every expert of the layer must be local."""
+    dev = _need_cuda(offsets, router_w, perm, dl, *dhpre, *w1, *dxs)
+    G, dt, h = len(w1), w1[0].dtype, w1[0].shape[1]
+    F1 = 2 * f if act == "swiglu" else f
+    _check_offsets(offsets, G)
+    _check_groups("w1", w1, G, dt, h, exact_shape=(F1, h))
+    _check_groups("dhpre", dhpre, G, dt, F1, rows_cap)
+    _check_groups("dx", dxs, G, dt, h, rows_cap)
+    _expect(router_w.dtype == torch.float32 and router_w.dim() == 2 and router_w.shape[1] == h
+            and router_w.is_contiguous() and 0 <= e0 and e0 + G <= router_w.shape[0],
+            "router_w must be a contiguous float32 [E, h] holding experts e0 .. e0 + G")
+    _expect(dl.dtype == torch.float32 and dl.is_contiguous(), "dl must be contiguous float32 [T, k]")
+    _check_map("perm", perm, rows_cap)
+    _split_call("rhp_expert_fc1_dgrad_router", dev, split, G, _ptr(offsets), rows_cap, dtype_code(w1[0]),
+                act_code(act), h, f, _arr(dhpre), _arr(w1), _ptr(router_w), e0, _ptr(perm), _ptr(dl), _arr(dxs))
+
+
 # ----------------------------------------------------------------------------- optimizer
 
 

@@ -67,6 +67,9 @@ def _concurrent(h: int, F1: int) -> bool:
     if CONCURRENT_BACKWARD == "auto":
         return max(h, F1) < SPLIT_MIN_K
     return bool(CONCURRENT_BACKWARD)
+# Add the router term of the input gradient in fc1's input-gradient epilogue (layers whose experts are
+# all local) instead of reading k router rows per token in the token backward.
+FOLD_ROUTER_TERM = True
 _side_streams: dict[int, torch.cuda.Stream] = {}
 
 
@@ -80,15 +83,25 @@ def _side_stream(dev: torch.device) -> torch.cuda.Stream:
 
 
 def expert_backward(dys, acts, hpres, offsets, rows_from_offsets: bool, rows_cap: int, fc1s, fc2s, f: int,
-                    act: str, dhpre, xs, dxs, dw1, dw2) -> None:
+                    act: str, dhpre, xs, dxs, dw1, dw2, router=None) -> None:
     """The expert FFN backward (fc2 then fc1, input and weight gradients) of a group launch.
 
     The weight gradients go to the side stream when the products run concurrently (CONCURRENT_BACKWARD);
-    the current stream waits for them before returning, so every output is ordered on it as usual."""
+    the current stream waits for them before returning, so every output is ordered on it as usual.
+    ``router`` = (router_w, e0, perm, dl) folds the router term into fc1's input gradient."""
     fc1s, fc2s = list(fc1s), list(fc2s)
+
+    def fc1_dgrad():
+        if router is None:
+            K.expert_fc1_bwd(dhpre, xs, offsets, rows_from_offsets, rows_cap, fc1s, f, act, dxs, None)
+        else:
+            K.expert_fc1_dgrad_router(dhpre, offsets, rows_cap, fc1s, f, act, *router, dxs)
+
     if not _concurrent(fc1s[0].shape[1], fc1s[0].shape[0]):
         K.expert_fc2_bwd(dys, acts, hpres, offsets, rows_from_offsets, rows_cap, fc2s, act, dhpre, dw2)
-        K.expert_fc1_bwd(dhpre, xs, offsets, rows_from_offsets, rows_cap, fc1s, f, act, dxs, dw1)
+        if dxs:
+            fc1_dgrad()
+        K.expert_fc1_bwd(dhpre, xs, offsets, rows_from_offsets, rows_cap, fc1s, f, act, None, dw1)
         return
     main = torch.cuda.current_stream(offsets.device)
     side = _side_stream(offsets.device)
@@ -100,7 +113,7 @@ def expert_backward(dys, acts, hpres, offsets, rows_from_offsets: bool, rows_cap
     with torch.cuda.stream(side):
         K.expert_fc1_bwd(dhpre, xs, offsets, rows_from_offsets, rows_cap, fc1s, f, act, None, dw1)
     if dxs:
-        K.expert_fc1_bwd(dhpre, xs, offsets, rows_from_offsets, rows_cap, fc1s, f, act, dxs, None)
+        fc1_dgrad()
     main.wait_stream(side)
 
 
@@ -251,6 +264,11 @@ class _MoELayerFn(torch.autograd.Function):
                 K.expert_fc2_bwd([dout] * S, shared_a, shared_h, shared_off, False, T, list(sfc2s), meta.act, dh, sdw2)
                 K.expert_fc1_bwd(dh, [x] * S, shared_off, False, T, list(sfc1s), fs, meta.act, shared_dx or None, sdw1)
         dy, dgates = K.combine_bwd(dout, y, gates, pair_row, P)
+        dl = K.route_bwd(dgates, gates, logits, topi, meta.score, meta.normalize, meta.gate_scale)
+        # With every expert local each routed slot has a row, so fc1's input-gradient product can add the
+        # router term to its rows (the token backward then sums it with the rows).
+        fold = (need_x and meta.full and ctx.fp8[0] is None and P > 0 and x.dtype != torch.float64
+                and router_w.dtype == torch.float32 and FOLD_ROUTER_TERM)
         dw2 = [torch.empty_like(w) for w in fc2s]
         dw1 = [torch.empty_like(w) for w in fc1s]
         dxp = x.new_empty(P, h) if need_x else None
@@ -260,7 +278,8 @@ class _MoELayerFn(torch.autograd.Function):
         elif P > 0:
             dhpre = x.new_empty(P, _fc1_rows(meta.act, f))
             expert_backward([dy] * G, [act] * G, [hpre] * G, offsets, True, P, fc1s, fc2s, f, meta.act, [dhpre] * G,
-                            [xp] * G, [dxp] * G if need_x else None, dw1, dw2)
+                            [xp] * G, [dxp] * G if need_x else None, dw1, dw2,
+                            router=(router_w, meta.window[0], perm, dl) if fold else None)
         else:
             for w in (*dw1, *dw2):
                 w.zero_()
@@ -269,8 +288,7 @@ class _MoELayerFn(torch.autograd.Function):
                             [x] * S, shared_dx or None, sdw1, sdw2)
         if shared_side:
             main.wait_stream(_side_stream(x.device))
-        dl = K.route_bwd(dgates, gates, logits, topi, meta.score, meta.normalize, meta.gate_scale)
-        dx = K.token_bwd(dout, dxp, pair_row, dl, topi, router_w, shared_dx) if need_x else None
+        dx = K.token_bwd(dout, dxp, pair_row, None if fold else dl, topi, router_w, shared_dx) if need_x else None
         dwr = None
         if ctx.needs_input_grad[3]:
             if meta.full:

@@ -330,3 +330,37 @@ def test_k_split_workspace_per_stream():
     assert torch.equal(y, alone[0])
     counters = ws[K.C.lib().rhp_expert_split_workspace_bytes() - 4 * 256:].view(torch.int32)
     assert int(counters.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("dtype,h,f,counts,e0", [(torch.bfloat16, 256, 128, [300, 0, 517], 2),
+                                                 (torch.bfloat16, 512, 256, [40, 700, 129, 1], 0),
+                                                 (torch.bfloat16, 1024, 8192, [200, 330], 1),
+                                                 (torch.float32, 96, 40, [33, 0, 70], 1)],
+                         ids=["bf16", "bf16-ragged", "bf16-k-split", "f32-generic"])
+def test_fc1_dgrad_router_term(dtype, h, f, counts, e0):
+    """fc1's input gradient with the router term in its epilogue: dxp[r] = dhpre[r] @ w1 + dl[perm[r]] *
+    W_router[e0 + g] against float64 on the same inputs (the third case's reduction of 16384 is K-split)."""
+    G, P = len(counts), sum(counts)
+    E, k = e0 + G + 2, 2
+    T = (P + k - 1) // k + 3
+    offsets = torch.tensor([0] + torch.tensor(counts).cumsum(0).tolist(), dtype=torch.int32, device=DEV)
+    g = torch.Generator().manual_seed(h + f)
+    perm = torch.randperm(T * k, generator=g)[:P].to(torch.int32)
+    dl = torch.randn(T, k, generator=g) * 0.5
+    W = torch.randn(E, h, generator=g) * 0.1 * (2 * f) ** 0.5   # router term as large as the product's rows
+    dh = seeded((P, 2 * f), 3, 1.0, dtype)
+    w1 = [seeded((2 * f, h), 10 + i, 0.05, dtype) for i in range(G)]
+    say(f"fc1 dgrad + router term {dtype} h={h} f={f} counts={counts} e0={e0}")
+    dx = torch.empty(P, h, dtype=dtype, device=DEV)
+    K.expert_fc1_dgrad_router([dh.to(DEV)] * G, offsets, P, [w.to(DEV) for w in w1], f, "swiglu", W.to(DEV), e0,
+                              perm.to(DEV), dl.to(DEV), [dx] * G)
+    torch.cuda.synchronize()
+    ref = torch.empty(P, h, dtype=torch.float64)
+    o = offsets.cpu().tolist()
+    for i in range(G):
+        r = slice(o[i], o[i + 1])
+        ref[r] = dh[r].double() @ w1[i].double() + dl.double().view(-1)[perm[r].long()][:, None] * W[e0 + i].double()
+    assert rel_err(dx, ref) <= (2e-2 if dtype == torch.bfloat16 else 1e-5)
+    # the router term is really there: without it the rows differ by far more than the rounding
+    bare = torch.cat([dh[o[i]:o[i + 1]].double() @ w1[i].double() for i in range(G)])
+    assert rel_err(bare, ref) > 1e-2

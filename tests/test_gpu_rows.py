@@ -135,12 +135,19 @@ def _rows_bit_exact(dtype, T, h, k, E, window, n_shared):
     for j in range(k):
         r = rows[:, j]
         a = np.where((r >= 0)[:, None], a + dxpn[np.clip(r, 0, None)], a)
+    a_rows = a.copy()
     dln, wn = dl.numpy(), w.numpy()
     for j in range(k):
         a = a + (dln[:, j][:, None] * wn[topi.numpy()[:, j]]).astype(acc)
     for sh in sdx:
         a = a + _to_np(sh, acc)
+        a_rows = a_rows + _to_np(sh, acc)
     assert torch.equal(dx.cpu(), _store(a, dtype))
+    # without the router term (the layer adds it in fc1's input-gradient epilogue when every expert is local)
+    dx0 = K.token_bwd(dout.to(DEV), dxp.to(DEV), pair_row.to(DEV), None, topi.to(DEV), w.to(DEV),
+                      [s.to(DEV) for s in sdx])
+    torch.cuda.synchronize()
+    assert torch.equal(dx0.cpu(), _store(a_rows, dtype))
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=str)
