@@ -79,13 +79,17 @@ def _map_case(counts, src_rows, seed, invalid):
 
 
 @pytest.mark.parametrize("dtype,h,f,invalid", [(torch.bfloat16, 256, 128, False), (torch.bfloat16, 2048, 768, True),
-                                               (torch.bfloat16, 96, 40, True), (torch.float32, 128, 64, True)],
-                         ids=["bf16-mfma", "bf16-mfma-ep128-dims-bad-idx", "bf16-generic", "f32-generic"])
+                                               (torch.bfloat16, 256, 4096, True), (torch.bfloat16, 96, 40, True),
+                                               (torch.float32, 128, 64, True)],
+                         ids=["bf16-mfma", "bf16-mfma-ep128-dims-bad-idx", "bf16-mfma-k-split", "bf16-generic",
+                              "f32-generic"])
 def test_row_map_products_equal_gather_then_product(dtype, h, f, invalid):
     """The four products on received rows (gathered inputs, scattered outputs) equal rhp_gather_rows
     followed by the plain product, bit for bit, on both kernels: ragged groups (one empty), distinct
     received rows in random order, indices outside the buffer (zero rows in, rows dropped out), and
-    buffer rows that no index names (left untouched)."""
+    buffer rows that no index names (left untouched).  With f = 4096 fc1's input-gradient product
+    reduces over 8192 and its last round is split along K (the scatter then runs in the epilogue of
+    the piece that finishes last)."""
     counts = [300, 0, 517, 64, 1029] if dtype == torch.bfloat16 and h >= 256 else [33, 0, 70, 5]
     src_rows = int(sum(counts)) + 41
     offsets, idx, P = _map_case(counts, src_rows, h + f, invalid)
