@@ -400,32 +400,52 @@ int rhp_fp8_cast(const void* x, int x_dtype, int64_t ldx, int cols, int G, const
                  const int32_t* poff, int64_t rows_cap, const float* history, int hist_len, int fmt, int margin,
                  uint32_t* amax_bits, float* scale_inv, void* q, void* qt, hipStream_t stream);
 
+/*
+ * rhp_fp8_cast of n whole tensors in one launch (the expert weights of a
+ * layer), each with its own history, amax and 1 / scale, row-major codes only:
+ * x[i] bf16 [rows[i], cols[i]] contiguous, q[i] fp8 [rows[i], cols[i]].  Codes,
+ * amax and 1 / scale equal those of one rhp_fp8_cast per tensor.  Host arrays
+ * of n entries; cols[i] a multiple of 64.
+ */
+int rhp_fp8_cast_many(int n, const void* const* x, const int64_t* rows, const int64_t* cols,
+                      const float* const* history, int hist_len, int fmt, int margin, uint32_t* const* amax_bits,
+                      float* const* scale_inv, void* const* q, hipStream_t stream);
+
 /* End of iteration for n tensors: history[i] = [amax_i, history[i][0 .. hist_len-2]], amax_i = 0 (reference_model.py:215). */
 int rhp_fp8_amax_roll(float* history, uint32_t* amax_bits, int n, int hist_len, hipStream_t stream);
 
 /*
  * Grouped fp8 product, bf16 output, with the epilogues of the bf16 entry points.
  * Replaces the expert FFN products of resihp/runtime/moe.py:82-83 and their
- * autograd backward when the experts run in fp8.  Both operands have K
- * contiguous ("NT"); the result is multiplied by y_scale_inv[0] * x_scale_inv[g * x_scale_stride].
- *   kgroups = 0: out[r, n] = sum_k y[g][r, k] x[g][n, k] for the rows r of expert g
+ * autograd backward when the experts run in fp8.  The result is multiplied by
+ * y_scale_inv[0] * x_scale_inv[g * x_scale_stride].  Modes 0 and 1 read both
+ * operands K-contiguous; modes 2 and 3 read x (and in mode 3 also y)
+ * N-contiguous, transposing in LDS, so they take the row-major codes where
+ * modes 0 and 1 need transposed copies, with the same sums bit for bit:
+ *   mode 0: out[r, n] = sum_k y[g][r, k] x[g][n, k] for the rows r of expert g
  *                (offsets; y[g] holds all rows, row pitch ldy; x[g]: [N or 2f, K], pitch ldx).
  *                epi: 0 store, 1 SwiGLU forward (x rows [gate; up], out = hpre [.., 2f], c2 = act,
  *                N = f), 2 GELU forward (c2 = act), 3 SwiGLU backward, 4 GELU backward
  *                (aux = hpre); K a multiple of 128.
- *   kgroups = 1: out_g[o, n] = sum_t y_g[o, t] x_g[n, t] over the R_g padded rows of expert g,
+ *   mode 1: out_g[o, n] = sum_t y_g[o, t] x_g[n, t] over the R_g padded rows of expert g,
  *                with y_g = y[0] + Mo * poff[g], x_g = x[0] + N * poff[g] (the qt copies of
  *                rhp_fp8_cast; offsets = poff), row pitch R_g; epi must be 0.
+ *   mode 2: out[r, n] = sum_k y[g][r, k] x[g][k, n]: as mode 0 with each x[g] held [K, N]
+ *                (row pitch ldx >= N), the input-gradient products on the row-major weight
+ *                codes; epi 0, 3 or 4; y e5m2.
+ *   mode 3: out_g[o, n] = sum_t y[0][t, o] x[0][t, n] over the rows t of expert g
+ *                (offsets[g] .. offsets[g+1], not padded): the weight gradients on the row-major
+ *                codes (y pitch ldy >= Mo, x pitch ldx >= N); epi 0; y e5m2.
  * y_fmt is the format of y, x_fmt of x (RHP_E4M3 / RHP_E5M2); x must be e4m3.
  * Outputs c[g] (and c2[g]) are bf16 with row pitches ldc (ldc2).
  */
-int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt, int x_fmt, int N,
+int rhp_fp8_gemm(int mode, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt, int x_fmt, int N,
                  int K, int Mo, int f, const void* const* y, int64_t ldy, const void* const* x, int64_t ldx,
                  void* const* c, int64_t ldc, void* const* c2, int64_t ldc2, const void* const* aux, int64_t ldaux,
                  const float* y_scale_inv, const float* x_scale_inv, int x_scale_stride, hipStream_t stream);
 
 /*
- * A row-grouped rhp_fp8_gemm (kgroups = 0) whose epilogue casts its bf16
+ * A row-grouped rhp_fp8_gemm (mode 0, or mode 2 with x_kn = 1) whose epilogue casts its bf16
  * activation output straight to fp8, fusing the cast that the next products
  * need (the quantise step of the fp8 recipe, reference_model.py:204-207, on
  * the expert FFN of moe.py:82-83 and its backward):
@@ -441,7 +461,7 @@ int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets, int64_t ro
  */
 int rhp_fp8_gemm_cast(int epi, int G, const int32_t* offsets, const int32_t* poff, int64_t rows_cap, int y_fmt,
                       int x_fmt, int N, int K, int f, const void* const* y, int64_t ldy, const void* const* x,
-                      int64_t ldx, void* const* c, int64_t ldc, const void* const* aux, int64_t ldaux,
+                      int64_t ldx, int x_kn, void* const* c, int64_t ldc, const void* const* aux, int64_t ldaux,
                       const float* y_scale_inv, const float* x_scale_inv, int x_scale_stride, const float* history,
                       int hist_len, int q_fmt, int margin, uint32_t* amax_bits, float* scale_inv, void* q, void* qt,
                       hipStream_t stream);

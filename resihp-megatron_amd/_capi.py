@@ -23,6 +23,7 @@ _i64 = ctypes.c_int64
 _d = ctypes.c_double
 _sz = ctypes.c_size_t
 _pp = ctypes.POINTER(ctypes.c_void_p)
+_pi64 = ctypes.POINTER(ctypes.c_int64)
 
 # name -> (restype, argtypes); mirrors include/resihp_moe.h
 SIGNATURES: dict[str, tuple[object, list]] = {
@@ -57,11 +58,12 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "rhp_adam_step": (_i, [_i, _pp, _pp, _pp, _pp, _p, _i, _d, _d, _d, _d, _d, _i64, _p]),
     "rhp_fp8_padded_offsets": (_i, [_p, _i, _i, _p, _p]),
     "rhp_fp8_cast": (_i, [_p, _i, _i64, _i, _i, _p, _p, _i64, _p, _i, _i, _i, _p, _p, _p, _p, _p]),
+    "rhp_fp8_cast_many": (_i, [_i, _pp, _pi64, _pi64, _pp, _i, _i, _i, _pp, _pp, _pp, _p]),
     "rhp_fp8_amax_roll": (_i, [_p, _p, _i, _i, _p]),
     "rhp_fp8_gemm": (_i, [_i, _i, _i, _p, _i64, _i, _i, _i, _i, _i, _i, _pp, _i64, _pp, _i64, _pp, _i64, _pp, _i64,
                           _pp, _i64, _p, _p, _i, _p]),
-    "rhp_fp8_gemm_cast": (_i, [_i, _i, _p, _p, _i64, _i, _i, _i, _i, _i, _pp, _i64, _pp, _i64, _pp, _i64, _pp, _i64,
-                               _p, _p, _i, _p, _i, _i, _i, _p, _p, _p, _p, _p]),
+    "rhp_fp8_gemm_cast": (_i, [_i, _i, _p, _p, _i64, _i, _i, _i, _i, _i, _pp, _i64, _pp, _i64, _i, _pp, _i64, _pp,
+                               _i64, _p, _p, _i, _p, _i, _i, _i, _p, _p, _p, _p, _p]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -168,6 +168,83 @@ __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
     }
 }
 
+// Many whole tensors (the expert weights) in one launch, each with its own
+// delayed scale, row-major codes only: block b takes 128 rows x 128 columns
+// of tensor i, the tensor whose block range holds b (ranges in the kernel
+// arguments).  The loads, the quantisation and the stores are those of
+// fp8_cast_kernel, so the codes, amax and 1 / scale are the same bits.
+constexpr int kCastMany = 32;   // tensors per launch
+
+struct CastManyParams {
+    struct Tensor {
+        const uint16_t* x;   // bf16 [rows][cols]
+        uint8_t* q;          // fp8 [rows][cols]
+        const float* hist;   // [L]
+        uint32_t* amax_bits;
+        float* scale_inv;
+        int rows, cols;
+        uint32_t block0;     // first block of the tensor
+    } t[kCastMany];
+    int n, L, margin;
+    uint32_t blocks;
+};
+
+template <int FMT>
+__global__ __launch_bounds__(256) void fp8_cast_many_kernel(CastManyParams c) {
+    __shared__ float wave_max[4];
+    const uint32_t b = blockIdx.x;
+    int i = 0;
+    while (i + 1 < c.n && b >= c.t[i + 1].block0) ++i;
+    const CastManyParams::Tensor& T = c.t[i];
+    const int ct_n = (T.cols + kCastCols - 1) / kCastCols;
+    const uint32_t local = b - T.block0;
+    const int rt = static_cast<int>(local / ct_n), ct = static_cast<int>(local % ct_n);
+    const float scale = history_scale(T.hist, c.L, fp8_max(FMT), c.margin);
+    if (local == 0 && threadIdx.x == 0) *T.scale_inv = 1.0f / scale;
+
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int col = ct * kCastCols + 8 * (lane & 15);
+    const bool col_ok = col < T.cols;
+    const int r0 = 32 * w + (lane >> 4);
+    const float lim = fp8_max(FMT);
+    float m = 0.0f;
+    uint4 u[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int row = rt * kCastRows + r0 + 4 * k;
+        u[k] = make_uint4(0u, 0u, 0u, 0u);
+        if (col_ok && row < T.rows) u[k] = *reinterpret_cast<const uint4*>(T.x + static_cast<int64_t>(row) * T.cols + col);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t wd[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = __uint_as_float(wd[e] << 16);
+            v[2 * e + 1] = __uint_as_float(wd[e] & 0xffff0000u);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            m = fmaxf(m, fabsf(v[e]));
+            v[e] = fminf(fmaxf(v[e] * scale, -lim), lim);
+        }
+        const int row = rt * kCastRows + r0 + 4 * k;
+        if (col_ok && row < T.rows)
+            *reinterpret_cast<uint2*>(T.q + static_cast<int64_t>(row) * T.cols + col) =
+                make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7]));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) wave_max[w] = m;
+    __syncthreads();
+    if (t == 0) {
+        const float bm = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+        const uint32_t seen = __hip_atomic_load(T.amax_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (bm > 0.0f && __float_as_uint(bm) > seen) atomicMax(T.amax_bits, __float_as_uint(bm));
+    }
+}
+
 // poff[g + 1] = poff[g] + roundup(offsets[g + 1] - offsets[g], align)
 __global__ void fp8_pad_offsets_kernel(const int32_t* offsets, int G, int align, int32_t* poff) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
@@ -215,6 +292,7 @@ static_assert(kF8LdsBytes <= 163840, "five 32 KB slots");
 constexpr uint32_t kF8PastView = 0x7ffffff0u;   // soffset that puts every lane past its buffer view
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int v2i32_t __attribute__((ext_vector_type(2)));
 
 struct F8Map {
     uint32_t vo[kF8PerWave];
@@ -234,6 +312,48 @@ __device__ __forceinline__ void f8_map(F8Map& m, uint32_t ld, int frag_row0, int
     for (int i = 0; i < 4; ++i) m.fr[i] = i < nfrag ? k64_off(frag_row0 + i * 32 + (L & 31), 2 * (L >> 5)) : 0;
 }
 
+// N-contiguous ("MN-major") operand tiles: 128 k rows of 256 mn bytes (32 KB),
+// 16-byte chunk c of k row r at position c ^ (r & 7), so that the eight k rows
+// one transposing read covers fall in eight distinct bank groups.  One direct
+// load fills four k rows: lane L takes row L / 16 of them and position L % 16,
+// i.e. source chunk (L % 16) ^ (row & 7).  vo[j] holds the lane's byte offset
+// from the operand's row 0 and column mn0 without the step's k; chunks past
+// mn_lim read zero.
+__device__ __forceinline__ void f8_map_mn(F8Map& m, uint32_t ld, int mn0, int mn_lim, int frag_mn0, int nfrag) {
+    const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < kF8PerWave; ++j) {
+        const int r = (j * kWaves + w) * 4 + (L >> 4);
+        const int c = (L & 15) ^ (r & 7);
+        m.vo[j] = c * 16 < mn_lim ? static_cast<uint32_t>(r) * ld + static_cast<uint32_t>(mn0 + c * 16) : kOutOfRange;
+    }
+    // Fragment reads (ds_read_b64_tr_b8): in each 16-lane group, lane j points at k row base + j / 2,
+    // bytes 8 (j % 2) .. +7 of the group's 16 mn columns, and receives k rows base .. base + 7 of
+    // column (j of the group).  Group G covers mn 16 (G % 2) .. +15 and k 32 (G / 2) .. +31 in four
+    // reads (k + 8 q), so lane L holds row L % 32 and k 32 (L / 32) .. +31, as the K-major fragments do.
+    const int G = L >> 4, j = L & 15;
+    const int kr = 32 * (G >> 1) + (j >> 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int mn = frag_mn0 + i * 32 + 16 * (G & 1);
+        m.fr[i] = i < nfrag ? static_cast<uint32_t>(kr * 256 + (((mn >> 4) ^ (kr & 7)) << 4) + 8 * (j & 1)) : 0;
+    }
+}
+
+// The fragment of k64 block b of an MN-major tile: four transposing reads, k + 8 q.
+__device__ __forceinline__ i32x8_t f8_frag_mn(const uint8_t* tile, uint32_t fr, int b) {
+    typedef v2i32_t __attribute__((address_space(3))) * lds_v2;
+    i32x8_t v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint8_t* p = tile + fr + (64 * b + 8 * q) * 256;
+        const v2i32_t r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_v2>(reinterpret_cast<uintptr_t>(p)));
+        v[2 * q] = r[0];
+        v[2 * q + 1] = r[1];
+    }
+    return v;
+}
+
 __device__ __forceinline__ i32x8_t f8_frag(const uint8_t* tile, uint32_t fr, int b) {
     const uint32_t o = fr ^ static_cast<uint32_t>(b << 6);
     const uint4 lo = *reinterpret_cast<const uint4*>(tile + o);
@@ -244,8 +364,16 @@ __device__ __forceinline__ i32x8_t f8_frag(const uint8_t* tile, uint32_t fr, int
     return v;
 }
 
-template <int MODE, int EPI, int YF, int XF, int QF>
+// MN: operands read from N-contiguous rows with transposing fragment reads
+// (bit 0: X, bit 1: Y).  MN = 1 with row-grouped products: X is a weight held
+// [K, N] (the input-gradient products on the row-major weight codes); MN = 3
+// with K-grouped products: both operands are row-major codes [rows, Mo] and
+// [rows, N], group g's rows from offsets[g] (the weight gradients on the
+// row-major activation and gradient codes).
+template <int MODE, int EPI, int YF, int XF, int QF, int MN = 0>
 __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
+    constexpr bool kXMN = (MN & 1) != 0, kYMN = (MN & 2) != 0;
+    static_assert(MN == 0 || (MODE == kFwd && MN == 1) || (MODE == kWgrad && MN == 3), "MN-major layouts");
     __shared__ __align__(1024) uint8_t lds[kF8LdsBytes];
     if constexpr (QF >= 0) {
         // The quantising epilogue's 1 / scale, written once (block 0 exists in every launch).
@@ -271,7 +399,19 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
     Rsrc rx, ry;
     F8Map mx, my;
     const int y_last = t.y_lim - 1;
-    if (MODE == kWgrad) {
+    uint32_t xstep = 0, ystep = 0;   // bytes per k of the MN-major operands
+    if (MODE == kWgrad && MN == 3) {
+        // Row-major codes: the group's rows through views of the group's rows (rows past its count read zero).
+        const uint32_t lda = static_cast<uint32_t>(p.lda), ldb = static_cast<uint32_t>(p.ldb);
+        const uint8_t* Y = static_cast<const uint8_t*>(p.a[0]) + static_cast<int64_t>(t.row0) * p.lda;
+        const uint8_t* X = static_cast<const uint8_t*>(p.b[0]) + static_cast<int64_t>(t.row0) * p.ldb;
+        ry = make_dma_rsrc(Y, static_cast<int64_t>(t.k_end) * p.lda);
+        rx = make_dma_rsrc(X, static_cast<int64_t>(t.k_end) * p.ldb);
+        f8_map_mn(my, lda, t.y0, t.y_lim, wy * kWaveY, kFragY);
+        f8_map_mn(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
+        ystep = lda;
+        xstep = ldb;
+    } else if (MODE == kWgrad) {
         const uint32_t ld = static_cast<uint32_t>(t.k_end);   // R_g
         const uint8_t* Y = static_cast<const uint8_t*>(p.a[0]) + static_cast<int64_t>(p.Mo) * t.row0;
         const uint8_t* X = static_cast<const uint8_t*>(p.b[0]) + static_cast<int64_t>(p.N) * t.row0;
@@ -286,8 +426,14 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
         const uint8_t* X = static_cast<const uint8_t*>(p.b[g]);
         const uint32_t lda = static_cast<uint32_t>(p.lda), ldb = static_cast<uint32_t>(p.ldb);
         ry = make_dma_rsrc(Y + (t.row0 + t.y0) * p.lda, static_cast<int64_t>(t.y_lim) * p.lda);
-        rx = make_dma_rsrc(X, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb);
         f8_map(my, lda, wy * kWaveY, kFragY, [&](int r) { return r < t.y_lim ? r : y_last; });
+        if constexpr (kXMN) {
+            // The weight held [K, N]: k rows of N bytes.
+            rx = make_dma_rsrc(X, static_cast<int64_t>(p.K) * p.ldb);
+            f8_map_mn(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
+            xstep = ldb;
+        } else {
+        rx = make_dma_rsrc(X, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb);
         f8_map(mx, ldb, wx * 128, 4, [&](int r) {
             if (EPI == kEpiSwigluFwd) {
                 // 256 weight rows = [gate 64 | up 64] for each half of 128 activation columns.
@@ -299,19 +445,22 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
             const int n = t.x0 + r;
             return n < p.N ? n : 0;
         });
+        }
     }
 
     const int nk = (t.k_end - t.k_begin + kF8K - 1) / kF8K;
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
     // X (Y) tile of step `step` into slot `slot`; past the last step, zeros.
     auto issue_x = [&](int step, int slot) {
-        const uint32_t soff = step < nk ? static_cast<uint32_t>(t.k_begin + step * kF8K) : kF8PastView;
+        const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kF8K);
+        const uint32_t soff = step < nk ? (kXMN ? k0 * xstep : k0) : kF8PastView;
         const uint32_t base = lds0 + slot * kF8TileBytes + wave * 1024;
 #pragma unroll
         for (int j = 0; j < kF8PerWave; ++j) dma16(rx, mx.vo[j], soff, base + j * kWaves * 1024);
     };
     auto issue_y = [&](int step, int slot) {
-        const uint32_t soff = step < nk ? static_cast<uint32_t>(t.k_begin + step * kF8K) : kF8PastView;
+        const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kF8K);
+        const uint32_t soff = step < nk ? (kYMN ? k0 * ystep : k0) : kF8PastView;
         const uint32_t base = lds0 + slot * kF8TileBytes + wave * 1024;
 #pragma unroll
         for (int j = 0; j < kF8PerWave; ++j) dma16(ry, my.vo[j], soff, base + j * kWaves * 1024);
@@ -340,9 +489,9 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
         const uint8_t* xt = lds + sx;
         const uint8_t* yt = lds + sy;
 #pragma unroll
-        for (int j = 0; j < kFragY; ++j) f[4 + j] = f8_frag(yt, my.fr[j], b);
+        for (int j = 0; j < kFragY; ++j) f[4 + j] = kYMN ? f8_frag_mn(yt, my.fr[j], b) : f8_frag(yt, my.fr[j], b);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = f8_frag(xt, mx.fr[i], b);
+        for (int i = 0; i < 4; ++i) f[i] = kXMN ? f8_frag_mn(xt, mx.fr[i], b) : f8_frag(xt, mx.fr[i], b);
     };
     auto mfmas = [&](const FragSet& f) {
 #pragma unroll
@@ -352,7 +501,7 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
                 acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[i], f[4 + j], acc[i][j], XF, YF, 0, 127,
                                                                            0, 127);
     };
-    constexpr int kReads = 2 * (4 + kFragY);
+    constexpr int kReads = (kXMN ? 4 : 2) * 4 + (kYMN ? 4 : 2) * kFragY;   // LDS reads of a block's fragments
     using Pending = std::integral_constant<int, kF8PerWave>;   // one operand tile stays in flight
     using Prolog = std::integral_constant<int, 3 * kF8PerWave>;
 
@@ -401,15 +550,24 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
     epilogue<MODE, EPI, kThreadsMfma, kWaveY, QF>(p, t, lds, acc, wx, wy, lane, mul);
 }
 
-template <int MODE, int EPI, int YF, int XF, int QF = -1>
+template <int MODE, int EPI, int YF, int XF, int QF = -1, int MN = 0>
 void launch_fp8(const Params& p, unsigned nb, hipStream_t s) {
-    hipLaunchKernelGGL((gg_fp8_kernel<MODE, EPI, YF, XF, QF>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
+    hipLaunchKernelGGL((gg_fp8_kernel<MODE, EPI, YF, XF, QF, MN>), dim3(nb), dim3(kThreadsMfma), 0, s, p);
 }
 
 // The quantising combinations: activations cast to e4m3 in the forward,
 // pre-activation gradients to e5m2 in the backward.
-bool launch_fp8_quant(int epi, int yf, int xf, int qf, const Params& p, unsigned nb, hipStream_t s) {
+bool launch_fp8_quant(int epi, int yf, int xf, int qf, bool x_kn, const Params& p, unsigned nb, hipStream_t s) {
     if (xf != kFmtE4m3) return false;
+    if (x_kn) {
+        if (epi == kEpiSwigluBwd && yf == kFmtE5m2 && qf == kFmtE5m2)
+            launch_fp8<kFwd, kEpiSwigluBwd, kFmtE5m2, kFmtE4m3, kFmtE5m2, 1>(p, nb, s);
+        else if (epi == kEpiGeluBwd && yf == kFmtE5m2 && qf == kFmtE5m2)
+            launch_fp8<kFwd, kEpiGeluBwd, kFmtE5m2, kFmtE4m3, kFmtE5m2, 1>(p, nb, s);
+        else
+            return false;
+        return true;
+    }
     if (epi == kEpiSwigluFwd && yf == kFmtE4m3 && qf == kFmtE4m3) {
         launch_fp8<kFwd, kEpiSwigluFwd, kFmtE4m3, kFmtE4m3, kFmtE4m3>(p, nb, s);
     } else if (epi == kEpiGeluFwd && yf == kFmtE4m3 && qf == kFmtE4m3) {
@@ -438,6 +596,17 @@ bool launch_fp8_any(int mode, int epi, int yf, int xf, const Params& p, unsigned
         case (kWgrad * 8 + kEpiStore) * 2 + kFmtE5m2: launch_fp8<kWgrad, kEpiStore, kFmtE5m2, kFmtE4m3>(p, nb, s); return true;
         default: return false;
     }
+}
+
+// Products on N-contiguous operands: mode 2 (row-grouped, x held [K, N]), mode 3 (K-grouped, row-major codes).
+bool launch_fp8_mn(int mode, int epi, int yf, int xf, const Params& p, unsigned nb, hipStream_t s) {
+    if (xf != kFmtE4m3 || yf != kFmtE5m2) return false;
+    if (mode == 2 && epi == kEpiStore) launch_fp8<kFwd, kEpiStore, kFmtE5m2, kFmtE4m3, -1, 1>(p, nb, s);
+    else if (mode == 2 && epi == kEpiSwigluBwd) launch_fp8<kFwd, kEpiSwigluBwd, kFmtE5m2, kFmtE4m3, -1, 1>(p, nb, s);
+    else if (mode == 2 && epi == kEpiGeluBwd) launch_fp8<kFwd, kEpiGeluBwd, kFmtE5m2, kFmtE4m3, -1, 1>(p, nb, s);
+    else if (mode == 3 && epi == kEpiStore) launch_fp8<kWgrad, kEpiStore, kFmtE5m2, kFmtE4m3, -1, 3>(p, nb, s);
+    else return false;
+    return true;
 }
 
 int fp8_fmt(int dtype) { return dtype == RHP_E4M3 ? kFmtE4m3 : dtype == RHP_E5M2 ? kFmtE5m2 : -1; }
@@ -497,6 +666,52 @@ extern "C" int rhp_fp8_cast(const void* x, int x_dtype, int64_t ldx, int cols, i
     return check_launch("rhp_fp8_cast");
 }
 
+extern "C" int rhp_fp8_cast_many(int n, const void* const* x, const int64_t* rows, const int64_t* cols,
+                                 const float* const* history, int hist_len, int fmt, int margin,
+                                 uint32_t* const* amax_bits, float* const* scale_inv, void* const* q,
+                                 hipStream_t stream) {
+    clear_error();
+    const int f8 = fp8_fmt(fmt);
+    RHP_REQUIRE(f8 >= 0, "rhp_fp8_cast_many: format must be RHP_E4M3 or RHP_E5M2");
+    RHP_REQUIRE(n >= 0 && (n == 0 || (x && rows && cols && history && amax_bits && scale_inv && q)),
+                "rhp_fp8_cast_many: null pointer");
+    RHP_REQUIRE(hist_len >= 1 && margin >= 0 && margin < 64, "rhp_fp8_cast_many: bad history or margin");
+    for (int i0 = 0; i0 < n; i0 += kCastMany) {
+        CastManyParams c{};
+        c.n = std::min(kCastMany, n - i0);
+        c.L = hist_len;
+        c.margin = margin;
+        int64_t blocks = 0;
+        for (int j = 0; j < c.n; ++j) {
+            const int i = i0 + j;
+            RHP_REQUIRE(history[i] && amax_bits[i] && scale_inv[i] &&
+                            (rows[i] == 0 || (x[i] && q[i] && aligned16(x[i]) && aligned16(q[i]))),
+                        "rhp_fp8_cast_many: null or unaligned tensor");
+            RHP_REQUIRE(rows[i] >= 0 && rows[i] < (int64_t(1) << 31) && cols[i] > 0 && cols[i] % 64 == 0 &&
+                            cols[i] < (int64_t(1) << 31),
+                        "rhp_fp8_cast_many: cols must be a positive multiple of 64 and rows in range");
+            c.t[j].x = static_cast<const uint16_t*>(x[i]);
+            c.t[j].q = static_cast<uint8_t*>(q[i]);
+            c.t[j].hist = history[i];
+            c.t[j].amax_bits = amax_bits[i];
+            c.t[j].scale_inv = scale_inv[i];
+            c.t[j].rows = static_cast<int>(rows[i]);
+            c.t[j].cols = static_cast<int>(cols[i]);
+            c.t[j].block0 = static_cast<uint32_t>(blocks);
+            // At least one block a tensor, so that an empty tensor still gets its 1 / scale.
+            blocks += std::max<int64_t>(1, (rows[i] + kCastRows - 1) / kCastRows) * ((cols[i] + kCastCols - 1) / kCastCols);
+            RHP_REQUIRE(blocks < (int64_t(1) << 31), "rhp_fp8_cast_many: too many tiles");
+        }
+        if (blocks == 0) continue;
+        if (f8 == kFmtE4m3)
+            hipLaunchKernelGGL(fp8_cast_many_kernel<kFmtE4m3>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, c);
+        else
+            hipLaunchKernelGGL(fp8_cast_many_kernel<kFmtE5m2>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, c);
+        if (int rc = check_launch("rhp_fp8_cast_many")) return rc;
+    }
+    return 0;
+}
+
 extern "C" int rhp_fp8_amax_roll(float* history, uint32_t* amax_bits, int n, int hist_len, hipStream_t stream) {
     clear_error();
     RHP_REQUIRE(history && amax_bits, "rhp_fp8_amax_roll: null pointer");
@@ -518,12 +733,15 @@ struct CastOut {
     uint8_t* qt;
 };
 
-int fp8_gemm_run(int kgroups, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt, int x_fmt, int N,
+int fp8_gemm_run(int mode, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt, int x_fmt, int N,
                  int K, int Mo, int f, const void* const* y, int64_t ldy, const void* const* x, int64_t ldx,
                  void* const* c, int64_t ldc, void* const* c2, int64_t ldc2, const void* const* aux, int64_t ldaux,
                  const float* y_scale_inv, const float* x_scale_inv, int x_scale_stride, const CastOut* cast,
                  hipStream_t stream) {
     const int yf = fp8_fmt(y_fmt), xf = fp8_fmt(x_fmt);
+    RHP_REQUIRE(mode >= 0 && mode <= 3, "rhp_fp8_gemm: mode must be 0 to 3");
+    RHP_REQUIRE(!cast || mode == 0 || mode == 2, "rhp_fp8_gemm_cast: row-grouped products only");
+    const bool kgroups = mode == 1 || mode == 3, x_kn = mode == 2;
     RHP_REQUIRE(yf >= 0 && xf >= 0, "rhp_fp8_gemm: operand formats must be RHP_E4M3 or RHP_E5M2");
     RHP_REQUIRE(G >= 1 && G <= RHP_MAX_GROUPS_PER_LAUNCH, "rhp_fp8_gemm: 1 to 64 groups per call");
     RHP_REQUIRE(offsets && y && x && (c || cast) && y_scale_inv && x_scale_inv, "rhp_fp8_gemm: null pointer");
@@ -534,7 +752,7 @@ int fp8_gemm_run(int kgroups, int epi, int G, const int32_t* offsets, int64_t ro
     // The epilogue writes (and reads aux) through views of kTile rows with 32-bit byte offsets.
     RHP_REQUIRE(std::max({ldc, ldc2, ldaux}) * 2 * kTile < (int64_t(1) << 31),
                 "rhp_fp8_gemm: output, activation and pre-activation rows must be narrower than 2^22 elements");
-    const int mode = kgroups ? kWgrad : kFwd;
+    const int kmode = kgroups ? kWgrad : kFwd;
     Params p{};
     const int ng = kgroups ? 1 : G;
     for (int g = 0; g < ng; ++g) {
@@ -548,12 +766,28 @@ int fp8_gemm_run(int kgroups, int epi, int G, const int32_t* offsets, int64_t ro
         p.c2[g] = c2 ? c2[g] : nullptr;
         p.aux[g] = aux ? aux[g] : nullptr;
     }
-    if (kgroups) {
+    if (mode == 3) {
+        RHP_REQUIRE(epi == kEpiStore, "rhp_fp8_gemm: K-grouped products store plain outputs");
+        RHP_REQUIRE(Mo > 0 && Mo % 64 == 0, "rhp_fp8_gemm: Mo must be a positive multiple of 64");
+        RHP_REQUIRE(ldy >= Mo && ldy % 16 == 0 && ldx >= N && ldx % 16 == 0, "rhp_fp8_gemm: bad row pitches");
+        // Each tile reads its group's rows of both operands through views of those rows.
+        RHP_REQUIRE((rows_cap + 1) * std::max(ldy, ldx) < (int64_t(1) << 31),
+                    "rhp_fp8_gemm: a group's rows of either operand must stay below 2 GiB");
+    } else if (kgroups) {
         RHP_REQUIRE(epi == kEpiStore, "rhp_fp8_gemm: K-grouped products store plain outputs");
         RHP_REQUIRE(Mo > 0 && Mo % 64 == 0, "rhp_fp8_gemm: Mo must be a positive multiple of 64");
         // Each tile reads 256 rows of an expert's transposed copies through its own view.
         RHP_REQUIRE((kTile + 1) * (rows_cap + 128) < (int64_t(1) << 31),
                     "rhp_fp8_gemm: an expert's padded rows must stay below 2^23");
+    } else if (x_kn) {
+        RHP_REQUIRE(K > 0 && K % kF8K == 0, "rhp_fp8_gemm: K must be a positive multiple of 128");
+        RHP_REQUIRE(ldy >= K && ldy % 16 == 0 && ldx >= N && ldx % 16 == 0, "rhp_fp8_gemm: bad row pitches");
+        RHP_REQUIRE(epi == kEpiStore || epi == kEpiSwigluBwd || epi == kEpiGeluBwd,
+                    "rhp_fp8_gemm: products on [K, N] weights take the store or activation-backward epilogues");
+        RHP_REQUIRE(kTile * ldy < (int64_t(1) << 31) && (K + 1) * ldx < (int64_t(1) << 31),
+                    "rhp_fp8_gemm: weights must stay below 2 GiB");
+        if (epi == kEpiSwigluBwd || epi == kEpiGeluBwd) RHP_REQUIRE(aux != nullptr, "rhp_fp8_gemm: pre-activation input missing");
+        if (epi == kEpiSwigluBwd) RHP_REQUIRE(f == N && f % 64 == 0, "rhp_fp8_gemm: SwiGLU needs N == f");
     } else {
         RHP_REQUIRE(K > 0 && K % kF8K == 0, "rhp_fp8_gemm: K must be a positive multiple of 128");
         RHP_REQUIRE(ldy >= K && ldy % 16 == 0 && ldx >= K && ldx % 16 == 0, "rhp_fp8_gemm: bad row pitches");
@@ -578,7 +812,7 @@ int fp8_gemm_run(int kgroups, int epi, int G, const int32_t* offsets, int64_t ro
     p.ldc2 = static_cast<int>(ldc2);
     p.ldaux = static_cast<int>(ldaux);
     p.f = f;
-    p.rows_cap = static_cast<int>(kgroups ? rows_cap + 128 * int64_t(G) : rows_cap);
+    p.rows_cap = static_cast<int>(mode == 1 ? rows_cap + 128 * int64_t(G) : rows_cap);
     p.scale_inv_y = y_scale_inv;
     p.scale_inv_x = x_scale_inv;
     p.scale_x_stride = x_scale_stride;
@@ -595,30 +829,35 @@ int fp8_gemm_run(int kgroups, int epi, int G, const int32_t* offsets, int64_t ro
         p.q_ld = epi == kEpiSwigluBwd ? 2 * N : N;
         p.q_L = cast->hist_len;
         p.q_margin = cast->margin;
-        RHP_REQUIRE(launch_fp8_quant(epi, yf, xf, fp8_fmt(cast->fmt), p, static_cast<unsigned>(nb), stream),
+        RHP_REQUIRE(launch_fp8_quant(epi, yf, xf, fp8_fmt(cast->fmt), x_kn, p, static_cast<unsigned>(nb), stream),
                     "rhp_fp8_gemm_cast: unsupported combination of epilogue and formats");
         return check_launch("rhp_fp8_gemm_cast");
     }
-    RHP_REQUIRE(launch_fp8_any(mode, epi, yf, xf, p, static_cast<unsigned>(nb), stream),
+    if (mode >= 2) {
+        RHP_REQUIRE(launch_fp8_mn(mode, epi, yf, xf, p, static_cast<unsigned>(nb), stream),
+                    "rhp_fp8_gemm: products on N-contiguous operands take e5m2 y and e4m3 x");
+        return check_launch("rhp_fp8_gemm");
+    }
+    RHP_REQUIRE(launch_fp8_any(kmode, epi, yf, xf, p, static_cast<unsigned>(nb), stream),
                 "rhp_fp8_gemm: unsupported combination of product, epilogue and formats");
     return check_launch("rhp_fp8_gemm");
 }
 
 }  // namespace
 
-extern "C" int rhp_fp8_gemm(int kgroups, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt,
+extern "C" int rhp_fp8_gemm(int mode, int epi, int G, const int32_t* offsets, int64_t rows_cap, int y_fmt,
                             int x_fmt, int N, int K, int Mo, int f, const void* const* y, int64_t ldy,
                             const void* const* x, int64_t ldx, void* const* c, int64_t ldc, void* const* c2,
                             int64_t ldc2, const void* const* aux, int64_t ldaux, const float* y_scale_inv,
                             const float* x_scale_inv, int x_scale_stride, hipStream_t stream) {
     clear_error();
-    return fp8_gemm_run(kgroups, epi, G, offsets, rows_cap, y_fmt, x_fmt, N, K, Mo, f, y, ldy, x, ldx, c, ldc, c2,
+    return fp8_gemm_run(mode, epi, G, offsets, rows_cap, y_fmt, x_fmt, N, K, Mo, f, y, ldy, x, ldx, c, ldc, c2,
                         ldc2, aux, ldaux, y_scale_inv, x_scale_inv, x_scale_stride, nullptr, stream);
 }
 
 extern "C" int rhp_fp8_gemm_cast(int epi, int G, const int32_t* offsets, const int32_t* poff, int64_t rows_cap,
                                  int y_fmt, int x_fmt, int N, int K, int f, const void* const* y, int64_t ldy,
-                                 const void* const* x, int64_t ldx, void* const* c, int64_t ldc,
+                                 const void* const* x, int64_t ldx, int x_kn, void* const* c, int64_t ldc,
                                  const void* const* aux, int64_t ldaux, const float* y_scale_inv,
                                  const float* x_scale_inv, int x_scale_stride, const float* history, int hist_len,
                                  int q_fmt, int margin, uint32_t* amax_bits, float* scale_inv, void* q, void* qt,
@@ -640,6 +879,8 @@ extern "C" int rhp_fp8_gemm_cast(int epi, int G, const int32_t* offsets, const i
     RHP_REQUIRE(rows_cap >= 0 && kTile * cols < (int64_t(1) << 31), "rhp_fp8_gemm_cast: N out of range");
     const CastOut cast{poff, history, hist_len, q_fmt, margin, amax_bits, scale_inv, static_cast<uint8_t*>(q),
                        static_cast<uint8_t*>(qt)};
-    return fp8_gemm_run(0, epi, G, offsets, rows_cap, y_fmt, x_fmt, N, K, 0, f, y, ldy, x, ldx, c, ldc, nullptr, 0,
-                        aux, ldaux, y_scale_inv, x_scale_inv, x_scale_stride, &cast, stream);
+    RHP_REQUIRE(x_kn == 0 || x_kn == 1, "rhp_fp8_gemm_cast: x_kn must be 0 or 1");
+    RHP_REQUIRE(!x_kn || !fwd, "rhp_fp8_gemm_cast: [K, N] weights only with the backward epilogues");
+    return fp8_gemm_run(x_kn ? 2 : 0, epi, G, offsets, rows_cap, y_fmt, x_fmt, N, K, 0, f, y, ldy, x, ldx, c, ldc,
+                        nullptr, 0, aux, ldaux, y_scale_inv, x_scale_inv, x_scale_stride, &cast, stream);
 }

@@ -124,23 +124,42 @@ class Fp8State:
              row_major: bool = True, transposed: bool = True) -> tuple[torch.Tensor | None, torch.Tensor | None]:
         """Casts rows of ``x`` with tensor i's scale; returns (row-major fp8, per-expert transposed fp8)."""
         rows, cols = x.shape
+        if row_major and not transposed and rows == rows_cap and x.is_contiguous():
+            # Row-major codes of the whole buffer: one scale for every expert's rows, so the grouping plays
+            # no part and the whole-tensor cast (no transposition stage) does it.
+            q = torch.empty(rows, cols, dtype=K.FP8_FORMATS[FORMATS.get(i, "e4m3")][1], device=x.device)
+            K.fp8_cast_many([x], [self.history[i]], FORMATS.get(i, "e4m3"), [self.amax[i:i + 1]],
+                            [self.scale_inv[i:i + 1]], [q], self.margin)
+            return q, None
         q, qt = self.codes(i, rows, cols, rows_cap, offsets.numel() - 1, x.device, row_major, transposed)
         K.fp8_cast(x, offsets, poff, rows_cap, self.history[i], FORMATS.get(i, "e4m3"), self.amax[i:i + 1],
                    self.scale_inv[i:i + 1], q, qt, self.margin)
         return q, qt
 
+    def cast_weights(self, fc1s: list[torch.Tensor], fc2s: list[torch.Tensor]) -> tuple[list, list]:
+        """Row-major e4m3 codes of every local expert's two weights, each with its own scale, in one launch."""
+        ws = list(fc1s) + list(fc2s)
+        rows = [self.w1(g) for g in range(self.G)] + [self.w2(g) for g in range(self.G)]
+        fdt = K.FP8_FORMATS["e4m3"][1]
+        qs = [torch.empty(w.shape, dtype=fdt, device=w.device) for w in ws]
+        K.fp8_cast_many(ws, [self.history[i] for i in rows], "e4m3", [self.amax[i:i + 1] for i in rows],
+                        [self.scale_inv[i:i + 1] for i in rows], qs, self.margin)
+        return qs[:self.G], qs[self.G:]
+
     def gemm_cast(self, i: int, epi: str, offsets: torch.Tensor, poff: torch.Tensor, rows_cap: int,
                   ys: list[torch.Tensor], y_fmt: str, xs: list[torch.Tensor], N: int, K_: int, f: int,
                   y_scale_inv: torch.Tensor, x_scale_inv: torch.Tensor, cs: list[torch.Tensor] | None = None,
-                  auxs: list[torch.Tensor] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                  auxs: list[torch.Tensor] | None = None, transposed: bool = True,
+                  x_kn: bool = False) -> tuple[torch.Tensor, torch.Tensor | None]:
         """An fp8 product whose epilogue casts its activation output as tensor i (``K.fp8_gemm_cast``).
 
-        Returns the (row-major, per-expert transposed) codes, equal to those of the product's bf16 output
-        cast with ``cast``.
+        Returns the (row-major, per-expert transposed or None) codes, equal to those of the product's bf16
+        output cast with ``cast``.  ``x_kn``: the weights are the row-major codes held [K, N].
         """
         cols = 2 * N if epi == "swiglu_bwd" else N
-        q, qt = self.codes(i, ys[0].shape[0], cols, rows_cap, offsets.numel() - 1, ys[0].device)
+        q, qt = self.codes(i, ys[0].shape[0], cols, rows_cap, offsets.numel() - 1, ys[0].device,
+                           transposed=transposed)
         K.fp8_gemm_cast(epi, offsets, poff, rows_cap, ys, y_fmt, xs, "e4m3", N, K_, f, y_scale_inv, x_scale_inv,
                         self.history[i], FORMATS.get(i, "e4m3"), self.amax[i:i + 1], self.scale_inv[i:i + 1], q, qt,
-                        cs=cs, auxs=auxs, margin=self.margin)
+                        cs=cs, auxs=auxs, margin=self.margin, x_kn=x_kn)
         return q, qt

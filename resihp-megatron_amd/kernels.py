@@ -636,6 +636,30 @@ def fp8_cast(x: torch.Tensor, offsets: torch.Tensor, poff: torch.Tensor, rows_ca
           history.numel(), code, margin, _ptr(amax_bits), _ptr(scale_inv), _ptr(q), _ptr(qt))
 
 
+def fp8_cast_many(xs: list[torch.Tensor], histories: list[torch.Tensor], fmt: str, amax_bits: list[torch.Tensor],
+                  scale_invs: list[torch.Tensor], qs: list[torch.Tensor], margin: int = 0) -> None:
+    """fp8_cast of whole tensors in one launch (row-major codes only), each with its own scale state."""
+    n = len(xs)
+    _expect(len(histories) == n and len(amax_bits) == n and len(scale_invs) == n and len(qs) == n,
+            "one history, amax, scale and code buffer per tensor")
+    if n == 0:
+        return
+    dev = _need_cuda(*xs, *histories, *amax_bits, *scale_invs, *qs)
+    code, fdt, _ = FP8_FORMATS[fmt]
+    L = histories[0].numel()
+    for x, hst, a, si, q in zip(xs, histories, amax_bits, scale_invs, qs):
+        _expect(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous() and x.shape[1] % 64 == 0,
+                "tensors must be contiguous bf16 [rows, cols], cols a multiple of 64")
+        _expect(q.dtype == fdt and tuple(q.shape) == tuple(x.shape) and q.is_contiguous(), f"codes must be {fdt} like x")
+        _expect(hst.dtype == torch.float32 and hst.numel() == L, f"histories must be float32 [{L}]")
+        _expect(a.dtype == torch.int32 and a.numel() == 1 and si.dtype == torch.float32 and si.numel() == 1,
+                "amax int32 [1] and 1/scale float32 [1] per tensor")
+    rows = (ctypes.c_int64 * n)(*[x.shape[0] for x in xs])
+    cols = (ctypes.c_int64 * n)(*[x.shape[1] for x in xs])
+    _call("rhp_fp8_cast_many", dev, n, _arr(xs), rows, cols, _arr(histories), L, code, margin, _arr(amax_bits),
+          _arr(scale_invs), _arr(qs))
+
+
 def fp8_amax_roll(history: torch.Tensor, amax_bits: torch.Tensor) -> None:
     """End of iteration: every history gets its pending amax prepended (newest first); the amax resets."""
     dev = _need_cuda(history, amax_bits)
@@ -644,11 +668,16 @@ def fp8_amax_roll(history: torch.Tensor, amax_bits: torch.Tensor) -> None:
     _call("rhp_fp8_amax_roll", dev, _ptr(history), _ptr(amax_bits), history.shape[0], history.shape[1])
 
 
-def fp8_gemm(kgroups: bool, epi: str, offsets: torch.Tensor, rows_cap: int, ys: list[torch.Tensor], y_fmt: str,
+def fp8_gemm(mode: int | bool, epi: str, offsets: torch.Tensor, rows_cap: int, ys: list[torch.Tensor], y_fmt: str,
              xs: list[torch.Tensor], x_fmt: str, N: int, K: int, Mo: int, f: int, cs: list[torch.Tensor],
              y_scale_inv: torch.Tensor, x_scale_inv: torch.Tensor, c2s: list[torch.Tensor] | None = None,
              auxs: list[torch.Tensor] | None = None) -> None:
-    """Grouped fp8 product with bf16 outputs (see rhp_fp8_gemm in include/resihp_moe.h)."""
+    """Grouped fp8 product with bf16 outputs (rhp_fp8_gemm).  ``mode``: 0 (or False) row-grouped on [N, K]
+    operands, 1 (or True) K-grouped on transposed copies, 2 row-grouped with x held [K, N], 3 K-grouped on
+    the row-major codes [rows, Mo] and [rows, N]."""
+    mode = int(mode)
+    _expect(mode in (0, 1, 2, 3), "mode must be 0 to 3")
+    kgroups = mode in (1, 3)
     G = offsets.numel() - 1
     dev = _need_cuda(offsets, *ys, *xs, *cs, *(c2s or []), *(auxs or []), y_scale_inv, x_scale_inv)
     ycode, ydt, _ = FP8_FORMATS[y_fmt]
@@ -662,13 +691,29 @@ def fp8_gemm(kgroups: bool, epi: str, offsets: torch.Tensor, rows_cap: int, ys: 
         _expect(t.dtype == torch.bfloat16 and t.dim() == 2, "outputs and pre-activations must be bf16 matrices")
     _expect(x_scale_inv.dtype == torch.float32 and x_scale_inv.numel() in (1, G), "x_scale_inv must be float32 [1] or [G]")
     _expect(y_scale_inv.dtype == torch.float32 and y_scale_inv.numel() == 1, "y_scale_inv must be float32 [1]")
-    if kgroups:
+    if mode == 3:
+        _expect(len(ys) == 1 and len(xs) == 1, "K-grouped products take one buffer per operand")
+        _expect(ys[0].dim() == 2 and ys[0].shape[1] == Mo and ys[0].shape[0] >= rows_cap and ys[0].is_contiguous(),
+                f"y must be [>= {rows_cap}, {Mo}]")
+        _expect(xs[0].dim() == 2 and xs[0].shape[1] == N and xs[0].shape[0] >= rows_cap and xs[0].is_contiguous(),
+                f"x must be [>= {rows_cap}, {N}]")
+        for t in cs:
+            _expect(tuple(t.shape) == (Mo, N), f"outputs must be [{Mo}, {N}]")
+        ldy, ldx = Mo, N
+    elif kgroups:
         _expect(len(ys) == 1 and len(xs) == 1, "K-grouped products take one transposed buffer per operand")
         _expect(ys[0].numel() >= fp8_transposed_numel(Mo, rows_cap, G), "y is too small")
         _expect(xs[0].numel() >= fp8_transposed_numel(N, rows_cap, G), "x is too small")
         for t in cs:
             _expect(tuple(t.shape) == (Mo, N), f"outputs must be [{Mo}, {N}]")
         ldy = ldx = 0
+    elif mode == 2:
+        _expect(len(ys) == G and len(xs) == G, f"expected {G} operands per side")
+        for t in ys:
+            _expect(t.dim() == 2 and t.shape[1] == K and t.shape[0] >= rows_cap, f"y must be [>= {rows_cap}, {K}]")
+        for t in xs:
+            _expect(tuple(t.shape) == (K, N) and t.is_contiguous(), f"x must be [{K}, {N}]")
+        ldy, ldx = K, N
     else:
         _expect(len(ys) == G and len(xs) == G, f"expected {G} operands per side")
         for t in ys:
@@ -679,7 +724,7 @@ def fp8_gemm(kgroups: bool, epi: str, offsets: torch.Tensor, rows_cap: int, ys: 
         ldy = ldx = K
     c2p = _arr(c2s) if c2s else None
     auxp = _arr(auxs) if auxs else None
-    _call("rhp_fp8_gemm", dev, int(kgroups), EPI_CODES[epi], G, _ptr(offsets), rows_cap, ycode, xcode, N, K, Mo, f,
+    _call("rhp_fp8_gemm", dev, mode, EPI_CODES[epi], G, _ptr(offsets), rows_cap, ycode, xcode, N, K, Mo, f,
           _arr(ys), ldy, _arr(xs), ldx, _arr(cs), cs[0].shape[1], c2p, c2s[0].shape[1] if c2s else 0, auxp,
           auxs[0].shape[1] if auxs else 0, _ptr(y_scale_inv), _ptr(x_scale_inv),
           0 if x_scale_inv.numel() == 1 else 1)
@@ -690,8 +735,9 @@ def fp8_gemm_cast(epi: str, offsets: torch.Tensor, poff: torch.Tensor, rows_cap:
                   y_scale_inv: torch.Tensor, x_scale_inv: torch.Tensor, history: torch.Tensor, q_fmt: str,
                   amax_bits: torch.Tensor, scale_inv: torch.Tensor, q: torch.Tensor | None, qt: torch.Tensor | None,
                   cs: list[torch.Tensor] | None = None, auxs: list[torch.Tensor] | None = None,
-                  margin: int = 0) -> None:
+                  margin: int = 0, x_kn: bool = False) -> None:
     """Row-grouped fp8 product whose epilogue casts its activation output to fp8 (rhp_fp8_gemm_cast).
+    ``x_kn``: the weights are held [K, N] (row-major codes; backward epilogues only).
 
     Forward epilogues store the pre-activation in ``cs`` and cast the activation; backward epilogues read
     the pre-activation from ``auxs`` and cast the pre-activation gradient.  The codes equal those of
@@ -710,8 +756,11 @@ def fp8_gemm_cast(epi: str, offsets: torch.Tensor, poff: torch.Tensor, rows_cap:
         _expect(t.dtype == ydt and t.dim() == 2 and t.shape[1] == K and t.shape[0] >= rows_cap,
                 f"y operands must be {ydt} [>= {rows_cap}, {K}]")
     xrows = 2 * f if epi == "swiglu_fwd" else N
+    xshape = (K, N) if x_kn else (xrows, K)
+    _expect(not (x_kn and fwd), "[K, N] weights only with the backward epilogues")
     for t in xs:
-        _expect(t.dtype == xdt and tuple(t.shape) == (xrows, K), f"x operands must be {xdt} [{xrows}, {K}]")
+        _expect(t.dtype == xdt and tuple(t.shape) == xshape and t.is_contiguous(),
+                f"x operands must be {xdt} {list(xshape)}")
     if fwd:
         _expect(cs is not None and len(cs) == G and auxs is None, "forward epilogues take G pre-activation outputs")
     else:
@@ -732,7 +781,7 @@ def fp8_gemm_cast(epi: str, offsets: torch.Tensor, poff: torch.Tensor, rows_cap:
     if qt is not None:
         _expect(qt.dtype == qdt and qt.numel() >= fp8_transposed_numel(cols, rows_cap, G), "qt is too small")
     _call("rhp_fp8_gemm_cast", dev, EPI_CODES[epi], G, _ptr(offsets), _ptr(poff), rows_cap, ycode, xcode, N, K, f,
-          _arr(ys), K, _arr(xs), K, _arr(cs) if cs else None, cs[0].shape[1] if cs else 0,
+          _arr(ys), K, _arr(xs), N if x_kn else K, int(x_kn), _arr(cs) if cs else None, cs[0].shape[1] if cs else 0,
           _arr(auxs) if auxs else None, auxs[0].shape[1] if auxs else 0, _ptr(y_scale_inv), _ptr(x_scale_inv),
           0 if x_scale_inv.numel() == 1 else 1, _ptr(history), history.numel(), qcode, margin, _ptr(amax_bits),
           _ptr(scale_inv), _ptr(q), _ptr(qt))

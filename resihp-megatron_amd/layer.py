@@ -118,41 +118,36 @@ def expert_backward(dys, acts, hpres, offsets, rows_from_offsets: bool, rows_cap
 
 
 def _fp8_forward(st: Fp8State, meta: LayerMeta, offsets, P, xp, fc1s, fc2s, hpre, y):
-    """Expert FFN forward in fp8; returns what the backward needs (codes and transposed copies).
+    """Expert FFN forward in fp8; returns what the backward needs (the row-major codes).
 
-    The fc1 product's epilogue casts the activation straight to fp8 (no bf16 activation rows).
+    The fc1 product's epilogue casts the activation straight to fp8 (no bf16 activation rows).  Every
+    operand is kept as row-major codes only: the backward products read them N-contiguous and transpose
+    in LDS (fp8 product modes 2 and 3).
     """
     G, f = st.G, meta.ffn
     h = xp.shape[1]
-    dev = xp.device
-    w1q, w1qt, w2q, w2qt = [], [], [], []
-    for g, (w1, w2) in enumerate(zip(fc1s, fc2s)):
-        o1, p1 = st.single_range(w1.shape[0], dev)
-        q, qt = st.cast(st.w1(g), w1, o1, p1, w1.shape[0])
-        w1q.append(q)
-        w1qt.append(qt[:w1.numel()].view(w1.shape[1], w1.shape[0]))
-        o2, p2 = st.single_range(w2.shape[0], dev)
-        q, qt = st.cast(st.w2(g), w2, o2, p2, w2.shape[0])
-        w2q.append(q)
-        w2qt.append(qt[:w2.numel()].view(w2.shape[1], w2.shape[0]))
+    w1q, w2q = st.cast_weights(fc1s, fc2s)
     sw1 = st.scale_inv[st.w1(0):st.w1(0) + G]
     sw2 = st.scale_inv[st.w2(0):st.w2(0) + G]
+    # The casts tile each expert's rows in blocks of 128 (the padded offsets); no transposed copy is written.
     poff = K.fp8_padded_offsets(offsets)
-    xqt = aqt = None
+    xq = aq = None
     if P > 0:
-        xq, xqt = st.cast(X, xp, offsets, poff, P)
+        xq, _ = st.cast(X, xp, offsets, poff, P, transposed=False)
         epi = "swiglu_fwd" if meta.act == "swiglu" else "gelu_fwd"
-        aq, aqt = st.gemm_cast(ACT, epi, offsets, poff, P, [xq] * G, "e4m3", w1q, f, h, f, st.scale_inv[X:X + 1],
-                               sw1, cs=[hpre] * G)
-        K.fp8_gemm(False, "store", offsets, P, [aq] * G, "e4m3", w2q, "e4m3", h, f, 0, f, [y] * G,
+        aq, _ = st.gemm_cast(ACT, epi, offsets, poff, P, [xq] * G, "e4m3", w1q, f, h, f, st.scale_inv[X:X + 1],
+                             sw1, cs=[hpre] * G, transposed=False)
+        K.fp8_gemm(0, "store", offsets, P, [aq] * G, "e4m3", w2q, "e4m3", h, f, 0, f, [y] * G,
                    st.scale_inv[ACT:ACT + 1], sw2)
-    return dict(poff=poff, xqt=xqt, aqt=aqt, w1qt=w1qt, w2qt=w2qt, sw1=sw1, sw2=sw2)
+    return dict(poff=poff, xq=xq, aq=aq, w1q=w1q, w2q=w2q, sw1=sw1, sw2=sw2)
 
 
 def _fp8_backward(st: Fp8State, q8: dict, meta: LayerMeta, offsets, P, dy, hpre, dxp, dw1, dw2):
     """Expert FFN backward in fp8 (e5m2 gradients, e4m3 weights and activations).
 
-    The fc2 input-gradient product's epilogue casts the pre-activation gradient straight to fp8.
+    The fc2 input-gradient product's epilogue casts the pre-activation gradient straight to fp8.  The
+    input-gradient products read the row-major weight codes as [K, N] (mode 2) and the weight gradients
+    the row-major activation and gradient codes (mode 3).
     """
     G, f = st.G, meta.ffn
     h = dy.shape[1]
@@ -161,18 +156,18 @@ def _fp8_backward(st: Fp8State, q8: dict, meta: LayerMeta, offsets, P, dy, hpre,
         for w in (*dw1, *dw2):
             w.zero_()
         return
-    poff = q8["poff"]
     s = st.scale_inv
-    dyq, dyqt = st.cast(DY, dy, offsets, poff, P)
+    poff = q8["poff"]
+    dyq, _ = st.cast(DY, dy, offsets, poff, P, transposed=False)
     epi = "swiglu_bwd" if meta.act == "swiglu" else "gelu_bwd"
-    dhq, dhqt = st.gemm_cast(DH, epi, offsets, poff, P, [dyq] * G, "e5m2", q8["w2qt"], f, h, f, s[DY:DY + 1],
-                             q8["sw2"], auxs=[hpre] * G)
-    K.fp8_gemm(True, "store", poff, P, [dyqt], "e5m2", [q8["aqt"]], "e4m3", f, 0, h, f, list(dw2), s[DY:DY + 1],
+    dhq, _ = st.gemm_cast(DH, epi, offsets, poff, P, [dyq] * G, "e5m2", q8["w2q"], f, h, f, s[DY:DY + 1],
+                          q8["sw2"], auxs=[hpre] * G, transposed=False, x_kn=True)
+    K.fp8_gemm(3, "store", offsets, P, [dyq], "e5m2", [q8["aq"]], "e4m3", f, 0, h, f, list(dw2), s[DY:DY + 1],
                s[ACT:ACT + 1])
     if dxp is not None:
-        K.fp8_gemm(False, "store", offsets, P, [dhq] * G, "e5m2", q8["w1qt"], "e4m3", h, F1, 0, f, [dxp] * G,
+        K.fp8_gemm(2, "store", offsets, P, [dhq] * G, "e5m2", q8["w1q"], "e4m3", h, F1, 0, f, [dxp] * G,
                    s[DH:DH + 1], q8["sw1"])
-    K.fp8_gemm(True, "store", poff, P, [dhqt], "e5m2", [q8["xqt"]], "e4m3", h, 0, F1, f, list(dw1), s[DH:DH + 1],
+    K.fp8_gemm(3, "store", offsets, P, [dhq], "e5m2", [q8["xq"]], "e4m3", h, 0, F1, f, list(dw1), s[DH:DH + 1],
                s[X:X + 1])
 
 

@@ -73,9 +73,9 @@ def test_dispatch_and_gemm_reject_bad_arguments():
         C.call("rhp_combine", fake, fake, fake, C.F32, fake, fake, ptrs, 9, C.BF16, 4, 64, 2, fake, None)
 
 
-def _gemm_cast(epi=1, q_fmt=C.E4M3, c=True, history=True, q=True, qt=True, margin=0):
+def _gemm_cast(epi=1, q_fmt=C.E4M3, c=True, history=True, q=True, qt=True, margin=0, x_kn=0):
     fake = ctypes.c_void_p(4096)   # 16-byte aligned, never dereferenced: validation fails first
-    C.call("rhp_fp8_gemm_cast", epi, 2, fake, fake, 512, C.E4M3, C.E4M3, 256, 256, 256, fake, 256, fake, 256,
+    C.call("rhp_fp8_gemm_cast", epi, 2, fake, fake, 512, C.E4M3, C.E4M3, 256, 256, 256, fake, 256, fake, 256, x_kn,
            fake if c else None, 512, fake, 512, fake, fake, 1, fake if history else None, 16, q_fmt, margin, fake,
            fake, fake if q else None, fake if qt else None, None)
 
@@ -88,6 +88,8 @@ def _gemm_cast(epi=1, q_fmt=C.E4M3, c=True, history=True, q=True, qt=True, margi
     (dict(margin=64), "bad history or margin"),
     (dict(epi=1, c=False), "store the pre-activation in c"),
     (dict(epi=3, c=True), "store no bf16 output"),
+    (dict(epi=1, x_kn=1), r"\[K, N\] weights only with the backward"),
+    (dict(epi=3, c=False, x_kn=2), "x_kn must be 0 or 1"),
 ])
 def test_fp8_gemm_cast_rejects_bad_arguments(kw, msg):
     with pytest.raises(RuntimeError, match=msg):

@@ -168,7 +168,21 @@ def test_fp8_expert_products(case):
     K.fp8_gemm(False, "store", offs, P, [dhq] * G, "e5m2", w1qt, "e4m3", h, 2 * f, 0, f, [dxp] * G, sdh, sw1)
     K.fp8_gemm(True, "store", poff, P, [dyqt], "e5m2", [aqt], "e4m3", f, 0, h, f, dw2, sdy, sa)
     K.fp8_gemm(True, "store", poff, P, [dhqt], "e5m2", [xqt], "e4m3", h, 0, 2 * f, f, dw1, sdh, sx)
+    # The same backward products on the row-major codes (modes 2 and 3: N-contiguous operands, transposed in
+    # LDS): every lane multiplies the same k as in modes 0 and 1, so the results are the same bits.
+    dhpre_kn, dxp_kn = torch.empty_like(dhpre), torch.empty_like(dxp)
+    dw2_mn, dw1_mn = [torch.empty_like(w) for w in dw2], [torch.empty_like(w) for w in dw1]
+    K.fp8_gemm(2, "swiglu_bwd", offs, P, [dyq] * G, "e5m2", w2q, "e4m3", f, h, 0, f, [dhpre_kn] * G, sdy, sw2,
+               auxs=[hp_in] * G)
+    K.fp8_gemm(2, "store", offs, P, [dhq] * G, "e5m2", w1q, "e4m3", h, 2 * f, 0, f, [dxp_kn] * G, sdh, sw1)
+    K.fp8_gemm(3, "store", offs, P, [dyq], "e5m2", [aq], "e4m3", f, 0, h, f, dw2_mn, sdy, sa)
+    K.fp8_gemm(3, "store", offs, P, [dhq], "e5m2", [xq], "e4m3", h, 0, 2 * f, f, dw1_mn, sdh, sx)
     torch.cuda.synchronize()
+    _same_bits(dhpre_kn, dhpre, "fc2 dgrad on [K, N] weight codes")
+    _same_bits(dxp_kn, dxp, "fc1 dgrad on [K, N] weight codes")
+    for g in range(G):
+        _same_bits(dw2_mn[g], dw2[g], f"fc2 wgrad on row-major codes, expert {g}")
+        _same_bits(dw1_mn[g], dw1[g], f"fc1 wgrad on row-major codes, expert {g}")
 
     xd, ad, dyd, dhd = _deq(xq, sx), _deq(aq, sa), _deq(dyq, sdy), _deq(dhq, sdh)
     hp64 = hp_in.cpu().double()
@@ -270,7 +284,15 @@ def _fused_case(act, hist_scale, margin, h, f, counts):
     df = _cast_buffers(P, F1, G, "e5m2")
     K.fp8_gemm_cast(f"{act}_bwd", offs, poff, P, [dyq] * G, "e5m2", w2qt, "e4m3", f, h, f, sdy, sw2, hist_d, "e5m2",
                     *df, auxs=[hp_in] * G, margin=margin)
+    # the same on the row-major fc2 codes held [h, f] (x_kn): the same codes, amax and scale
+    w2q = [wt.t().contiguous() for wt in w2qt]
+    dk = _cast_buffers(P, F1, G, "e5m2")
+    K.fp8_gemm_cast(f"{act}_bwd", offs, poff, P, [dyq] * G, "e5m2", w2q, "e4m3", f, h, f, sdy, sw2, hist_d, "e5m2",
+                    *dk, auxs=[hp_in] * G, margin=margin, x_kn=True)
     torch.cuda.synchronize()
+    _same_bits(dk[2], df[2], "pre-activation gradient codes from [K, N] weights")
+    _same_bits(dk[3], df[3], "transposed pre-activation gradient codes from [K, N] weights")
+    assert dk[0].item() == df[0].item() and dk[1].item() == df[1].item()
 
     _same_bits(hpre_f, hpre_u, "pre-activations")
     for name, (ua, us, uq, uqt), (fa, fs, fq, fqt) in (("activation", au, af), ("pre-activation gradient", du, df)):
@@ -353,3 +375,31 @@ def test_fp8_layer_matches_quantized_emulation(case):
         assert rel_err(fc2[e].grad, dyq.t() @ aq) <= LAYER_BAR, f"fc2 weight gradient of expert {e}"
         assert rel_err(fc1[e].grad, dhq.t() @ xq) <= DW1_BAR, f"fc1 weight gradient of expert {e}"
     assert rel_err(out, out_ref) <= LAYER_BAR
+
+
+def test_cast_many_equals_one_cast_per_tensor():
+    """rhp_fp8_cast_many (the expert weights in one launch) gives every tensor the codes, amax and 1/scale
+    of its own rhp_fp8_cast: tensors of different shapes, rows not a multiple of 128, an empty one."""
+    shapes = [(512, 256), (256, 384), (130, 64), (0, 128), (1000, 192)]
+    xs = [seeded(s, 90 + i, 0.3, torch.bfloat16).to(DEV) for i, s in enumerate(shapes)]
+    hists = [_history(95 + i, scale=0.5).to(DEV) for i in range(len(shapes))]
+    say(f"fp8 cast_many over {shapes}")
+    fdt = K.FP8_FORMATS["e4m3"][1]
+    amax_m = [torch.zeros(1, dtype=torch.int32, device=DEV) for _ in shapes]
+    sinv_m = [torch.zeros(1, dtype=torch.float32, device=DEV) for _ in shapes]
+    q_m = [torch.empty(s, dtype=fdt, device=DEV) for s in shapes]
+    K.fp8_cast_many(xs, hists, "e4m3", amax_m, sinv_m, q_m)
+    for i, (x, hst) in enumerate(zip(xs, hists)):
+        if x.shape[0] == 0:   # no codes; the 1/scale is still written, the amax stays 0
+            x = torch.zeros(1, x.shape[1], dtype=torch.bfloat16, device=DEV)
+        rows = x.shape[0]
+        off = torch.tensor([0, rows], dtype=torch.int32, device=DEV)
+        poff = torch.tensor([0, (rows + 127) // 128 * 128], dtype=torch.int32, device=DEV)
+        a = torch.zeros(1, dtype=torch.int32, device=DEV)
+        si = torch.zeros(1, dtype=torch.float32, device=DEV)
+        q = torch.empty(x.shape, dtype=fdt, device=DEV)
+        K.fp8_cast(x, off, poff, rows, hst, "e4m3", a, si, q, None)
+        torch.cuda.synchronize()
+        if shapes[i][0]:
+            _same_bits(q_m[i], q, f"codes of tensor {i}")
+        assert amax_m[i].item() == a.item() and sinv_m[i].item() == si.item(), f"amax / scale of tensor {i}"
