@@ -418,8 +418,8 @@ def main() -> int:
     kernels.set_timer(None)
 
     per = {name: (ms / args.steps, n // args.steps) for name, (ms, n) in timer.totals_ms().items()}
-    S = w["S"]
     fp8 = w["fp8"] is not None
+    S = w["S"]
     peak = PEAK_FP8_TFLOPS if fp8 else PEAK_BF16_TFLOPS
     gemm_flops = 18.0 * (P + S * T) * h * f          # SwiGLU: fwd 6 P h f + bwd 12 P h f
     gemm_ms = timer.union_ms(GEMM_CALLS) / args.steps
@@ -428,11 +428,13 @@ def main() -> int:
     if received:   # the products read and write received rows through the plan's row map; two row gathers a
         # step make the expert-major copies the weight gradients read (inputs, output gradients)
         row_bytes = {"rhp_gather_rows": 2 * (2 * P * h * s + 4 * P)}
-    else:          # algorithmic HBM bytes per step of the row kernels (token-major permute)
+    else:          # algorithmic HBM bytes per step of the row kernels (token-major permute); with fp8
+        # experts the permute and the combine backward write 1-byte codes instead of bf16 rows
+        c = 1 if fp8 else s
         row_bytes = {
-            "rhp_permute": T * h * s + P * h * s + 4 * P,
+            "rhp_permute_fp8" if fp8 else "rhp_permute": T * h * s + P * h * c + 4 * P,
             "rhp_combine": P * h * s + 2 * T * h * s + 8 * P + S * T * h * s,
-            "rhp_combine_bwd": T * h * s + 2 * P * h * s + 8 * P,
+            "rhp_combine_bwd_fp8" if fp8 else "rhp_combine_bwd": T * h * s + P * h * s + P * h * c + 8 * P,
             "rhp_token_bwd": 2 * T * h * s + P * h * s + 12 * P + S * T * h * s,
         }
     row_ms = sum(per.get(n, (0.0, 0))[0] for n in row_bytes)

@@ -411,6 +411,28 @@ int rhp_fp8_cast_many(int n, const void* const* x, const int64_t* rows, const in
                       const float* const* history, int hist_len, int fmt, int margin, uint32_t* const* amax_bits,
                       float* const* scale_inv, void* const* q, hipStream_t stream);
 
+/*
+ * rhp_permute of bf16 rows with fp8 codes as the output: q [rows, h] receives
+ * the row-major codes that rhp_fp8_cast would write for the bf16 rows that
+ * rhp_permute stores, with the scale of `history`; *amax_bits rises to their
+ * max |value| and *scale_inv = 1 / scale, bit for bit as permute then cast
+ * (T == 0 writes nothing).
+ * Replaces the dispatch copy of resihp/runtime/moe.py:78 followed by the
+ * input cast of the fp8 expert products (reference_model.py:188-203).
+ */
+int rhp_permute_fp8(const void* x, int64_t T, int h, int k, const int32_t* pair_row, int fmt,
+                    const float* history, int hist_len, int margin, uint32_t* amax_bits, float* scale_inv, void* q,
+                    hipStream_t stream);
+
+/*
+ * rhp_combine_bwd (bf16, float32 gates, top-k <= 8) with dy leaving as fp8
+ * codes: q [rows, h] receives the codes of the bf16 dy rows, bit for bit as
+ * rhp_combine_bwd then rhp_fp8_cast; dgates as rhp_combine_bwd.
+ */
+int rhp_combine_bwd_fp8(const void* dout, const void* y, const float* gates, const int32_t* pair_row, int64_t T,
+                        int h, int k, float* dgates, int fmt, const float* history, int hist_len, int margin,
+                        uint32_t* amax_bits, float* scale_inv, void* q, hipStream_t stream);
+
 /* End of iteration for n tensors: history[i] = [amax_i, history[i][0 .. hist_len-2]], amax_i = 0 (reference_model.py:215). */
 int rhp_fp8_amax_roll(float* history, uint32_t* amax_bits, int n, int hist_len, hipStream_t stream);
 

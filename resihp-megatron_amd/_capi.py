@@ -60,6 +60,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "rhp_fp8_cast": (_i, [_p, _i, _i64, _i, _i, _p, _p, _i64, _p, _i, _i, _i, _p, _p, _p, _p, _p]),
     "rhp_fp8_cast_many": (_i, [_i, _pp, _pi64, _pi64, _pp, _i, _i, _i, _pp, _pp, _pp, _p]),
     "rhp_fp8_amax_roll": (_i, [_p, _p, _i, _i, _p]),
+    "rhp_permute_fp8": (_i, [_p, _i64, _i, _i, _p, _i, _p, _i, _i, _p, _p, _p, _p]),
+    "rhp_combine_bwd_fp8": (_i, [_p, _p, _p, _p, _i64, _i, _i, _p, _i, _p, _i, _i, _p, _p, _p, _p]),
     "rhp_fp8_gemm": (_i, [_i, _i, _i, _p, _i64, _i, _i, _i, _i, _i, _i, _pp, _i64, _pp, _i64, _pp, _i64, _pp, _i64,
                           _pp, _i64, _p, _p, _i, _p]),
     "rhp_fp8_gemm_cast": (_i, [_i, _i, _p, _p, _i64, _i, _i, _i, _i, _i, _pp, _i64, _pp, _i64, _i, _pp, _i64, _pp,

@@ -7,6 +7,7 @@
 #include <atomic>
 #include <string>
 
+#include "fp8_common.h"
 #include "rhp_common.h"
 
 
@@ -353,38 +354,6 @@ constexpr uint32_t kOutOfRange = 0x80000000u;   // a buffer offset past every vi
 
 // ------------------------------------------------------------------ fp8 codes
 
-constexpr int kFmtE4m3 = 0;   // MFMA operand format codes (cbsz / blgp)
-constexpr int kFmtE5m2 = 1;
-
-__host__ __device__ constexpr float fp8_max(int fmt) { return fmt == kFmtE4m3 ? 448.0f : 57344.0f; }
-
-// scale = fp8_max / max(history) / 2^margin, evaluated in double and rounded
-// once to float; 1 when the maximum is not a positive finite number.
-__device__ __forceinline__ float history_scale(const float* hist, int L, float fmax, int margin) {
-    float a = -__builtin_huge_valf();
-    bool nan = false;
-    for (int i = 0; i < L; ++i) {
-        const float v = hist[i];
-        nan |= v != v;
-        a = v > a ? v : a;
-    }
-    if (nan || !(a > 0.0f) || a == __builtin_huge_valf()) return 1.0f;
-    return static_cast<float>(static_cast<double>(fmax) / static_cast<double>(a) / __builtin_ldexp(1.0, margin));
-}
-
-template <int FMT>
-__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
-    uint32_t w;
-    if (FMT == kFmtE4m3) {
-        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false));
-        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, static_cast<int>(w), true));
-    } else {
-        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false));
-        w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(c, d, static_cast<int>(w), true));
-    }
-    return w;
-}
-
 // 4 x 4 byte transpose: word j holds bytes (row j, cols 0..3); word i of the
 // result holds bytes (rows 0..3, col i).
 __device__ __forceinline__ void transpose4x4(const uint32_t a[4], uint32_t b[4]) {
@@ -728,10 +697,12 @@ __device__ __forceinline__ void epilogue_half_q(const Params& p, const Tile& t, 
             const uint32_t code = quant4<QF>(silu_f(gv.x) * uv.x, silu_f(gv.y) * uv.y, silu_f(gv.z) * uv.z,
                                              silu_f(gv.w) * uv.w, ok && r0 + r < t.y_lim, qa);
             __builtin_amdgcn_raw_buffer_store_b32(code, qv, static_cast<int>(oq), 0, 0);
-            ep[code_word(r, threadIdx.x & 31)] = __uint_as_float(code);
+            if (p.qt) ep[code_word(r, threadIdx.x & 31)] = __uint_as_float(code);
         }
-        lds_barrier();
-        store_transposed_half<kW, kW, NT>(p, t, ep, r0);
+        if (p.qt) {   // the transposed copy (uniform: every wave takes the same branch)
+            lds_barrier();
+            store_transposed_half<kW, kW, NT>(p, t, ep, r0);
+        }
     } else {
         // Thread t covers columns 4 (t % 64) .. + 3 of rows r0 + t / 64 + (NT / 64) n.
         constexpr int kParts = EPI == kEpiSwigluBwd ? 2 : 1, kW = 64 * kParts, kN = kEpRows * 64 / NT;
@@ -778,11 +749,13 @@ __device__ __forceinline__ void epilogue_half_q(const Params& p, const Tile& t, 
 #pragma unroll
             for (int pt = 0; pt < kParts; ++pt) {
                 __builtin_amdgcn_raw_buffer_store_b32(code[pt], qv, static_cast<int>(oq), pt * p.f, 0);
-                ep[code_word(r, pt * 64 + (threadIdx.x & 63))] = __uint_as_float(code[pt]);
+                if (p.qt) ep[code_word(r, pt * 64 + (threadIdx.x & 63))] = __uint_as_float(code[pt]);
             }
         }
-        lds_barrier();
-        store_transposed_half<kW, 64, NT>(p, t, ep, r0);
+        if (p.qt) {   // the transposed copy (uniform: every wave takes the same branch)
+            lds_barrier();
+            store_transposed_half<kW, 64, NT>(p, t, ep, r0);
+        }
     }
 }
 

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 
+#include "fp8_common.h"
 #include "rhp_common.h"
 
 namespace rhp {
@@ -338,6 +339,84 @@ __device__ __forceinline__ uint4 pack_bf16x8(const float* v) {
                       pack_bf16x2(v[6], v[7]));
 }
 
+// fp8 codes instead of bf16 rows (the permute and combine backward of fp8
+// layers): the cast of rhp_fp8_cast applied to the rows the kernel would
+// store, with the delayed scale of `hist`; *amax_bits rises to the rows' max
+// |value| (float bits), *scale_inv receives 1 / scale.
+struct CodeOut {
+    uint8_t* q;
+    const float* hist;
+    int L, margin;
+    uint32_t* amax_bits;
+    float* scale_inv;
+};
+
+// Eight values as they would be stored in bf16, cast to fp8 (8 bytes); m rises to their max |value|.
+template <int FMT>
+__device__ __forceinline__ uint2 codes8(const float* v, float scale, float& m) {
+    const uint4 b = pack_bf16x8(v);
+    float r[8];
+    unpack_bf16x8(b, r);
+    const float lim = fp8_max(FMT);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        m = fmaxf(m, fabsf(r[e]));
+        r[e] = fminf(fmaxf(r[e] * scale, -lim), lim);
+    }
+    return make_uint2(pack4<FMT>(r[0], r[1], r[2], r[3]), pack4<FMT>(r[4], r[5], r[6], r[7]));
+}
+
+// Wave maximum of m, then one atomic per wave when it raises the running maximum (non-negative floats
+// order like their bits; the value read may be stale but never larger than the true one).
+__device__ __forceinline__ void raise_amax(uint32_t* amax_bits, float m) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0 && m > 0.0f) {
+        const uint32_t seen = __hip_atomic_load(amax_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__float_as_uint(m) > seen) atomicMax(amax_bits, __float_as_uint(m));
+    }
+}
+
+// Permute to fp8 codes: each token's row is cast once and stored at every
+// local row of the token (codes rows of h bytes).
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void permute_fp8_kernel(const bf16* __restrict__ x, int64_t T, int h, int k,
+                                                               const int32_t* __restrict__ pair_row, CodeOut co) {
+    const float scale = history_scale(co.hist, co.L, fp8_max(FMT), co.margin);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *co.scale_inv = 1.0f / scale;
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (t >= T) return;
+    int32_t rows[kMaxTopK];
+    bool any = false;
+    for (int j = 0; j < k; ++j) {
+        rows[j] = pair_row[t * k + j];
+        any |= rows[j] >= 0;
+    }
+    if (!any) return;
+    constexpr int U = 8;
+    const int nch = h / 8;
+    const bf16* src = x + t * h;
+    float m = 0.0f;
+    for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (c0 + u * 64 < nch) v[u] = nt_load16(src + (c0 + u * 64) * 8);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + u * 64 >= nch) continue;
+            float f[8];
+            unpack_bf16x8(v[u], f);
+            const uint2 c = codes8<FMT>(f, scale, m);
+            for (int j = 0; j < k; ++j)
+                if (rows[j] >= 0)
+                    *reinterpret_cast<uint2*>(co.q + static_cast<int64_t>(rows[j]) * h + (c0 + u * 64) * 8) = c;
+        }
+    }
+    raise_amax(co.amax_bits, m);
+}
+
 // Rank of each slot in ascending expert id (ids of one token are distinct,
 // equal ids rank by slot), then the slot holding each rank, all by selects.
 template <int KM>
@@ -453,13 +532,19 @@ __global__ __launch_bounds__(kThreads) void combine_bf16_kernel(const bf16* __re
     }
 }
 
-template <int KM, int U>
+template <int KM, int U, int QF = -1>
 __global__ __launch_bounds__(kThreads) void combine_bwd_bf16_kernel(const bf16* __restrict__ dout,
                                                                     const bf16* __restrict__ y,
                                                                     const float* __restrict__ gates,
                                                                     const int32_t* __restrict__ pair_row, int64_t T,
                                                                     int h, int k, bf16* __restrict__ dy,
-                                                                    float* __restrict__ dgates) {
+                                                                    float* __restrict__ dgates, CodeOut co) {
+    // QF >= 0: dy leaves as fp8 codes of that format (co) instead of bf16 rows.
+    float scale = 1.0f, m = 0.0f;
+    if constexpr (QF >= 0) {
+        scale = history_scale(co.hist, co.L, fp8_max(QF), co.margin);
+        if (blockIdx.x == 0 && threadIdx.x == 0) *co.scale_inv = 1.0f / scale;
+    }
     const int lane = threadIdx.x & 63;
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
     if (t >= T) return;
@@ -501,7 +586,11 @@ __global__ __launch_bounds__(kThreads) void combine_bwd_bf16_kernel(const bf16* 
                         o[i] = g[j] * d[i];
                         dot[j] = dot[j] + d[i] * v[i];
                     }
-                    store16(dy + static_cast<int64_t>(rows[j]) * h + (c0 + u * 64) * 8, pack_bf16x8(o));
+                    if constexpr (QF >= 0)
+                        *reinterpret_cast<uint2*>(co.q + static_cast<int64_t>(rows[j]) * h + (c0 + u * 64) * 8) =
+                            codes8<QF>(o, scale, m);
+                    else
+                        store16(dy + static_cast<int64_t>(rows[j]) * h + (c0 + u * 64) * 8, pack_bf16x8(o));
                 }
         }
     }
@@ -512,6 +601,7 @@ __global__ __launch_bounds__(kThreads) void combine_bwd_bf16_kernel(const bf16* 
         for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
         if (lane == 0) dgates[t * k + j] = v;
     }
+    if constexpr (QF >= 0) raise_amax(co.amax_bits, m);
 }
 
 // One token of the bf16 token backward: dx[t] = dout[t] + sum_j dxp[row_j] + sum_j dl_j * router_w[e_j]
@@ -884,11 +974,11 @@ extern "C" int rhp_combine_bwd(const void* dout, const void* y, const void* gate
             switch (row_variant(k, 0)) {
                 case RowVariant::kSmall:
                     hipLaunchKernelGGL((combine_bwd_bf16_kernel<2, 8>), grid, block, 0, stream, db, yb, gf, pair_row,
-                                       T, h, k, dyb, dg);
+                                       T, h, k, dyb, dg, CodeOut{});
                     break;
                 case RowVariant::kWide:
                     hipLaunchKernelGGL((combine_bwd_bf16_kernel<8, 2>), grid, block, 0, stream, db, yb, gf, pair_row,
-                                       T, h, k, dyb, dg);
+                                       T, h, k, dyb, dg, CodeOut{});
                     break;
                 default:
                     hipLaunchKernelGGL((combine_bwd_kernel<bf16, float>), grid, block, 0, stream, db, yb, gf,
@@ -901,6 +991,74 @@ extern "C" int rhp_combine_bwd(const void* dout, const void* y, const void* gate
                                static_cast<float*>(dgates));
     }
     return check_launch("combine_bwd_kernel");
+}
+
+namespace {
+// The code outputs of the fp8 row entries: checks shared by rhp_permute_fp8 and rhp_combine_bwd_fp8.
+int code_out(const char* fn, int fmt, void* q, const float* history, int hist_len, int margin, uint32_t* amax_bits,
+             float* scale_inv, int& f8, CodeOut& co) {
+    f8 = fmt == RHP_E4M3 ? kFmtE4m3 : fmt == RHP_E5M2 ? kFmtE5m2 : -1;
+    if (f8 < 0) return fail(std::string(fn) + ": format must be RHP_E4M3 or RHP_E5M2");
+    if (!q || !history || !amax_bits || !scale_inv || !aligned16(q))
+        return fail(std::string(fn) + ": null code output or unaligned codes");
+    if (hist_len < 1 || margin < 0 || margin >= 64) return fail(std::string(fn) + ": bad history length or margin");
+    co = CodeOut{static_cast<uint8_t*>(q), history, hist_len, margin, amax_bits, scale_inv};
+    return 0;
+}
+}  // namespace
+
+extern "C" int rhp_permute_fp8(const void* x, int64_t T, int h, int k, const int32_t* pair_row, int fmt,
+                               const float* history, int hist_len, int margin, uint32_t* amax_bits, float* scale_inv,
+                               void* q, hipStream_t stream) {
+    clear_error();
+    if (int rc = check_rows("rhp_permute_fp8", RHP_BF16, T, h, k)) return rc;
+    RHP_REQUIRE(fmt == RHP_E4M3 || fmt == RHP_E5M2, "rhp_permute_fp8: format must be RHP_E4M3 or RHP_E5M2");
+    if (T == 0) return 0;
+    int f8;
+    CodeOut co;
+    if (int rc = code_out("rhp_permute_fp8", fmt, q, history, hist_len, margin, amax_bits, scale_inv, f8, co))
+        return rc;
+    RHP_REQUIRE(x && pair_row && aligned16(x), "rhp_permute_fp8: null or unaligned pointer");
+    const dim3 grid(row_blocks(T)), block(kThreads);
+    const bf16* xb = static_cast<const bf16*>(x);
+    if (f8 == kFmtE4m3)
+        hipLaunchKernelGGL(permute_fp8_kernel<kFmtE4m3>, grid, block, 0, stream, xb, T, h, k, pair_row, co);
+    else
+        hipLaunchKernelGGL(permute_fp8_kernel<kFmtE5m2>, grid, block, 0, stream, xb, T, h, k, pair_row, co);
+    return check_launch("permute_fp8_kernel");
+}
+
+extern "C" int rhp_combine_bwd_fp8(const void* dout, const void* y, const float* gates, const int32_t* pair_row,
+                                   int64_t T, int h, int k, float* dgates, int fmt, const float* history,
+                                   int hist_len, int margin, uint32_t* amax_bits, float* scale_inv, void* q,
+                                   hipStream_t stream) {
+    clear_error();
+    if (int rc = check_rows("rhp_combine_bwd_fp8", RHP_BF16, T, h, k)) return rc;
+    RHP_REQUIRE(fmt == RHP_E4M3 || fmt == RHP_E5M2, "rhp_combine_bwd_fp8: format must be RHP_E4M3 or RHP_E5M2");
+    const RowVariant rv = row_variant(k, 0);
+    RHP_REQUIRE(rv == RowVariant::kSmall || rv == RowVariant::kWide, "rhp_combine_bwd_fp8: top-k above 8");
+    if (T == 0) return 0;
+    int f8;
+    CodeOut co;
+    if (int rc = code_out("rhp_combine_bwd_fp8", fmt, q, history, hist_len, margin, amax_bits, scale_inv, f8, co))
+        return rc;
+    RHP_REQUIRE(dout && gates && pair_row && dgates && aligned16(dout) && (y == nullptr || aligned16(y)),
+                "rhp_combine_bwd_fp8: null or unaligned pointer");
+    const dim3 grid(row_blocks(T)), block(kThreads);
+    const bf16* db = static_cast<const bf16*>(dout);
+    const bf16* yb = static_cast<const bf16*>(y);
+#define RHP_CBQ(KM, U, F)                                                                                       \
+    hipLaunchKernelGGL((combine_bwd_bf16_kernel<KM, U, F>), grid, block, 0, stream, db, yb, gates, pair_row, T, h, \
+                       k, nullptr, dgates, co)
+    if (rv == RowVariant::kSmall) {
+        if (f8 == kFmtE4m3) RHP_CBQ(2, 8, kFmtE4m3);
+        else RHP_CBQ(2, 8, kFmtE5m2);
+    } else {
+        if (f8 == kFmtE4m3) RHP_CBQ(8, 2, kFmtE4m3);
+        else RHP_CBQ(8, 2, kFmtE5m2);
+    }
+#undef RHP_CBQ
+    return check_launch("combine_bwd_bf16_kernel");
 }
 
 extern "C" int rhp_token_bwd(const void* dout, const void* dxp, const int32_t* pair_row, const void* dlogits_sel,

@@ -136,15 +136,29 @@ class Fp8State:
                    self.scale_inv[i:i + 1], q, qt, self.margin)
         return q, qt
 
-    def cast_weights(self, fc1s: list[torch.Tensor], fc2s: list[torch.Tensor]) -> tuple[list, list]:
-        """Row-major e4m3 codes of every local expert's two weights, each with its own scale, in one launch."""
-        ws = list(fc1s) + list(fc2s)
-        rows = [self.w1(g) for g in range(self.G)] + [self.w2(g) for g in range(self.G)]
+    def permute(self, i: int, x: torch.Tensor, pair_row: torch.Tensor, k: int, rows: int) -> torch.Tensor:
+        """Row-major codes of the permuted rows of ``x`` cast as tensor i, without the bf16 rows: the codes
+        that ``cast`` gives for ``K.permute(x, pair_row, k, rows)`` when every row is filled."""
+        return K.permute_fp8(x, pair_row, k, rows, self.history[i], FORMATS.get(i, "e4m3"), self.amax[i:i + 1],
+                             self.scale_inv[i:i + 1], self.margin)
+
+    def combine_bwd(self, i: int, dout: torch.Tensor, y: torch.Tensor, gates: torch.Tensor, pair_row: torch.Tensor,
+                    rows: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """``K.combine_bwd`` with the row gradients cast as tensor i: (row-major codes, gate gradients)."""
+        return K.combine_bwd_fp8(dout, y, gates, pair_row, rows, self.history[i], FORMATS.get(i, "e4m3"),
+                                 self.amax[i:i + 1], self.scale_inv[i:i + 1], self.margin)
+
+    def weight_codes(self, ws: list[torch.Tensor]) -> list[torch.Tensor]:
+        """Uninitialised row-major e4m3 code buffers for expert weights (``cast_weights`` fills them)."""
         fdt = K.FP8_FORMATS["e4m3"][1]
-        qs = [torch.empty(w.shape, dtype=fdt, device=w.device) for w in ws]
-        K.fp8_cast_many(ws, [self.history[i] for i in rows], "e4m3", [self.amax[i:i + 1] for i in rows],
+        return [torch.empty(w.shape, dtype=fdt, device=w.device) for w in ws]
+
+    def cast_weights(self, which: str, ws: list[torch.Tensor], qs: list[torch.Tensor]) -> None:
+        """Row-major e4m3 codes of every local expert's fc1 (``which`` = "fc1") or fc2 weight into ``qs``, each
+        with its own scale, in one launch."""
+        rows = [self.w1(g) if which == "fc1" else self.w2(g) for g in range(self.G)]
+        K.fp8_cast_many(list(ws), [self.history[i] for i in rows], "e4m3", [self.amax[i:i + 1] for i in rows],
                         [self.scale_inv[i:i + 1] for i in rows], qs, self.margin)
-        return qs[:self.G], qs[self.G:]
 
     def gemm_cast(self, i: int, epi: str, offsets: torch.Tensor, poff: torch.Tensor, rows_cap: int,
                   ys: list[torch.Tensor], y_fmt: str, xs: list[torch.Tensor], N: int, K_: int, f: int,

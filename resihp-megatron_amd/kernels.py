@@ -660,6 +660,46 @@ def fp8_cast_many(xs: list[torch.Tensor], histories: list[torch.Tensor], fmt: st
           _arr(scale_invs), _arr(qs))
 
 
+def _code_state(history, amax_bits, scale_inv):
+    _expect(history.dtype == torch.float32 and history.dim() == 1, "history must be float32 [L]")
+    _expect(amax_bits.dtype == torch.int32 and amax_bits.numel() == 1, "amax_bits must be int32 [1]")
+    _expect(scale_inv.dtype == torch.float32 and scale_inv.numel() == 1, "scale_inv must be float32 [1]")
+
+
+def permute_fp8(x: torch.Tensor, pair_row: torch.Tensor, k: int, rows: int, history: torch.Tensor, fmt: str,
+                amax_bits: torch.Tensor, scale_inv: torch.Tensor, margin: int = 0) -> torch.Tensor:
+    """fp8 codes of ``permute(x, pair_row, k, rows)``, cast with the delayed scale of ``history`` in one pass."""
+    dev = _need_cuda(x, pair_row, history, amax_bits, scale_inv)
+    code, fdt, _ = FP8_FORMATS[fmt]
+    _expect(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x must be contiguous bf16 [T, h]")
+    T, h = x.shape
+    _index(pair_row, "pair_row", (T * k,))
+    _code_state(history, amax_bits, scale_inv)
+    q = torch.empty(max(rows, 1), h, dtype=fdt, device=dev)   # a valid address also without rows
+    _call("rhp_permute_fp8", dev, _ptr(x), T, h, k, _ptr(pair_row), code, _ptr(history), history.numel(), margin,
+          _ptr(amax_bits), _ptr(scale_inv), _ptr(q))
+    return q[:rows]
+
+
+def combine_bwd_fp8(dout: torch.Tensor, y: torch.Tensor, gates: torch.Tensor, pair_row: torch.Tensor, rows: int,
+                    history: torch.Tensor, fmt: str, amax_bits: torch.Tensor, scale_inv: torch.Tensor,
+                    margin: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """``combine_bwd`` with dy leaving as fp8 codes (the cast of its bf16 rows): (dy codes, dgates)."""
+    dev = _need_cuda(dout, y, gates, pair_row, history, amax_bits, scale_inv)
+    code, fdt, _ = FP8_FORMATS[fmt]
+    _expect(dout.dtype == torch.bfloat16 and gates.dtype == torch.float32, "bf16 rows and float32 gates")
+    T, h = dout.shape
+    k = gates.shape[1]
+    _index(pair_row, "pair_row", (T * k,))
+    _expect(_rows_of(y, "y", h, dout.dtype) >= rows, "y has fewer rows than the plan")
+    _code_state(history, amax_bits, scale_inv)
+    q = torch.empty(max(rows, 1), h, dtype=fdt, device=dev)
+    dgates = torch.empty_like(gates)
+    _call("rhp_combine_bwd_fp8", dev, _ptr(dout), _ptr(y), _ptr(gates), _ptr(pair_row), T, h, k, _ptr(dgates), code,
+          _ptr(history), history.numel(), margin, _ptr(amax_bits), _ptr(scale_inv), _ptr(q))
+    return q[:rows], dgates
+
+
 def fp8_amax_roll(history: torch.Tensor, amax_bits: torch.Tensor) -> None:
     """End of iteration: every history gets its pending amax prepended (newest first); the amax resets."""
     dev = _need_cuda(history, amax_bits)

@@ -117,40 +117,63 @@ def expert_backward(dys, acts, hpres, offsets, rows_from_offsets: bool, rows_cap
     main.wait_stream(side)
 
 
-def _fp8_forward(st: Fp8State, meta: LayerMeta, offsets, P, xp, fc1s, fc2s, hpre, y):
-    """Expert FFN forward in fp8; returns what the backward needs (the row-major codes).
+def _fp8_weight_casts(st: Fp8State, fc1s, fc2s, main: torch.cuda.Stream):
+    """Starts the casts of the expert weights on the side stream: fc1's while the routing, dispatch and
+    permute run, fc2's while fc1's product runs.  Returns the code buffers and the events that mark them
+    written (the buffers are allocated on the caller's stream, which waits for the events before use)."""
+    w1q, w2q = st.weight_codes(fc1s), st.weight_codes(fc2s)
+    side = _side_stream(main.device)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        st.cast_weights("fc1", fc1s, w1q)
+        ev1 = torch.cuda.Event()
+        ev1.record(side)
+        st.cast_weights("fc2", fc2s, w2q)
+        ev2 = torch.cuda.Event()
+        ev2.record(side)
+    return w1q, w2q, ev1, ev2
+
+
+def _fp8_forward(st: Fp8State, meta: LayerMeta, offsets, P, xq, fc1s, fc2s, hpre, y, wcast):
+    """Expert FFN forward in fp8 on the permuted input's codes ``xq``; returns what the backward needs
+    (the row-major codes).
 
     The fc1 product's epilogue casts the activation straight to fp8 (no bf16 activation rows).  Every
     operand is kept as row-major codes only: the backward products read them N-contiguous and transpose
     in LDS (fp8 product modes 2 and 3).
     """
     G, f = st.G, meta.ffn
-    h = xp.shape[1]
-    w1q, w2q = st.cast_weights(fc1s, fc2s)
+    h = xq.shape[1]
+    w1q, w2q, ev1, ev2 = wcast
+    main = torch.cuda.current_stream(xq.device)
     sw1 = st.scale_inv[st.w1(0):st.w1(0) + G]
     sw2 = st.scale_inv[st.w2(0):st.w2(0) + G]
-    # The casts tile each expert's rows in blocks of 128 (the padded offsets); no transposed copy is written.
+    # The product casts tile each expert's rows in blocks of 128 (the padded offsets); no transposed copy
+    # is written.
     poff = K.fp8_padded_offsets(offsets)
-    xq = aq = None
+    aq = None
     if P > 0:
-        xq, _ = st.cast(X, xp, offsets, poff, P, transposed=False)
         epi = "swiglu_fwd" if meta.act == "swiglu" else "gelu_fwd"
+        main.wait_event(ev1)
         aq, _ = st.gemm_cast(ACT, epi, offsets, poff, P, [xq] * G, "e4m3", w1q, f, h, f, st.scale_inv[X:X + 1],
                              sw1, cs=[hpre] * G, transposed=False)
+        main.wait_event(ev2)
         K.fp8_gemm(0, "store", offsets, P, [aq] * G, "e4m3", w2q, "e4m3", h, f, 0, f, [y] * G,
                    st.scale_inv[ACT:ACT + 1], sw2)
+    main.wait_event(ev2)   # the weight casts are complete (and their amax raised) before the layer returns
     return dict(poff=poff, xq=xq, aq=aq, w1q=w1q, w2q=w2q, sw1=sw1, sw2=sw2)
 
 
-def _fp8_backward(st: Fp8State, q8: dict, meta: LayerMeta, offsets, P, dy, hpre, dxp, dw1, dw2):
-    """Expert FFN backward in fp8 (e5m2 gradients, e4m3 weights and activations).
+def _fp8_backward(st: Fp8State, q8: dict, meta: LayerMeta, offsets, P, dyq, hpre, dxp, dw1, dw2):
+    """Expert FFN backward in fp8 (e5m2 gradients, e4m3 weights and activations) from the codes ``dyq`` of
+    the output rows' gradient.
 
     The fc2 input-gradient product's epilogue casts the pre-activation gradient straight to fp8.  The
     input-gradient products read the row-major weight codes as [K, N] (mode 2) and the weight gradients
     the row-major activation and gradient codes (mode 3).
     """
     G, f = st.G, meta.ffn
-    h = dy.shape[1]
+    h = dyq.shape[1]
     F1 = _fc1_rows(meta.act, f)
     if P == 0:
         for w in (*dw1, *dw2):
@@ -158,7 +181,6 @@ def _fp8_backward(st: Fp8State, q8: dict, meta: LayerMeta, offsets, P, dy, hpre,
         return
     s = st.scale_inv
     poff = q8["poff"]
-    dyq, _ = st.cast(DY, dy, offsets, poff, P, transposed=False)
     epi = "swiglu_bwd" if meta.act == "swiglu" else "gelu_bwd"
     dhq, _ = st.gemm_cast(DH, epi, offsets, poff, P, [dyq] * G, "e5m2", q8["w2q"], f, h, f, s[DY:DY + 1],
                           q8["sw2"], auxs=[hpre] * G, transposed=False, x_kn=True)
@@ -199,19 +221,24 @@ class _MoELayerFn(torch.autograd.Function):
             with torch.cuda.stream(side):
                 K.expert_fc1_fwd([x] * S, shared_off, False, T, sfc1s, fs, meta.act, shared_h, shared_a)
                 K.expert_fc2_fwd(shared_a, shared_off, False, T, sfc2s, shared_y)
+        # fp8 experts (never with shared experts): the weight casts start now, on the side stream.
+        wcast = _fp8_weight_casts(fp8, fc1s, fc2s, main) if fp8 is not None else None
         logits, topi, gates = K.route(x, router_w, bias, k, meta.score, meta.normalize, meta.gate_scale)
         plan = K.dispatch(topi, meta.num_experts, e0, e1, meta.n_src)
         # The reference materialises counts on the host here too (moe.py:210-211);
         # with every expert local the row count is known without a sync.
         P = T * k if meta.full else int(plan.offsets[-1].item())
         F1 = _fc1_rows(meta.act, f)
-        xp = K.permute(x, plan.pair_row, k, P)
+        # fp8 experts read only the input rows' codes: the permute writes them instead of bf16 rows.
+        xp = K.permute(x, plan.pair_row, k, P) if fp8 is None else x.new_empty(0, h)
         hpre = x.new_empty(P, F1)
         act = x.new_empty(0 if fp8 is not None else P, f)   # the fp8 path keeps only the activation's codes
         y = x.new_empty(P, h)
         q8 = None
         if fp8 is not None:
-            q8 = _fp8_forward(fp8, meta, plan.offsets, P, xp, fc1s, fc2s, hpre, y)
+            xq = fp8.permute(X, x, plan.pair_row, k, P)
+            q8 = _fp8_forward(fp8, meta, plan.offsets, P, xq, fc1s, fc2s, hpre, y, wcast)
+            q8["xq"] = xq
         elif P > 0:
             K.expert_fc1_fwd([xp] * G, plan.offsets, True, P, fc1s, f, meta.act, [hpre] * G, [act] * G)
             K.expert_fc2_fwd([act] * G, plan.offsets, True, P, fc2s, [y] * G)
@@ -258,7 +285,11 @@ class _MoELayerFn(torch.autograd.Function):
             with torch.cuda.stream(side):
                 K.expert_fc2_bwd([dout] * S, shared_a, shared_h, shared_off, False, T, list(sfc2s), meta.act, dh, sdw2)
                 K.expert_fc1_bwd(dh, [x] * S, shared_off, False, T, list(sfc1s), fs, meta.act, shared_dx or None, sdw1)
-        dy, dgates = K.combine_bwd(dout, y, gates, pair_row, P)
+        fp8, q8 = ctx.fp8
+        if fp8 is None:
+            dy, dgates = K.combine_bwd(dout, y, gates, pair_row, P)
+        else:   # the fp8 products read only the codes of the rows' gradient
+            dy, dgates = fp8.combine_bwd(DY, dout, y, gates, pair_row, P)
         dl = K.route_bwd(dgates, gates, logits, topi, meta.score, meta.normalize, meta.gate_scale)
         # With every expert local each routed slot has a row, so fc1's input-gradient product can add the
         # router term to its rows (the token backward then sums it with the rows).
@@ -267,7 +298,6 @@ class _MoELayerFn(torch.autograd.Function):
         dw2 = [torch.empty_like(w) for w in fc2s]
         dw1 = [torch.empty_like(w) for w in fc1s]
         dxp = x.new_empty(P, h) if need_x else None
-        fp8, q8 = ctx.fp8
         if fp8 is not None:
             _fp8_backward(fp8, q8, meta, offsets, P, dy, hpre, dxp, dw1, dw2)
         elif P > 0:

@@ -403,3 +403,60 @@ def test_cast_many_equals_one_cast_per_tensor():
         if shapes[i][0]:
             _same_bits(q_m[i], q, f"codes of tensor {i}")
         assert amax_m[i].item() == a.item() and sinv_m[i].item() == si.item(), f"amax / scale of tensor {i}"
+
+
+# (T, h, k, E, window): k <= 2 and k <= 8 variants, one or several 64-lane passes, slots of other devices.
+ROW_CODE_CASES = [(300, 4096, 2, 8, (0, 8)), (97, 2048, 6, 16, (4, 12)), (64, 1024, 8, 8, (0, 8)),
+                  (33, 192, 1, 4, (1, 3)), (0, 256, 2, 8, (0, 8)), (5, 256, 1, 64, (63, 64))]
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("case", ROW_CODE_CASES, ids=lambda c: f"T{c[0]}-h{c[1]}-k{c[2]}-E{c[3]}")
+def test_row_kernels_emit_the_codes_of_the_cast(case, fmt):
+    """rhp_permute_fp8 / rhp_combine_bwd_fp8 equal rhp_permute / rhp_combine_bwd followed by rhp_fp8_cast of
+    the bf16 rows they would store: codes, amax and 1/scale bit for bit; dgates too."""
+    from oracle import route_c as R
+
+    T, h, k, E, (e0, e1) = case
+    g = torch.Generator().manual_seed(7)
+    topi = torch.sort(torch.randn(max(T, 1), E, generator=g), dim=1, descending=True).indices[:T, :k]
+    plan = R.dispatch(topi.to(torch.int32).numpy(), E, e0, e1, 1)
+    P = int(plan["offsets"][-1])
+    pair_row = torch.from_numpy(plan["pair_row"].astype("int32")).to(DEV)
+    off = torch.from_numpy(plan["offsets"].astype("int32")).to(DEV)
+    x = seeded((T, h), 21, 1.0, torch.bfloat16).to(DEV)
+    dout = seeded((T, h), 22, 1.0, torch.bfloat16).to(DEV)
+    y = seeded((P, h), 23, 1.0, torch.bfloat16).to(DEV)
+    gates = seeded((T, k), 24, 0.5, torch.float32).abs().to(DEV)
+    hist = _history(25, scale=2.0).to(DEV)
+    say(f"fp8 row codes {fmt} T={T} h={h} k={k} E={E} window={(e0, e1)} P={P}")
+    fdt = K.FP8_FORMATS[fmt][1]
+    poff = K.fp8_padded_offsets(off)
+    state = lambda: (torch.zeros(1, dtype=torch.int32, device=DEV),  # noqa: E731
+                     torch.zeros(1, dtype=torch.float32, device=DEV))
+
+    a1, s1 = state()
+    q1 = K.permute_fp8(x, pair_row, k, P, hist, fmt, a1, s1)
+    a2, s2 = state()
+    q2 = torch.empty(P, h, dtype=fdt, device=DEV)
+    xp = K.permute(x, pair_row, k, P)
+    if P:
+        K.fp8_cast(xp, off, poff, P, hist, fmt, a2, s2, q2, None)
+    torch.cuda.synchronize()
+    _same_bits(q1, q2, "permute codes")
+    assert a1.item() == a2.item(), "permute amax"
+    if P:
+        assert s1.item() == s2.item(), "permute 1/scale"
+
+    a1, s1 = state()
+    q1, dg1 = K.combine_bwd_fp8(dout, y, gates, pair_row, P, hist, fmt, a1, s1)
+    a2, s2 = state()
+    dy, dg2 = K.combine_bwd(dout, y, gates, pair_row, P)
+    if P:
+        K.fp8_cast(dy, off, poff, P, hist, fmt, a2, s2, q2, None)
+    torch.cuda.synchronize()
+    _same_bits(q1, q2, "combine backward codes")
+    assert torch.equal(dg1, dg2), "dgates"
+    assert a1.item() == a2.item(), "combine backward amax"
+    if P:
+        assert s1.item() == s2.item(), "combine backward 1/scale"
