@@ -139,7 +139,8 @@ constexpr size_t kSplitBytes = kSplitPartBytes + kSplitSlots * sizeof(int32_t);
 
 enum TileFound { kTileDone = 0, kTileOk = 1, kTileSkip = 2 };
 
-constexpr int kWgradPanel = 4;   // row tiles per panel of the K-grouped tile order
+constexpr int kWgradPanel = 6;   // row tiles per panel of the K-grouped tile order
+constexpr int kRowPanel = 8;     // most row tiles per panel of the row-grouped tile order
 
 // Blocks of a K-grouped (weight-gradient) launch of G groups of per_group
 // tiles each: XCD x runs tiles [x per_group / 8, (x + 1) per_group / 8) of
@@ -175,10 +176,11 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
         t->g = static_cast<int>(j / n);
         const int rem = lo + static_cast<int>(j % n);
         // Within a group, panels of kWgradPanel row tiles, column tiles outer
-        // within a panel: the 32 tiles one XCD runs at a time then span 4 row
-        // and 8 column tiles, 12 operand blocks per K step (a row-major order
-        // spans 1-2 rows and 16-32 columns, up to 34 blocks, which the XCD's
-        // L2 cannot keep, and the products fetched 9x their operands).
+        // within a panel: the 32 tiles one XCD runs at a time then span 6 row
+        // and 5-6 column tiles, 11-12 operand blocks per K step (a row-major
+        // order spans 1-2 rows and 16-32 columns, up to 34 blocks, which the
+        // XCD's L2 cannot keep, and the products fetched 9x their operands;
+        // panels of 4 rows measured 0.3-0.8 % slower, of 2 or 8 no better).
         const int full = yt_n / kWgradPanel, in_full = full * kWgradPanel * xt_n;
         int yt, xt;
         if (rem < in_full) {
@@ -253,7 +255,26 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
         const int mt = (M + yt_rows - 1) / yt_rows;
         const uint32_t n_tiles = static_cast<uint32_t>(mt) * xt_n;
         if (L < n_tiles) {
-            const int xt = L / mt, yt = L % mt;
+            // Panels of at most kRowPanel row tiles (of balanced height), column
+            // tiles outer within a panel: the 32 consecutive tiles an XCD runs at
+            // a time then span 5-8 row tiles by 4-6 column tiles instead of a
+            // whole expert's row tiles by 1-2 columns (fp8 Mixtral: 17 row tiles,
+            // the EP-128 share: 55), so fewer operand blocks per K step leave L2
+            // (measured: EP-128 share +7.7 %, fp8 Mixtral +2 %; at most 4 or 12
+            // rows a panel no better).
+            int xt, yt;
+            const int np = (mt + kRowPanel - 1) / kRowPanel;
+            const int R = (mt + np - 1) / np;
+            const uint32_t full = static_cast<uint32_t>(mt / R), band = static_cast<uint32_t>(R * xt_n);
+            if (L < full * band) {
+                const uint32_t r = L % band;
+                xt = static_cast<int>(r / R);
+                yt = static_cast<int>((L / band) * R + r % R);
+            } else {
+                const uint32_t py = static_cast<uint32_t>(mt) - full * R, r = L - full * band;   // the last panel
+                xt = static_cast<int>(r / py);
+                yt = static_cast<int>(full * R + r % py);
+            }
             t->g = g;
             t->x0 = xt * xt_cols;
             t->x_lim = p.N - t->x0;
