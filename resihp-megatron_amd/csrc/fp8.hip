@@ -450,20 +450,23 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
 
     const int nk = (t.k_end - t.k_begin + kF8K - 1) / kF8K;
     const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
-    // X (Y) tile of step `step` into slot `slot`; past the last step, zeros.
-    auto issue_x = [&](int step, int slot) {
+    // Loads [j0, j1) of this wave's share of the X (Y) tile of step `step`
+    // into slot `slot`; past the last step, zeros.
+    auto issue_x = [&](int step, int slot, int j0 = 0, int j1 = kF8PerWave) {
         const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kF8K);
         const uint32_t soff = step < nk ? (kXMN ? k0 * xstep : k0) : kF8PastView;
         const uint32_t base = lds0 + slot * kF8TileBytes + wave * 1024;
 #pragma unroll
-        for (int j = 0; j < kF8PerWave; ++j) dma16(rx, mx.vo[j], soff, base + j * kWaves * 1024);
+        for (int j = 0; j < kF8PerWave; ++j)
+            if (j >= j0 && j < j1) dma16(rx, mx.vo[j], soff, base + j * kWaves * 1024);
     };
-    auto issue_y = [&](int step, int slot) {
+    auto issue_y = [&](int step, int slot, int j0 = 0, int j1 = kF8PerWave) {
         const uint32_t k0 = static_cast<uint32_t>(t.k_begin + step * kF8K);
         const uint32_t soff = step < nk ? (kYMN ? k0 * ystep : k0) : kF8PastView;
         const uint32_t base = lds0 + slot * kF8TileBytes + wave * 1024;
 #pragma unroll
-        for (int j = 0; j < kF8PerWave; ++j) dma16(ry, my.vo[j], soff, base + j * kWaves * 1024);
+        for (int j = 0; j < kF8PerWave; ++j)
+            if (j >= j0 && j < j1) dma16(ry, my.vo[j], soff, base + j * kWaves * 1024);
     };
     // vmcnt(n loads of this wave) lgkmcnt(0).
     auto wait_lds = [](auto n_c) {
@@ -488,10 +491,13 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
     auto read_frags = [&](FragSet& f, uint32_t sx, uint32_t sy, int b) {
         const uint8_t* xt = lds + sx;
         const uint8_t* yt = lds + sy;
+        // In the order the MFMAs consume them (X0 with every Y, then X1 ..), so
+        // each MFMA waits only for its own fragments.
+        f[0] = kXMN ? f8_frag_mn(xt, mx.fr[0], b) : f8_frag(xt, mx.fr[0], b);
 #pragma unroll
         for (int j = 0; j < kFragY; ++j) f[4 + j] = kYMN ? f8_frag_mn(yt, my.fr[j], b) : f8_frag(yt, my.fr[j], b);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = kXMN ? f8_frag_mn(xt, mx.fr[i], b) : f8_frag(xt, mx.fr[i], b);
+        for (int i = 1; i < 4; ++i) f[i] = kXMN ? f8_frag_mn(xt, mx.fr[i], b) : f8_frag(xt, mx.fr[i], b);
     };
     auto mfmas = [&](const FragSet& f) {
 #pragma unroll
@@ -500,6 +506,41 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
             for (int j = 0; j < kFragY; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[i], f[4 + j], acc[i][j], XF, YF, 0, 127,
                                                                            0, 127);
+    };
+    auto read_one = [&](FragSet& f, uint32_t sx, uint32_t sy, int b, int n) {
+        if (n >= 4)
+            f[n] = kYMN ? f8_frag_mn(lds + sy, my.fr[n - 4], b) : f8_frag(lds + sy, my.fr[n - 4], b);
+        else
+            f[n] = kXMN ? f8_frag_mn(lds + sx, mx.fr[n], b) : f8_frag(lds + sx, mx.fr[n], b);
+    };
+    // The block after the barrier: the MFMAs of f (X fragment q with every Y
+    // fragment in quarter q), the reads of the next step's first block into g
+    // in the order its MFMAs use them, and the step's eight tile loads, two
+    // per quarter (Y first, so the wait before the next barrier still leaves
+    // exactly the X loads in flight): the loads reach the address unit at the
+    // rate it drains them instead of stalling every wave behind a burst.
+    auto block_after_barrier = [&](const FragSet& f, FragSet& g, uint32_t sx, uint32_t sy, int ly_step, int ly_slot,
+                                   int lx_step, int lx_slot) {
+        static_assert(kFragY == 2 && kF8PerWave == 4, "two Y fragments, four loads per tile and wave");
+        constexpr int order[6] = {0, 4, 5, 1, 2, 3};   // X0, Y0, Y1, X1, X2, X3
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (q < 2) {
+                read_one(g, sx, sy, 0, order[2 * q]);
+                read_one(g, sx, sy, 0, order[2 * q + 1]);
+            } else {
+                read_one(g, sx, sy, 0, order[q + 2]);
+            }
+#pragma unroll
+            for (int j = 0; j < kFragY; ++j)
+                acc[q][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[4 + j], acc[q][j], XF, YF, 0, 127,
+                                                                           0, 127);
+            if (q < 2)
+                issue_y(ly_step, ly_slot, 2 * q, 2 * q + 2);
+            else
+                issue_x(lx_step, lx_slot, 2 * (q - 2), 2 * (q - 2) + 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
     constexpr int kReads = (kXMN ? 4 : 2) * 4 + (kYMN ? 4 : 2) * kFragY;   // LDS reads of a block's fragments
     using Pending = std::integral_constant<int, kF8PerWave>;   // one operand tile stays in flight
@@ -524,6 +565,12 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
             }
         } else {
             read_frags(fa, 0, kF8TileBytes, 0);
+            // lgkmcnt(0): the loop's first block then waits only for the
+            // fragments it uses.  With these reads still counted on entry, the
+            // compiler's wait analysis, which merges the entry and the loop's own
+            // back edge, loses their order and waits for every read at the top
+            // of each step.
+            __builtin_amdgcn_s_waitcnt(0xc07f);
             // Slots of X and Y of step kt (sx, sy) and of step kt + 1 (nx, ny).
             int sx = 0, sy = 1, nx = 2, ny = 3;
             for (int kt = 0; kt < nk; ++kt) {
@@ -533,11 +580,7 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
                 // Steps up to kt + 1 complete, every read of slots sx and sy done.
                 wait_lds(Pending{});
                 barrier();
-                issue_y(kt + 2, sx);
-                issue_x(kt + 3, sy);
-                read_frags(fa, nx * kF8TileBytes, ny * kF8TileBytes, 0);
-                mfmas(fb);
-                interleave_reads<0, 4 * kFragY, kReads>();
+                block_after_barrier(fb, fa, nx * kF8TileBytes, ny * kF8TileBytes, kt + 2, sx, kt + 3, sy);
                 sx = nx;
                 sy = ny;
                 nx = ny + 1 == kF8Slots ? 0 : ny + 1;

@@ -321,6 +321,12 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
             }
         } else {
             read_frags(fa, 0, kT64Bytes, 0);
+            // lgkmcnt(0): the loop's first block then waits only for the
+            // fragments it uses.  With these reads still counted on entry, the
+            // compiler's wait analysis, which merges the entry and the loop's own
+            // back edge, loses their order and waits for every read at the top
+            // of each step.
+            __builtin_amdgcn_s_waitcnt(0xc07f);
             // Slots of X and Y of step kt (sx, sy), of step kt + 1 (nx, ny),
             // and the slot that receives X of step kt + 2 (fx).  Two loads go
             // with each block: the second half of Y of step kt + 1 (block 0),
