@@ -174,6 +174,12 @@ __global__ __launch_bounds__(256) void fp8_cast_kernel(CastParams c) {
 // arguments).  The loads, the quantisation and the stores are those of
 // fp8_cast_kernel, so the codes, amax and 1 / scale are the same bits.
 constexpr int kCastMany = 32;   // tensors per launch
+// Rows of one block's tile in the batched cast (4 loads of 16 bytes per
+// thread): measured on the 16 Mixtral weights, 64-row tiles ran 3 % faster
+// than 128-row ones and 8 % faster than 256-row ones.
+constexpr int kManyRows = 64;
+constexpr int kManyLoads = kManyRows / 16;   // 16-byte loads in flight per thread
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 struct CastManyParams {
     struct Tensor {
@@ -205,18 +211,23 @@ __global__ __launch_bounds__(256) void fp8_cast_many_kernel(CastManyParams c) {
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int col = ct * kCastCols + 8 * (lane & 15);
     const bool col_ok = col < T.cols;
-    const int r0 = 32 * w + (lane >> 4);
+    const int r0 = (kManyRows / 4) * w + (lane >> 4);
     const float lim = fp8_max(FMT);
     float m = 0.0f;
-    uint4 u[8];
+    uint4 u[kManyLoads];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int row = rt * kCastRows + r0 + 4 * k;
+    for (int k = 0; k < kManyLoads; ++k) {
+        const int row = rt * kManyRows + r0 + 4 * k;
         u[k] = make_uint4(0u, 0u, 0u, 0u);
-        if (col_ok && row < T.rows) u[k] = *reinterpret_cast<const uint4*>(T.x + static_cast<int64_t>(row) * T.cols + col);
+        if (col_ok && row < T.rows) {
+            // read once: non-temporal, so the weights do not displace the operands the GEMMs beside it reuse
+            const u32x4_t v = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4_t*>(T.x + static_cast<int64_t>(row) * T.cols + col));
+            u[k] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < kManyLoads; ++k) {
         const uint32_t wd[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
         float v[8];
 #pragma unroll
@@ -229,7 +240,7 @@ __global__ __launch_bounds__(256) void fp8_cast_many_kernel(CastManyParams c) {
             m = fmaxf(m, fabsf(v[e]));
             v[e] = fminf(fmaxf(v[e] * scale, -lim), lim);
         }
-        const int row = rt * kCastRows + r0 + 4 * k;
+        const int row = rt * kManyRows + r0 + 4 * k;
         if (col_ok && row < T.rows)
             *reinterpret_cast<uint2*>(T.q + static_cast<int64_t>(row) * T.cols + col) =
                 make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7]));
@@ -742,7 +753,7 @@ extern "C" int rhp_fp8_cast_many(int n, const void* const* x, const int64_t* row
             c.t[j].cols = static_cast<int>(cols[i]);
             c.t[j].block0 = static_cast<uint32_t>(blocks);
             // At least one block a tensor, so that an empty tensor still gets its 1 / scale.
-            blocks += std::max<int64_t>(1, (rows[i] + kCastRows - 1) / kCastRows) * ((cols[i] + kCastCols - 1) / kCastCols);
+            blocks += std::max<int64_t>(1, (rows[i] + kManyRows - 1) / kManyRows) * ((cols[i] + kCastCols - 1) / kCastCols);
             RHP_REQUIRE(blocks < (int64_t(1) << 31), "rhp_fp8_cast_many: too many tiles");
         }
         if (blocks == 0) continue;
