@@ -261,7 +261,14 @@ size_t rhp_expert_split_workspace_bytes(void);
  * stream): before its first use, and after a call that did not complete. */
 int rhp_expert_split_workspace_reset(void* split_ws, size_t split_ws_bytes, hipStream_t stream);
 
-/* hpre[r] = xp[r] @ w1^T  ([M_g, F1]);  act[r] = silu(gate) * up  or  gelu(hpre)  ([M_g, f]). */
+/*
+ * h = xp[r] @ w1^T  ([M_g, F1]);  act[r] = silu(gate) * up  or  gelu(h)  ([M_g, f]);
+ * hpre[r] = what the backward of the activation needs: for SwiGLU the two
+ * factors of the activation gradient, [up * silu'(gate) | silu(gate)]
+ * ([M_g, 2f], gate = h[:, :f], up = h[:, f:]; the forward has the sigmoid at
+ * hand, and the backward then costs two products per element); for GELU the
+ * pre-activation h itself.
+ */
 int rhp_expert_fc1_fwd(int G, const int32_t* offsets, int rows_from_offsets, int64_t rows_cap, int dtype, int act,
                        int h, int f, const void* const* xp, const void* const* w1, void* const* hpre,
                        void* const* act_out, void* split_ws, size_t split_ws_bytes, hipStream_t stream);
@@ -273,7 +280,8 @@ int rhp_expert_fc2_fwd(int G, const int32_t* offsets, int rows_from_offsets, int
 
 /*
  * Backward through fc2 and the activation:
- *   dact = dy @ w2;  dhpre = activation backward of dact at hpre  ([M_g, F1])
+ *   dact = dy @ w2;  dhpre = activation backward of dact from hpre  ([M_g, F1]):
+ *   SwiGLU [dact * hpre[:, :f] | dact * hpre[:, f:]], GELU dact * gelu'(hpre)
  *   dw2[g] = dy_g^T @ act_g  ([h, f])      (written, not accumulated)
  * dhpre may be NULL to skip the input-gradient product (then hpre and w2 are
  * not read), or dw2 NULL to skip the weight gradient, not both.  The two
@@ -446,7 +454,8 @@ int rhp_fp8_amax_roll(float* history, uint32_t* amax_bits, int n, int hist_len, 
  * modes 0 and 1 need transposed copies, with the same sums bit for bit:
  *   mode 0: out[r, n] = sum_k y[g][r, k] x[g][n, k] for the rows r of expert g
  *                (offsets; y[g] holds all rows, row pitch ldy; x[g]: [N or 2f, K], pitch ldx).
- *                epi: 0 store, 1 SwiGLU forward (x rows [gate; up], out = hpre [.., 2f], c2 = act,
+ *                epi: 0 store, 1 SwiGLU forward (x rows [gate; up], out = hpre [.., 2f] as
+ *                rhp_expert_fc1_fwd writes it, c2 = act,
  *                N = f), 2 GELU forward (c2 = act), 3 SwiGLU backward, 4 GELU backward
  *                (aux = hpre); K a multiple of 128.
  *   mode 1: out_g[o, n] = sum_t y_g[o, t] x_g[n, t] over the R_g padded rows of expert g,

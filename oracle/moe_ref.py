@@ -455,9 +455,11 @@ def fp8_layer_emulation(x, router, fc1s, fc2s, topi, dout, scales, quantize_on: 
         hpb = bf(hp)
         dact = dyq @ w2q
         if act == "swiglu":
-            gg, uu = hpb[:, :f], hpb[:, f:]
+            # The forward stores the backward's factors [up silu'(gate) | silu(gate)] in bf16 (computed from
+            # the unrounded products), and the backward multiplies them by dact.
+            gg, uu = hp[:, :f], hp[:, f:]
             sg = torch.sigmoid(gg)
-            dh = bf(torch.cat([dact * uu * sg * (1 + gg * (1 - sg)), dact * gg * sg], 1))
+            dh = bf(torch.cat([dact * bf(uu * sg * (1 + gg * (1 - sg))), dact * bf(gg * sg)], 1))
         else:
             phi = torch.exp(-0.5 * hpb * hpb) / math.sqrt(2 * math.pi)
             dh = bf(dact * (0.5 * (1 + torch.erf(hpb / math.sqrt(2))) + hpb * phi))

@@ -96,6 +96,18 @@ __device__ __forceinline__ double dsilu_f(double g) {
     const double s = 1.0 / (1.0 + exp(-g));
     return s * (1.0 + g * (1.0 - s));
 }
+// SwiGLU saves for its backward the two factors the activation gradient is
+// multiplied by, not the pre-activation: [u silu'(g) | silu(g)] (the gate
+// rows' and the up rows' factor).  The forward has the sigmoid at hand, and
+// the backward then needs two products per element instead of a sigmoid.
+struct SwigluOut {
+    float act, fg, fu;   // silu(g) u, u silu'(g), silu(g)
+};
+__device__ __forceinline__ SwigluOut swiglu_fwd(float g, float u) {
+    const float s = sigmoid_fast(g);
+    const float si = g * s;
+    return {si * u, u * (s + si * (1.0f - s)), si};
+}
 __device__ __forceinline__ float gelu_f(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
 __device__ __forceinline__ double gelu_f(double v) { return 0.5 * v * (1.0 + erf(v * 0.70710678118654752440)); }
 __device__ __forceinline__ float dgelu_f(float v) {
@@ -554,10 +566,11 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
         for (int n = 0; n < kEpRows * 32 / NT; ++n, oh += sh, oa += sa) {
             const int r = rr + n * (NT / 32);
             const float4 gv = lds_f4(ep, r, xg), uv = lds_f4(ep, r, xg + 64);
-            view_store_bf16x4(hv, oh, 0, gv.x, gv.y, gv.z, gv.w);
-            view_store_bf16x4(hv, oh, up, uv.x, uv.y, uv.z, uv.w);
-            view_store_bf16x4(av, oa, 0, silu_f(gv.x) * uv.x, silu_f(gv.y) * uv.y, silu_f(gv.z) * uv.z,
-                              silu_f(gv.w) * uv.w);
+            const SwigluOut o0 = swiglu_fwd(gv.x, uv.x), o1 = swiglu_fwd(gv.y, uv.y), o2 = swiglu_fwd(gv.z, uv.z),
+                            o3 = swiglu_fwd(gv.w, uv.w);
+            view_store_bf16x4(hv, oh, 0, o0.fg, o1.fg, o2.fg, o3.fg);
+            view_store_bf16x4(hv, oh, up, o0.fu, o1.fu, o2.fu, o3.fu);
+            view_store_bf16x4(av, oa, 0, o0.act, o1.act, o2.act, o3.act);
         }
         return;
     }
@@ -587,18 +600,13 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
             view_store_bf16x4(ov, off, 0, v.x * dgelu_f(hv[0]), v.y * dgelu_f(hv[1]), v.z * dgelu_f(hv[2]),
                               v.w * dgelu_f(hv[3]));
         } else if (EPI == kEpiSwigluBwd) {
-            float gv[4], uv[4];
-            unpack_bf16x4(aux.v[n][0], gv);
-            unpack_bf16x4(aux.v[n][EPI == kEpiSwigluBwd ? 1 : 0], uv);
-            const float dv[4] = {v.x, v.y, v.z, v.w};
-            float dg[4], du[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                dg[e] = dv[e] * uv[e] * dsilu_f(gv[e]);
-                du[e] = dv[e] * silu_f(gv[e]);
-            }
-            view_store_bf16x4(ov, off, 0, dg[0], dg[1], dg[2], dg[3]);
-            view_store_bf16x4(ov, off, static_cast<uint32_t>(p.f * 2), du[0], du[1], du[2], du[3]);
+            // the saved factors [u silu'(g) | silu(g)] times the activation gradient
+            float fg[4], fu[4];
+            unpack_bf16x4(aux.v[n][0], fg);
+            unpack_bf16x4(aux.v[n][EPI == kEpiSwigluBwd ? 1 : 0], fu);
+            view_store_bf16x4(ov, off, 0, v.x * fg[0], v.y * fg[1], v.z * fg[2], v.w * fg[3]);
+            view_store_bf16x4(ov, off, static_cast<uint32_t>(p.f * 2), v.x * fu[0], v.y * fu[1], v.z * fu[2],
+                              v.w * fu[3]);
         }
     }
 }
@@ -713,10 +721,11 @@ __device__ __forceinline__ void epilogue_half_q(const Params& p, const Tile& t, 
         for (int n = 0; n < kN; ++n, oh += sh, oq += sq) {
             const int r = rr + n * (NT / 32);
             const float4 gv = lds_f4(ep, r, xg), uv = lds_f4(ep, r, xg + 64);
-            view_store_bf16x4(hv, oh, 0, gv.x, gv.y, gv.z, gv.w);
-            view_store_bf16x4(hv, oh, up, uv.x, uv.y, uv.z, uv.w);
-            const uint32_t code = quant4<QF>(silu_f(gv.x) * uv.x, silu_f(gv.y) * uv.y, silu_f(gv.z) * uv.z,
-                                             silu_f(gv.w) * uv.w, ok && r0 + r < t.y_lim, qa);
+            const SwigluOut o0 = swiglu_fwd(gv.x, uv.x), o1 = swiglu_fwd(gv.y, uv.y), o2 = swiglu_fwd(gv.z, uv.z),
+                            o3 = swiglu_fwd(gv.w, uv.w);
+            view_store_bf16x4(hv, oh, 0, o0.fg, o1.fg, o2.fg, o3.fg);
+            view_store_bf16x4(hv, oh, up, o0.fu, o1.fu, o2.fu, o3.fu);
+            const uint32_t code = quant4<QF>(o0.act, o1.act, o2.act, o3.act, ok && r0 + r < t.y_lim, qa);
             __builtin_amdgcn_raw_buffer_store_b32(code, qv, static_cast<int>(oq), 0, 0);
             if (p.qt) ep[code_word(r, threadIdx.x & 31)] = __uint_as_float(code);
         }
@@ -754,18 +763,11 @@ __device__ __forceinline__ void epilogue_half_q(const Params& p, const Tile& t, 
                                      v.w * dgelu_f(h[3]), valid, qa);
             } else {
                 static_assert(EPI == kEpiSwigluBwd, "quantising epilogues: SwiGLU / GELU, forward or backward");
-                float gv[4], uv[4];
-                unpack_bf16x4(aux.v[n][0], gv);
-                unpack_bf16x4(aux.v[n][kParts - 1], uv);
-                const float dv[4] = {v.x, v.y, v.z, v.w};
-                float dg[4], du[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    dg[e] = dv[e] * uv[e] * dsilu_f(gv[e]);
-                    du[e] = dv[e] * silu_f(gv[e]);
-                }
-                code[0] = quant4<QF>(dg[0], dg[1], dg[2], dg[3], valid, qa);
-                code[kParts - 1] = quant4<QF>(du[0], du[1], du[2], du[3], valid, qa);
+                float fg[4], fu[4];   // the saved factors [u silu'(g) | silu(g)]
+                unpack_bf16x4(aux.v[n][0], fg);
+                unpack_bf16x4(aux.v[n][kParts - 1], fu);
+                code[0] = quant4<QF>(v.x * fg[0], v.y * fg[1], v.z * fg[2], v.w * fg[3], valid, qa);
+                code[kParts - 1] = quant4<QF>(v.x * fu[0], v.y * fu[1], v.z * fu[2], v.w * fu[3], valid, qa);
             }
 #pragma unroll
             for (int pt = 0; pt < kParts; ++pt) {

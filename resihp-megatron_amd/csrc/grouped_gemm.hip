@@ -426,17 +426,17 @@ __global__ __launch_bounds__(256) void gg_simt_kernel(Params p) {
             const A w = static_cast<A>(p.rw[static_cast<int64_t>(p.rw_e0 + g) * p.N + col]);
             Elem<S>::st(C, row * p.ldc + col, acc + static_cast<A>(p.rdl[p.rperm[row]]) * w);
         } else if (EPI == kEpiSwigluFwd) {
-            Elem<S>::st(C, row * p.ldc + col, acc);
-            Elem<S>::st(C, row * p.ldc + p.f + col, acc_up);
+            // the backward's factors [u silu'(g) | silu(g)] and the activation silu(g) u
+            Elem<S>::st(C, row * p.ldc + col, acc_up * dsilu_f(acc));
+            Elem<S>::st(C, row * p.ldc + p.f + col, silu_f(acc));
             Elem<S>::st(static_cast<S*>(p.c2[g]), row * p.ldc2 + col, silu_f(acc) * acc_up);
         } else if (EPI == kEpiGeluFwd) {
             Elem<S>::st(C, row * p.ldc + col, acc);
             Elem<S>::st(static_cast<S*>(p.c2[g]), row * p.ldc2 + col, gelu_f(acc));
         } else if (EPI == kEpiSwigluBwd) {
             const S* hp = static_cast<const S*>(p.aux[g]);
-            const A gv = Elem<S>::ld(hp, row * p.ldaux + col), uv = Elem<S>::ld(hp, row * p.ldaux + p.f + col);
-            Elem<S>::st(C, row * p.ldc + col, acc * uv * dsilu_f(gv));
-            Elem<S>::st(C, row * p.ldc + p.f + col, acc * silu_f(gv));
+            Elem<S>::st(C, row * p.ldc + col, acc * Elem<S>::ld(hp, row * p.ldaux + col));
+            Elem<S>::st(C, row * p.ldc + p.f + col, acc * Elem<S>::ld(hp, row * p.ldaux + p.f + col));
         } else if (EPI == kEpiGeluBwd) {
             const S* hp = static_cast<const S*>(p.aux[g]);
             Elem<S>::st(C, row * p.ldc + col, acc * dgelu_f(Elem<S>::ld(hp, row * p.ldaux + col)));

@@ -110,10 +110,16 @@ def _deq(q, sinv):
     return q.detach().cpu().to(torch.float64) * float(sinv.item())
 
 
-def _swiglu_bwd(da, hp, f):
+def _swiglu_saved(hp, f):
+    """What the SwiGLU forward saves for the backward: [up silu'(gate) | silu(gate)]."""
     g, u = hp[:, :f], hp[:, f:]
     s = torch.sigmoid(g)
-    return torch.cat([da * u * s * (1 + g * (1 - s)), da * g * s], 1)
+    return torch.cat([u * s * (1 + g * (1 - s)), g * s], 1)
+
+
+def _swiglu_bwd(da, saved, f):
+    """The SwiGLU backward from the saved factors."""
+    return torch.cat([da * saved[:, :f], da * saved[:, f:]], 1)
 
 
 GEMM_CASES = [
@@ -190,7 +196,7 @@ def test_fp8_expert_products(case):
         r = slice(o[g], o[g + 1])
         w1d, w2d = _deq(w1q[g], sw1[g]), _deq(w2q[g], sw2[g])
         ref_h = xd[r] @ w1d.t()
-        assert rel_err(hpre[r], ref_h) <= BAR, f"fc1 fwd expert {g}"
+        assert rel_err(hpre[r], _swiglu_saved(ref_h, f)) <= BAR, f"fc1 fwd expert {g}"
         assert rel_err(act[r], F.silu(ref_h[:, :f]) * ref_h[:, f:]) <= BAR, f"SwiGLU expert {g}"
         assert rel_err(y[r], ad[r] @ w2d.t()) <= BAR, f"fc2 fwd expert {g}"
         assert rel_err(dhpre[r], _swiglu_bwd(dyd[r] @ w2d, hp64[r], f)) <= BAR, f"fc2 dgrad expert {g}"
@@ -364,11 +370,8 @@ def test_fp8_layer_matches_quantized_emulation(case):
         out_ref.index_add_(0, rows, g * y)
         dy = _bf16(g * d64[rows])
         dyq = _q(dy, s[DY], "e4m3".replace("4m3", "5m2"))
-        hpb = _bf16(hp)
         dact = dyq @ w2q
-        gg, uu = hpb[:, :f], hpb[:, f:]
-        sg = torch.sigmoid(gg)
-        dh = _bf16(torch.cat([dact * uu * sg * (1 + gg * (1 - sg)), dact * gg * sg], 1))
+        dh = _bf16(_swiglu_bwd(dact, _bf16(_swiglu_saved(hp, f)), f))
         dhq = _q(dh, s[DH], "e5m2")
         say(f"  expert {e}: rows {rows.numel()} dW2 {rel_err(fc2[e].grad, dyq.t() @ aq):.2e} "
             f"dW1 {rel_err(fc1[e].grad, dhq.t() @ xq):.2e}")

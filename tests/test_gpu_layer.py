@@ -214,11 +214,9 @@ def _sampled_expert_grads(xr, g, dout, w1, w2, cols, outs, scales=None, e=0):
     aq = q(bf(F.silu(gt) * up), s["act"], "e4m3")
     dyq = q(bf(g * dout), s["dy"], "e5m2")
     dact = dyq @ q(w2[:, cols], s["w2"][e], "e4m3")
-    hb = bf(hp)
-    gb, ub = hb[:, :n], hb[:, n:]
-    sg = torch.sigmoid(gb)
-    dg = q(bf(dact * ub * sg * (1 + gb * (1 - sg))), s["dh"], "e5m2")
-    du = q(bf(dact * gb * sg), s["dh"], "e5m2")
+    sg = torch.sigmoid(gt)   # the forward's saved factors [up silu'(gate) | silu(gate)], stored in bf16
+    dg = q(bf(dact * bf(up * sg * (1 + gt * (1 - sg)))), s["dh"], "e5m2")
+    du = q(bf(dact * bf(gt * sg)), s["dh"], "e5m2")
     return dyq[:, outs].t() @ aq, dg.t() @ xq[:, outs], du.t() @ xq[:, outs]
 
 
