@@ -424,7 +424,8 @@ int rhp_fp8_cast_many(int n, const void* const* x, const int64_t* rows, const in
  * the row-major codes that rhp_fp8_cast would write for the bf16 rows that
  * rhp_permute stores, with the scale of `history`; *amax_bits rises to their
  * max |value| and *scale_inv = 1 / scale, bit for bit as permute then cast
- * (T == 0 writes nothing).
+ * (T == 0 writes nothing; q must be a valid 16-byte aligned pointer even when
+ * no pair is local).
  * Replaces the dispatch copy of resihp/runtime/moe.py:78 followed by the
  * input cast of the fp8 expert products (reference_model.py:188-203).
  */
