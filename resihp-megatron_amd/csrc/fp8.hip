@@ -324,18 +324,27 @@ __device__ __forceinline__ void f8_map(F8Map& m, uint32_t ld, int frag_row0, int
 }
 
 // N-contiguous ("MN-major") operand tiles: 128 k rows of 256 mn bytes (32 KB),
-// 16-byte chunk c of k row r at position c ^ (r & 7), so that the eight k rows
-// one transposing read covers fall in eight distinct bank groups.  One direct
+// 16-byte chunk c of k row r at position mn_pos(c, r) = c ^ (r & 7) ^ 8 (c & 1).
+// A transposing read's 16-lane group covers eight k rows of one chunk (eight
+// positions c ^ (r & 7)), and the two groups read together hold the chunks c
+// and c + 1 of the same rows: the ^ 8 (c & 1) puts those in the other half of
+// the row, so the 32 lanes cover all 64 banks (with c ^ (r & 7) alone both
+// groups fell on the same 32 banks: 40 % bank-conflict cycles).  One direct
 // load fills four k rows: lane L takes row L / 16 of them and position L % 16,
-// i.e. source chunk (L % 16) ^ (row & 7).  vo[j] holds the lane's byte offset
+// i.e. source chunk mn_chunk(L % 16, row).  vo[j] holds the lane's byte offset
 // from the operand's row 0 and column mn0 without the step's k; chunks past
 // mn_lim read zero.
+__device__ __forceinline__ int mn_pos(int c, int r) { return c ^ (r & 7) ^ ((c & 1) << 3); }
+__device__ __forceinline__ int mn_chunk(int p, int r) {
+    const int lo = (p ^ r) & 7;
+    return lo | (((p >> 3) ^ (lo & 1)) << 3);
+}
 __device__ __forceinline__ void f8_map_mn(F8Map& m, uint32_t ld, int mn0, int mn_lim, int frag_mn0, int nfrag) {
     const int L = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
     for (int j = 0; j < kF8PerWave; ++j) {
         const int r = (j * kWaves + w) * 4 + (L >> 4);
-        const int c = (L & 15) ^ (r & 7);
+        const int c = mn_chunk(L & 15, r);
         m.vo[j] = c * 16 < mn_lim ? static_cast<uint32_t>(r) * ld + static_cast<uint32_t>(mn0 + c * 16) : kOutOfRange;
     }
     // Fragment reads (ds_read_b64_tr_b8): in each 16-lane group, lane j points at k row base + j / 2,
@@ -347,7 +356,7 @@ __device__ __forceinline__ void f8_map_mn(F8Map& m, uint32_t ld, int mn0, int mn
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int mn = frag_mn0 + i * 32 + 16 * (G & 1);
-        m.fr[i] = i < nfrag ? static_cast<uint32_t>(kr * 256 + (((mn >> 4) ^ (kr & 7)) << 4) + 8 * (j & 1)) : 0;
+        m.fr[i] = i < nfrag ? static_cast<uint32_t>(kr * 256 + (mn_pos(mn >> 4, kr) << 4) + 8 * (j & 1)) : 0;
     }
 }
 
