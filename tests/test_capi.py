@@ -106,3 +106,31 @@ def test_workspace_queries_are_pure():
     assert L.rhp_router_wgrad_workspace_bytes(8192, 4096, 8, 2, C.F64) == 2 * a
     # K-split workspace: 8 XCDs x 32 CUs of one fp32 256 x 256 tile each, then one int32 counter per slot
     assert L.rhp_expert_split_workspace_bytes() == 256 * 256 * 256 * 4 + 256 * 4
+
+
+def _row_codes(entry, fmt=C.E4M3, q=True, hist_len=16, margin=0, k=2, T=4, h=64):
+    fake = ctypes.c_void_p(4096)   # 16-byte aligned, never dereferenced: validation fails first
+    qp = fake if q else None
+    if entry == "rhp_permute_fp8":
+        C.call(entry, fake, T, h, k, fake, fmt, fake, hist_len, margin, fake, fake, qp, None)
+    else:
+        C.call(entry, fake, fake, fake, fake, T, h, k, fake, fmt, fake, hist_len, margin, fake, fake, qp, None)
+
+
+@pytest.mark.parametrize("entry", ["rhp_permute_fp8", "rhp_combine_bwd_fp8"])
+@pytest.mark.parametrize("kw,msg", [
+    (dict(fmt=C.BF16), "RHP_E4M3 or RHP_E5M2"),
+    (dict(q=False), "null code output"),
+    (dict(hist_len=0), "bad history length or margin"),
+    (dict(margin=64), "bad history length or margin"),
+    (dict(h=60), "h must be a multiple of 8"),
+    (dict(k=17), "1 <= k <= 16"),
+])
+def test_fp8_row_entries_reject_bad_arguments(entry, kw, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        _row_codes(entry, **kw)
+
+
+def test_combine_bwd_fp8_rejects_top_k_above_8():
+    with pytest.raises(RuntimeError, match="top-k above 8"):
+        _row_codes("rhp_combine_bwd_fp8", k=9)
