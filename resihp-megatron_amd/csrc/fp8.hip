@@ -500,11 +500,8 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
         asm volatile("" ::: "memory");
     };
 
-    f32x16_t acc[4][kFragY];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < kFragY; ++j) acc[i][j] = f32x16_t{};
+    Acc32<kWaveY> acc;
+    acc.zero();
 
     typedef i32x8_t FragSet[4 + kFragY];
     // sx, sy: byte offsets of the slots of the X and Y tiles.
@@ -524,7 +521,7 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < kFragY; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[i], f[4 + j], acc[i][j], XF, YF, 0, 127,
+                acc.v[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[i], f[4 + j], acc.v[i][j], XF, YF, 0, 127,
                                                                            0, 127);
     };
     auto read_one = [&](FragSet& f, uint32_t sx, uint32_t sy, int b, int n) {
@@ -553,7 +550,7 @@ __global__ __launch_bounds__(kThreadsMfma) void gg_fp8_kernel(Params p) {
             }
 #pragma unroll
             for (int j = 0; j < kFragY; ++j)
-                acc[q][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[4 + j], acc[q][j], XF, YF, 0, 127,
+                acc.v[q][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f[q], f[4 + j], acc.v[q][j], XF, YF, 0, 127,
                                                                            0, 127);
             if (q < 2)
                 issue_y(ly_step, ly_slot, 2 * q, 2 * q + 2);

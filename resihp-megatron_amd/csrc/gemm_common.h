@@ -318,14 +318,17 @@ template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI =
 // ------------------------------------------------------------------ MFMA kernels (bf16)
 //
 // A 256 x 256 output tile per workgroup of 8 waves (two per SIMD).  Wave w
-// owns X rows [128 (w % 2), +128) and Y rows [64 (w / 2), +64): 4 x 2
-// accumulators of v_mfma_f32_32x32x16_bf16 (128 registers).  The bf16
-// forward products run the same tile on 4 waves (one per SIMD), wave w owning
-// Y rows [128 (w / 2), +128) in 4 x 4 accumulators (256 registers): a third
-// fewer fragment reads per MFMA.  Under load the GPU runs at its power limit,
-// and LDS reads are a large share of the energy of a step, so the clock rises
-// by more than the single wave per SIMD loses in latency hiding; for the
-// backward products (DGRAD, and WGRAD's transposing reads) the two are even.
+// owns X rows [128 (w % 2), +128) and Y rows [64 (w / 2), +64).  The bf16
+// products hold them in 8 x 4 accumulators of v_mfma_f32_16x16x32_bf16 (128
+// registers), the fp8 products in 4 x 2 of the 32x32x64 fp8 MFMA.  Under load
+// the GPU runs at its power limit, so energy per step sets the clock: the
+// 16x16x32 shape reads and writes half the accumulator bytes per FLOP of
+// 32x32x16, and with operands in registers sustains 1.9 PFLOP/s against 1.75.
+// In these kernels it raises the clock by 8-15 % and lowers MFMA busy by
+// about as much for the input gradients (whose step time stays with the
+// operand loads), 3-4 % net for the weight gradients and the forward.  A
+// 4-wave tile of 128 x 128 per wave (one wave per SIMD) hides too little of
+// the 16-cycle MFMA issue stream and runs slower.
 //
 // Operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds:
 // no staging registers and no LDS stores.  One such load moves 64 lanes x 16
@@ -335,38 +338,79 @@ template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI =
 //     keep rows of K-step elements with the 16-byte chunks XOR-swizzled by
 //     row, so the 16 rows of one ds_read_b128 hit 16 distinct bank slots.
 //   MN-major tiles (K is the slow dimension: DGRAD weights, both WGRAD
-//     operands) keep 512-byte k rows with chunk c at position c ^ 4 (k & 3)
+//     operands) keep 512-byte k rows with chunk c at position c ^ mn_swz(k)
 //     and are read with gfx950's ds_read_b64_tr_b16, which transposes 4 x 16
 //     blocks across each 16-lane group; two such reads give one fragment.
 // No transposed copy of any operand is made in HBM.
 //
 // The loads are inline assembly so that the compiler, which does not see them,
 // does not make every LDS read wait for all of them; each kernel counts them
-// itself (s_waitcnt vmcnt) before its barriers.  Fragments are double-buffered
-// in registers: the reads of the next k16 block are interleaved with the
-// MFMAs of the current one.
+// itself (s_waitcnt vmcnt) before its barriers.  The fragment reads of the
+// next k32 block are interleaved with the MFMAs of the current one.
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
 constexpr int kThreadsMfma = 64 * kWaves;
 constexpr int kWaveY = kTile / (kWaves / 2);               // Y rows per wave
 constexpr int kFragY = kWaveY / 32;                        // Y fragments per wave
 
-__device__ __forceinline__ int mnmaj_off(int k, int mn) {
-    return k * 512 + (((mn >> 3) ^ ((k & 3) << 2)) << 4) + ((mn & 7) << 1);
-}
+// The accumulators of one wave's 128 X x WY Y share of the tile, as the
+// epilogue and the K split see them: kVec float4 pieces per lane, piece n
+// holding X columns x(n) .. x(n) + 3 of Y row y(n) (offsets within the
+// wave's share).
+//   Acc32: 32 x 32 MFMA tiles (the fp8 32x32x64) v[i][j] (i < 4, j < WY / 32);
+//     lane holds X 32 i + 8 q + 4 (lane >> 5) + e, Y 32 j + (lane & 31) in
+//     v[i][j][4 q + e].
+//   Acc16: v_mfma_f32_16x16x32 tiles v[i][j] (i < 8, j < WY / 16); lane holds
+//     X 16 i + 4 (lane >> 4) + e, Y 16 j + (lane & 15) in v[i][j][e].
+template <int WY>
+struct Acc32 {
+    static constexpr int FY = WY / 32, kVec = 16 * FY;
+    f32x16_t v[4][FY];
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < FY; ++j) v[i][j] = f32x16_t{};
+    }
+    __device__ __forceinline__ float4 get(int n) const {
+        const f32x16_t& a = v[n / (4 * FY)][(n / 4) % FY];
+        const int q = n % 4;
+        return make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+    }
+    static __device__ __forceinline__ int x(int n, int lane) { return 32 * (n / (4 * FY)) + 8 * (n % 4) + 4 * (lane >> 5); }
+    static __device__ __forceinline__ int y(int n, int lane) { return 32 * ((n / 4) % FY) + (lane & 31); }
+};
+template <int WY>
+struct Acc16 {
+    static constexpr int FY = WY / 16, kVec = 8 * FY;
+    f32x4_t v[8][FY];
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < FY; ++j) v[i][j] = f32x4_t{};
+    }
+    __device__ __forceinline__ float4 get(int n) const {
+        const f32x4_t& a = v[n / FY][n % FY];
+        return make_float4(a[0], a[1], a[2], a[3]);
+    }
+    static __device__ __forceinline__ int x(int n, int lane) { return 16 * (n / FY) + 4 * (lane >> 4); }
+    static __device__ __forceinline__ int y(int n, int lane) { return 16 * (n % FY) + (lane & 15); }
+};
 
-// Two transposed reads, k rows kb .. kb + 3 and kb + 4 .. kb + 7 (512 B apart per k row).
-__device__ __forceinline__ bf16x8_t frag_mnmaj(const uint8_t* tile, uint32_t fr, int kk) {
-    typedef s16x4_t __attribute__((address_space(3))) * lds_v4;
-    const uint8_t* p = tile + fr + kk * 16 * 512;
-    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(p)));
-    const s16x4_t hi =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(p + 4 * 512)));
-    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+// Chunk swizzle of MN-major tiles: chunk c of k row k sits at c ^ mn_swz(k).
+// A transposed fragment read covers, per 16-lane group g, k rows 8 g + 0..3
+// and 16 columns (two chunks); the 32 lanes served together (two groups, k
+// rows 8 apart) then reach 16 distinct chunk positions, all 64 banks.
+__device__ __forceinline__ int mn_swz(int k) { return ((k & 3) << 2) ^ (((k >> 3) & 1) << 1); }
+
+__device__ __forceinline__ int mnmaj_off(int k, int mn) {
+    return k * 512 + (((mn >> 3) ^ mn_swz(k)) << 4) + ((mn & 7) << 1);
 }
 
 __device__ __forceinline__ void store_bf16x4(uint16_t* p, float a, float b, float c, float d) {
@@ -783,8 +827,8 @@ __device__ __forceinline__ void epilogue_half_q(const Params& p, const Tile& t, 
 }
 
 // The partial tiles of a K-split tile's pieces: piece q at first + q * stride
-// (float4 units), each thread's accumulators at float4 (i FY + j) 4 + v,
-// thread-major.  pieces = 0: no split, the accumulators are the tile.
+// (float4 units), each thread's accumulator piece n at float4 n NT + thread
+// (thread-major).  pieces = 0: no split, the accumulators are the tile.
 struct SplitSum {
     const float4* first;
     int pieces;
@@ -793,10 +837,9 @@ struct SplitSum {
 
 // One half of the epilogue (rows [HALF * 128, +128) of the tile): load the
 // half's aux values, stage the fp32 results in LDS, then write the half.
-template <int HALF, int MODE, int EPI, int NT, int WY, int QF, bool MAP>
-__device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, float* ep, f32x16_t (&acc)[4][WY / 32],
-                                              int wx, int wy, int lane, float mul, const SplitSum& split, QuantAcc& qa) {
-    constexpr int FY = WY / 32;
+template <int HALF, int MODE, int EPI, int NT, int QF, bool MAP, class Acc>
+__device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, float* ep, const Acc& acc, int wx, int wy,
+                                              int wy_rows, int lane, float mul, const SplitSum& split, QuantAcc& qa) {
     AuxHalf<EPI, NT> aux;
     load_aux_half<MODE, EPI, NT>(p, t, HALF * kEpRows, aux);
     int32_t dst_rows = -1;
@@ -804,50 +847,37 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
         if (p.c_idx != nullptr) dst_rows = scatter_rows_half<NT>(p, t, HALF * kEpRows);
     if constexpr (EPI == kEpiStoreRouter) dst_rows = __float_as_int(router_scale_half<NT>(p, t, HALF * kEpRows));
     lds_barrier();
-    if ((wy * WY) / kEpRows == HALF) {
+    if ((wy * wy_rows) / kEpRows == HALF) {
+        float* wave_ep = ep + (wy * wy_rows - HALF * kEpRows) * kEpPitchF + wx * 128;
         if (split.pieces) {
             // The sum of the pieces, in piece order.
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < FY; ++j) {
-                    const int y = wy * WY + j * 32 + (lane & 31) - HALF * kEpRows;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int x = wx * 128 + i * 32 + q * 8 + 4 * (lane >> 5);
-                        const float4* src = split.first + ((i * FY + j) * 4 + q) * NT + threadIdx.x;
-                        float4 v = src[0];
-                        for (int pc = 1; pc < split.pieces; ++pc) {
-                            const float4 w = src[pc * split.stride];
-                            v.x += w.x;
-                            v.y += w.y;
-                            v.z += w.z;
-                            v.w += w.w;
-                        }
-                        v.x *= mul;
-                        v.y *= mul;
-                        v.z *= mul;
-                        v.w *= mul;
-                        *reinterpret_cast<float4*>(ep + y * kEpPitchF + x) = v;
-                    }
+            for (int n = 0; n < Acc::kVec; ++n) {
+                const float4* src = split.first + n * NT + threadIdx.x;
+                float4 v = src[0];
+                for (int pc = 1; pc < split.pieces; ++pc) {
+                    const float4 w = src[pc * split.stride];
+                    v.x += w.x;
+                    v.y += w.y;
+                    v.z += w.z;
+                    v.w += w.w;
                 }
+                v.x *= mul;
+                v.y *= mul;
+                v.z *= mul;
+                v.w *= mul;
+                *reinterpret_cast<float4*>(wave_ep + Acc::y(n, lane) * kEpPitchF + Acc::x(n, lane)) = v;
+            }
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < FY; ++j) {
-                    const int y = wy * WY + j * 32 + (lane & 31) - HALF * kEpRows;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int x = wx * 128 + i * 32 + q * 8 + 4 * (lane >> 5);
-                        float4 v;
-                        v.x = acc[i][j][4 * q + 0] * mul;
-                        v.y = acc[i][j][4 * q + 1] * mul;
-                        v.z = acc[i][j][4 * q + 2] * mul;
-                        v.w = acc[i][j][4 * q + 3] * mul;
-                        *reinterpret_cast<float4*>(ep + y * kEpPitchF + x) = v;
-                    }
-                }
+            for (int n = 0; n < Acc::kVec; ++n) {
+                float4 v = acc.get(n);
+                v.x *= mul;
+                v.y *= mul;
+                v.z *= mul;
+                v.w *= mul;
+                *reinterpret_cast<float4*>(wave_ep + Acc::y(n, lane) * kEpPitchF + Acc::x(n, lane)) = v;
+            }
         }
     }
     lds_barrier();
@@ -863,25 +893,24 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
 // LDS ([128 rows][256 X] at kEpPitchF floats per row), and every thread takes
 // 4-column pieces, so each wave instruction reads or writes whole contiguous
 // row segments in HBM.  Barriers here wait only for LDS accesses: the global
-// stores of one half drain while the next is staged.  A wave owns WY Y rows
-// (NT threads in the workgroup); for MFMA tile (i, j) a lane holds Y row
-// wy * WY + 32 j + (lane & 31) and X columns wx * 128 + 32 i + 8 q +
-// 4 (lane >> 5) + e in acc[i][j][4 q + e].  The caller guarantees that every
-// load into the LDS buffer has completed.  With a K split, the staged values
-// are the sum of the pieces' partial tiles instead of acc.  QF >= 0 (an fp8
-// format) makes the epilogue quantising (the Params q fields): each wave
-// raises the amax once, after both halves.  MAP: a plain-store epilogue
-// writes its rows through the c_idx scatter map when one is given.
-template <int MODE, int EPI, int NT = kThreadsMfma, int WY = kWaveY, int QF = -1, bool MAP = false>
-__device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, f32x16_t (&acc)[4][WY / 32],
-                                         int wx, int wy, int lane, float mul = 1.0f,
-                                         SplitSum split = SplitSum{nullptr, 0, 0}) {
+// stores of one half drain while the next is staged.  A wave owns X columns
+// [128 wx, +128) and Y rows [WY wy, +WY) (NT threads in the workgroup), held
+// as the Acc layout says.  The caller guarantees that every load into the LDS
+// buffer has completed.  With a K split, the staged values are the sum of the
+// pieces' partial tiles instead of acc.  QF >= 0 (an fp8 format) makes the
+// epilogue quantising (the Params q fields): each wave raises the amax once,
+// after both halves.  MAP: a plain-store epilogue writes its rows through the
+// c_idx scatter map when one is given.
+template <int MODE, int EPI, int NT, int WY, int QF = -1, bool MAP = false, class Acc>
+__device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t* lds, const Acc& acc, int wx, int wy,
+                                         int lane, float mul = 1.0f, SplitSum split = SplitSum{nullptr, 0, 0}) {
     static_assert(WY <= kEpRows && kEpRows % WY == 0, "a wave's rows lie in one half");
+    static_assert(NT * Acc::kVec * 4 == kTile * kTile, "the waves' accumulators cover the tile");
     float* ep = reinterpret_cast<float*>(lds);
     QuantAcc qa{1.0f, 0.0f};
     if constexpr (QF >= 0) qa.scale = history_scale(p.q_hist, p.q_L, fp8_max(QF), p.q_margin);
-    epilogue_pass<0, MODE, EPI, NT, WY, QF, MAP>(p, t, ep, acc, wx, wy, lane, mul, split, qa);
-    epilogue_pass<1, MODE, EPI, NT, WY, QF, MAP>(p, t, ep, acc, wx, wy, lane, mul, split, qa);
+    epilogue_pass<0, MODE, EPI, NT, QF, MAP>(p, t, ep, acc, wx, wy, WY, lane, mul, split, qa);
+    epilogue_pass<1, MODE, EPI, NT, QF, MAP>(p, t, ep, acc, wx, wy, WY, lane, mul, split, qa);
     if constexpr (QF >= 0) {
         // Wave maximum, then one atomic per wave; non-negative floats order like
         // their bits, and a maximum not above the value read (possibly stale,
@@ -903,21 +932,13 @@ __device__ __forceinline__ void epilogue(const Params& p, const Tile& t, uint8_t
 // memory in piece order (the same bits whichever piece is last), instead of
 // its own accumulators.  It resets the counter for the next launch.  No block
 // ever waits for another.
-template <int NT, int FY>
-__device__ __forceinline__ bool split_arrive(const Params& p, const Tile& t, const f32x16_t (&acc)[4][FY],
-                                             uint8_t* lds) {
-    constexpr int kVec = 4 * FY * 4;   // float4 per thread
-    static_assert(NT * kVec * 4 == kTile * kTile, "a piece holds a whole tile");
+template <int NT, class Acc>
+__device__ __forceinline__ bool split_arrive(const Params& p, const Tile& t, const Acc& acc, uint8_t* lds) {
+    static_assert(NT * Acc::kVec * 4 == kTile * kTile, "a piece holds a whole tile");
     const int tid = threadIdx.x;
-    float4* mine = reinterpret_cast<float4*>(p.split_part) + static_cast<size_t>(t.slot + t.piece * t.stride) * (NT * kVec);
+    float4* mine = reinterpret_cast<float4*>(p.split_part) + static_cast<size_t>(t.slot + t.piece * t.stride) * (NT * Acc::kVec);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < FY; ++j)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                mine[((i * FY + j) * 4 + v) * NT + tid] =
-                    make_float4(acc[i][j][4 * v], acc[i][j][4 * v + 1], acc[i][j][4 * v + 2], acc[i][j][4 * v + 3]);
+    for (int n = 0; n < Acc::kVec; ++n) mine[n * NT + tid] = acc.get(n);
     // Each wave waits for its own stores; after the barrier one thread makes
     // the whole block's stores visible device-wide and counts the piece in.
     // (An agent-scope fence writes back the XCD's L2; one per piece, not one

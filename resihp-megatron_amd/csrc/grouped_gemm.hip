@@ -11,7 +11,7 @@
 //   DGRAD(row-grouped, "NN"):  out[r, n] = sum_k A[r, k] * W[k, n]     W: [K, N]
 //   WGRAD(K-grouped,  "TN"):   dW[o, i]  = sum_r G[r, o] * V[r, i]     rows r of the group
 //
-// MFMA mapping (v_mfma_f32_32x32x16_bf16): the MFMA "A" operand is the
+// MFMA mapping (v_mfma_f32_16x16x32_bf16): the MFMA "A" operand is the
 // X tile, whose rows are the contiguous dimension of the output (n or i); the
 // "B" operand is the Y tile, whose rows are the output's row dimension (token
 // rows or o).  Each lane then holds 4 consecutive output columns, so stores are
@@ -35,9 +35,9 @@ namespace {
 // An operand tile is 256 rows (or mn columns) by 64 k, 32 KB:
 //   K-major [256 rows][64 k]: 128-byte rows, chunk c of row r at position
 //     c ^ ((r >> 1) & 7), so the 16 rows of one ds_read_b128 hit 16 distinct
-//     bank slots, and a lane's offset for k16 block b is its block-0 offset
-//     XOR 32 b.
-//   MN-major [64 k][256 mn]: 512-byte k rows, chunk c at c ^ 4 (k & 3).
+//     bank slots, and a lane's offset for k32 block b is its block-0 offset
+//     XOR 64 b.
+//   MN-major [64 k][256 mn]: 512-byte k rows, chunk c at c ^ mn_swz(k).
 // One load moves 1 KB: 8 K-major rows or 2 MN-major k rows.
 
 constexpr int kK64 = 64;
@@ -47,7 +47,7 @@ static_assert((kT64Bytes / 1024) % kWaves == 0, "whole loads per wave");
 template <int NW = kWaves>
 struct Dma64Map {
     uint32_t vo[kT64Bytes / 1024 / NW];
-    uint32_t fr[4];   // K-major: block-0 offset (block b: XOR 32 b); MN-major: block-0 offset (block b: + 8192 b)
+    uint32_t fr[8];   // K-major: block-0 offset (block b: XOR 64 b); MN-major: block-0 offset (block b: + 16384 b)
 };
 
 // Load j of wave w fills 1 KB block j * NW + w of an operand's stage.
@@ -61,7 +61,7 @@ __device__ __forceinline__ void d64_kmaj(Dma64Map<NW>& m, uint32_t ld, int frag_
         m.vo[j] = (static_cast<uint32_t>(src_row(row)) * ld + chunk * 8) * 2u;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) m.fr[i] = i < nfrag ? k64_off(frag_row0 + i * 32 + (L & 31), L >> 5) : 0;
+    for (int i = 0; i < 8; ++i) m.fr[i] = i < nfrag ? k64_off(frag_row0 + i * 16 + (L & 15), L >> 4) : 0;
 }
 
 template <int NW>
@@ -70,27 +70,39 @@ __device__ __forceinline__ void d64_mnmaj(Dma64Map<NW>& m, uint32_t ld, int mn0,
 #pragma unroll
     for (int j = 0; j < kT64Bytes / 1024 / NW; ++j) {
         const int k = (j * NW + w) * 2 + (L >> 5);
-        const int chunk = (L & 31) ^ ((k & 3) << 2);
+        const int chunk = (L & 31) ^ mn_swz(k);
         m.vo[j] = chunk * 8 < mn_lim ? (static_cast<uint32_t>(k) * ld + static_cast<uint32_t>(mn0 + chunk * 8)) * 2u
                                      : kOutOfRange;
     }
     const int g = L >> 4, r = L & 15;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        m.fr[i] = i < nfrag ? mnmaj_off(8 * (g >> 1) + (r >> 2), frag_row0 + i * 32 + 16 * (g & 1) + 4 * (r & 3)) : 0;
+    for (int i = 0; i < 8; ++i) m.fr[i] = i < nfrag ? mnmaj_off(8 * g + (r >> 2), frag_row0 + i * 16 + 4 * (r & 3)) : 0;
+}
+
+// Fragment of k32 block b from an MN-major tile: two transposed reads, k rows
+// 32 b + 8 g + 0..3 and + 4..7 for the lanes of 16-lane group g.
+__device__ __forceinline__ bf16x8_t frag_mn32(const uint8_t* tile, uint32_t fr, int b) {
+    typedef s16x4_t __attribute__((address_space(3))) * lds_v4;
+    const uint8_t* q = tile + fr + b * 32 * 512;
+    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(q)));
+    const s16x4_t hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(q + 4 * 512)));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // ------------------------------------------------------------------ the MFMA kernel: a ring of five operand slots
 //
 // LDS holds five operand tiles ("slots", 160 KB), filled in the order X0 Y0
 // X1 Y1 X2 Y2 ..., operand tile q (X of step q / 2 for even q, Y for odd q)
-// in slot q mod 5.  Each K step of 64 runs four k16 blocks; the fragments of
-// block b + 1 are read while the MFMAs of block b run.  The barrier that
-// closes step kt comes after the reads of its last block and needs steps up
-// to kt + 1 complete, so X of step kt + 2 stays in flight across it; right
-// after it the two slots of step kt are refilled with Y of step kt + 2 and X
-// of step kt + 3, and the MFMAs of the last block cover the LDS latency of the
-// next step's first fragments.  Loads are thus never drained to zero at a
+// in slot q mod 5.  Each K step of 64 runs two k32 blocks; the fragments of
+// block b + 1 are read while the MFMAs of block b run.  X of step kt + 2 is
+// loaded with block 0 into the slot Y of step kt - 1 left; the barrier that
+// closes step kt comes after the reads of block 1 and needs steps up to kt + 1
+// complete, so X of step kt + 2 stays in flight across it; right after it Y
+// of step kt + 2 goes into the slot X of step kt leaves, with block 1, whose
+// MFMAs cover the LDS latency of the next step's first fragments.  The next
+// block's Y fragments are read over the first half of a block, so a whole
+// half-block of MFMAs separates each read from its use.  Loads are thus never drained to zero at a
 // barrier: with the latency of L2 and HBM under load near a microsecond, the
 // bytes in flight per CU set the rate at which tiles arrive.  Tiles past the
 // last step are loaded from an offset past the buffer view (they read zeros
@@ -111,7 +123,7 @@ constexpr uint32_t kPastView = 0x7ffffff0u;   // soffset that puts every lane pa
 template <int MODE, int EPI, int NW, bool REBASE = false, bool MAP = false>
 __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* lds) {
     // NW waves: wave w owns X rows [128 (w % 2), +128) and Y rows [WY (w / 2), +WY).
-    constexpr int WY = kTile / (NW / 2), FY = WY / 32;
+    constexpr int WY = kTile / (NW / 2), FY = WY / 16;   // Y rows and 16-row Y fragments per wave
     constexpr int kPerWave = kT64Bytes / 1024 / NW;   // loads per wave per operand tile
     t.g = __builtin_amdgcn_readfirstlane(t.g);
     t.x0 = __builtin_amdgcn_readfirstlane(t.x0);
@@ -144,7 +156,7 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
         const int64_t rows = t.k_end;   // group rows; reads past them return zero
         rx = make_dma_rsrc(B + t.row0 * p.ldb, rows * p.ldb * 2);
         ry = make_dma_rsrc(A + t.row0 * p.lda, rows * p.lda * 2);
-        d64_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
+        d64_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 8);
         d64_mnmaj(my, lda, t.y0, t.y_lim, wy * WY, FY);
     } else {
         const int y_last = t.y_lim - 1;
@@ -165,7 +177,7 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
         }
         if (MODE == kFwd) {
             rx = make_dma_rsrc(B, static_cast<int64_t>(EPI == kEpiSwigluFwd ? 2 * p.f : p.N) * p.ldb * 2);
-            d64_kmaj(mx, ldb, wx * 128, 4, [&](int r) {
+            d64_kmaj(mx, ldb, wx * 128, 8, [&](int r) {
                 if (EPI == kEpiSwigluFwd) {
                     // 256 weight rows = [gate 64 | up 64] for each half of 128 activation columns.
                     const int half = r >> 7, qq = r & 127;
@@ -178,7 +190,7 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
             });
         } else {
             rx = make_dma_rsrc(B, static_cast<int64_t>(p.K) * p.ldb * 2);
-            d64_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 4);
+            d64_mnmaj(mx, ldb, t.x0, t.x_lim, wx * 128, 8);
         }
     }
     const int nk = (t.k_end - t.k_begin + kK64 - 1) / kK64;
@@ -237,127 +249,122 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
         asm volatile("" ::: "memory");
     };
 
-    f32x16_t acc[4][FY];
+    f32x4_t acc[8][FY];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < FY; ++j) acc[i][j] = f32x16_t{};
+        for (int j = 0; j < FY; ++j) acc[i][j] = f32x4_t{};
 
-    typedef bf16x8_t FragSet[4 + FY];
+    // Fragments of one k32 block: X fragments 0..7 (16 X rows each) and Y
+    // fragments 0 .. FY - 1.  Y fragments are double-buffered; X fragment q
+    // of the next block is read right after the MFMAs of part q (its last use
+    // in this block), so X takes one set of registers.
+    typedef bf16x8_t YSet[FY];
+    bf16x8_t xf[8];
     auto kfrag = [](const uint8_t* tile, uint32_t fr, int b) {
-        return *reinterpret_cast<const bf16x8_t*>(tile + (fr ^ static_cast<uint32_t>(b << 5)));
+        return *reinterpret_cast<const bf16x8_t*>(tile + (fr ^ static_cast<uint32_t>(b << 6)));
     };
     // sx, sy: byte offsets of the slots, wave-uniform values the compiler
     // cannot fold into per-slot address registers.
-    auto read_frags = [&](FragSet& f, uint32_t sx, uint32_t sy, int b) {
-        const uint8_t* xt = lds + sx;
-        const uint8_t* yt = lds + sy;
-#pragma unroll
-        for (int j = 0; j < FY; ++j)
-            f[4 + j] = kYK ? kfrag(yt, my.fr[j], b) : frag_mnmaj(yt, my.fr[j], b);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) f[i] = kXK ? kfrag(xt, mx.fr[i], b) : frag_mnmaj(xt, mx.fr[i], b);
+    auto read_x = [&](uint32_t sx, int b, int i) {
+        xf[i] = kXK ? kfrag(lds + sx, mx.fr[i], b) : frag_mn32(lds + sx, mx.fr[i], b);
     };
-    // MFMAs [m0, m1) of a block: accumulator (m / FY, m % FY).
-    auto mfma_range = [&](const FragSet& f, int m0, int m1) {
-#pragma unroll
-        for (int m = m0; m < m1; ++m)
-            acc[m / FY][m % FY] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[m / FY], f[4 + m % FY], acc[m / FY][m % FY],
-                                                                        0, 0, 0);
+    auto read_y = [&](YSet& y, uint32_t sy, int b, int j) {
+        y[j] = kYK ? kfrag(lds + sy, my.fr[j], b) : frag_mn32(lds + sy, my.fr[j], b);
     };
-    // One fragment of block b: Y fragment j (n = 4 + j) or X fragment i (n = i).
-    auto read_one = [&](FragSet& f, uint32_t sx, uint32_t sy, int b, int n) {
-        if (n >= 4) {
-            const uint8_t* yt = lds + sy;
-            f[n] = kYK ? kfrag(yt, my.fr[n - 4], b) : frag_mnmaj(yt, my.fr[n - 4], b);
-        } else {
-            const uint8_t* xt = lds + sx;
-            f[n] = kXK ? kfrag(xt, mx.fr[n], b) : frag_mnmaj(xt, mx.fr[n], b);
-        }
-    };
-    // The MFMAs of one block (fragments f) in four quarters, the fragment reads
-    // of the next block (into g, from slots sx, sy, block b) in the order its
-    // MFMAs use them, and n <= 4 loads, one after each of the first n quarters:
-    // the loads then reach the address unit at the rate it drains them,
-    // instead of every wave queueing a whole tile at once and stalling.
-    auto block = [&](const FragSet& f, FragSet& g, uint32_t sx, uint32_t sy, int b, auto load, int n) {
-        static_assert(FY == 2 || FY == 4, "read orders for two or four Y fragments");
-        // First the fragments the next block's first MFMAs use: Y 0 and X 0, then the other Y.
-        constexpr int order2[6] = {4, 0, 5, 1, 2, 3};
-        constexpr int order4[8] = {4, 0, 5, 6, 7, 1, 2, 3};
+    // The MFMAs of one k32 block (X fragments xf, Y fragments yc) in eight
+    // parts, part q being X fragment q with every Y fragment.  Spread over the
+    // parts go the reads of the next block (block b of slots sx, sy): its Y
+    // fragments (into yn) over the first four parts, X fragment q after part
+    // q; and the n loads `load` issues: the loads then reach the address unit
+    // at the rate it drains them, instead of every wave queueing a whole tile
+    // at once and stalling.
+    auto block = [&](const YSet& yc, YSet& yn, uint32_t sx, uint32_t sy, int b, auto load, auto n_c) {
+        constexpr int n = decltype(n_c)::value;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 8; ++q) {
+            if (q < 4) {
 #pragma unroll
-            for (int r = 0; r < 2; ++r)
-                if (2 * q + r < 4 + FY) read_one(g, sx, sy, b, FY == 2 ? order2[2 * q + r] : order4[2 * q + r]);
-            mfma_range(f, FY * q, FY * q + FY);
-            if (q < n) load(q);
+                for (int j = FY * q / 4; j < FY * (q + 1) / 4; ++j) read_y(yn, sy, b, j);
+            }
+#pragma unroll
+            for (int j = 0; j < FY; ++j)
+                acc[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[q], yc[j], acc[q][j], 0, 0, 0);
+            read_x(sx, b, q);
+#pragma unroll
+            for (int l = n * q / 8; l < n * (q + 1) / 8; ++l) load(l);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    constexpr int H = kPerWave / 2;   // loads per wave issued with each k16 block
-    static_assert(H <= 4, "at most one load per quarter block");
-    using Pending = std::integral_constant<int, kPerWave>;   // one operand tile stays in flight
-    using Prolog = std::integral_constant<int, kPerWave + H>;   // X1 and half of Y1 in flight
+    using Pending = std::integral_constant<int, kPerWave>;        // one operand tile stays in flight
+    using Prolog = std::integral_constant<int, 2 * kPerWave>;     // X1 and Y1 in flight
+    static_assert(2 * kPerWave <= 63, "vmcnt counts up to 63");
 
     // A wave whose Y rows all lie past the tile's valid rows only loads its
     // share and joins the barriers.
     const bool idle = wy * WY >= t.y_lim;
-    FragSet fa, fb;
+    YSet ya, yb;
     if (nk > 0) {
         issue_x(0, 0);
         issue_y(0, 1);
         issue_x(1, 2);
-        issue_y(1, 3, 0, H);
+        issue_y(1, 3);
         wait_lds(Prolog{});   // step 0 complete
         barrier();
         if (idle) {
             for (int kt = 0; kt < nk; ++kt) {
-                issue_y(kt + 1, (2 * kt + 3) % kSlots, H, 2 * H);
                 issue_x(kt + 2, (2 * kt + 4) % kSlots);
                 wait_lds(Pending{});
                 barrier();
-                issue_y(kt + 2, (2 * kt) % kSlots, 0, H);
+                issue_y(kt + 2, (2 * kt) % kSlots);
             }
         } else {
-            read_frags(fa, 0, kT64Bytes, 0);
+#pragma unroll
+            for (int j = 0; j < FY; ++j) read_y(ya, kT64Bytes, 0, j);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) read_x(0, 0, i);
             // lgkmcnt(0): the loop's first block then waits only for the
             // fragments it uses.  With these reads still counted on entry, the
             // compiler's wait analysis, which merges the entry and the loop's own
             // back edge, loses their order and waits for every read at the top
             // of each step.
             __builtin_amdgcn_s_waitcnt(0xc07f);
-            // Slots of X and Y of step kt (sx, sy), of step kt + 1 (nx, ny),
-            // and the slot that receives X of step kt + 2 (fx).  Two loads go
-            // with each block: the second half of Y of step kt + 1 (block 0),
-            // X of step kt + 2 (blocks 1 and 2), and after the barrier the
-            // first half of Y of step kt + 2 (block 3).
+            // A K step of 64 is two k32 blocks.  Slots of X and Y of step kt
+            // (sx, sy), of step kt + 1 (nx, ny), and the free slot (fx).  X of
+            // step kt + 2 goes into fx with block 0; after the barrier that
+            // closes the reads of step kt, Y of step kt + 2 goes into the slot
+            // X of step kt leaves, with block 1.
             int sx = 0, sy = 1, nx = 2, ny = 3, fx = 4;
             for (int kt = 0; kt < nk; ++kt) {
-                const uint32_t ox = sx * kT64Bytes, oy = sy * kT64Bytes;
-                block(fa, fb, ox, oy, 1, [&](int q) { issue_y(kt + 1, ny, q + H, q + H + 1); }, H);
-                block(fb, fa, ox, oy, 2, [&](int q) { issue_x(kt + 2, fx, q, q + 1); }, H);
-                block(fa, fb, ox, oy, 3, [&](int q) { issue_x(kt + 2, fx, q + H, q + H + 1); }, H);
+                block(ya, yb, sx * kT64Bytes, sy * kT64Bytes, 1, [&](int l) { issue_x(kt + 2, fx, l, l + 1); },
+                      Pending{});
                 // Steps up to kt + 1 complete (X of step kt + 2 in flight),
                 // every read of slots sx and sy done.
                 wait_lds(Pending{});
                 barrier();
-                block(fb, fa, nx * kT64Bytes, ny * kT64Bytes, 0, [&](int q) { issue_y(kt + 2, sx, q, q + 1); }, H);
+                block(yb, ya, nx * kT64Bytes, ny * kT64Bytes, 0, [&](int l) { issue_y(kt + 2, sx, l, l + 1); },
+                      Pending{});
+                const int x2 = fx, y2 = sx;
                 fx = sy;
                 sx = nx;
                 sy = ny;
-                nx = ny + 1 == kSlots ? 0 : ny + 1;
-                ny = nx + 1 == kSlots ? 0 : nx + 1;
+                nx = x2;
+                ny = y2;
             }
         }
         wait_loads_all();   // the tiles past the last step
     }
+    Acc16<WY> out;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < FY; ++j) out.v[i][j] = acc[i][j];
     if (MODE != kWgrad && t.pieces > 1) {
-        if (!split_arrive<64 * NW, FY>(p, t, acc, lds)) return;
-        epilogue<MODE, EPI, 64 * NW, WY, -1, MAP>(p, t, lds, acc, wx, wy, lane, 1.0f, split_sum_of(p, t));
+        if (!split_arrive<64 * NW>(p, t, out, lds)) return;
+        epilogue<MODE, EPI, 64 * NW, WY, -1, MAP>(p, t, lds, out, wx, wy, lane, 1.0f, split_sum_of(p, t));
         return;
     }
-    epilogue<MODE, EPI, 64 * NW, WY, -1, MAP>(p, t, lds, acc, wx, wy, lane);
+    epilogue<MODE, EPI, 64 * NW, WY, -1, MAP>(p, t, lds, out, wx, wy, lane);
 }
 
 // One block per tile (hardware block b runs on XCD b % 8).
@@ -498,7 +505,7 @@ void launch_one(const Job& j, const Params& p, hipStream_t s) {
         if (!nb) return;
         // A K split adds at most one round of pieces to each XCD's items.
         if (MODE != kWgrad && p.split_cap > 1) nb = kXcds * ((nb + kXcds - 1) / kXcds + p.cu_per_xcd);
-        constexpr int nw = MODE == kFwd ? 4 : kWaves;
+        constexpr int nw = kWaves;
         if constexpr (MODE != kWgrad) {
             if (j.a_idx || j.c_idx) {
                 hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, nw, false, true>), dim3(static_cast<unsigned>(nb)),
