@@ -235,7 +235,10 @@ __global__ __launch_bounds__(kThreads) void route_kernel(const XT* __restrict__ 
 //     total in registers.
 // Either way every logit is the same fma chains summed in the same order as
 // route_kernel's (and the oracle's), bit for bit.  Experts past E in the last
-// group are computed on a clamped row and discarded.
+// group are computed on a clamped row and discarded.  TOK tokens per block:
+// 64, or 32 where 64-token blocks would not reach every CU (lanes 32..63 then
+// repeat lanes 0..31's rows, which keeps the loads and weights wave-uniform,
+// and store nothing).
 constexpr int kRtTokens = 64;
 constexpr int kRtMaxWaves = 16;
 
@@ -268,7 +271,7 @@ __device__ __forceinline__ void segment_chains(const bf16* xr, const float* cons
     }
 }
 
-template <int EC>
+template <int EC, int TOK>
 __global__ __launch_bounds__(64 * kRtMaxWaves) void route_bf16_kernel(const bf16* __restrict__ x,
                                                                     const float* __restrict__ w,
                                                                     const float* __restrict__ bias, int64_t T, int h,
@@ -278,14 +281,15 @@ __global__ __launch_bounds__(64 * kRtMaxWaves) void route_bf16_kernel(const bf16
                                                                     int32_t* __restrict__ topi,
                                                                     float* __restrict__ gates) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    float* lg = reinterpret_cast<float*>(smem_raw);                                 // [64][E]
-    int* sel = reinterpret_cast<int*>(lg + static_cast<size_t>(kRtTokens) * E);     // [64][k]
-    float* part = reinterpret_cast<float*>(sel + kRtTokens * k);                    // [S][EC][64], segment mode
-    const int lane = threadIdx.x & 63;
+    float* lg = reinterpret_cast<float*>(smem_raw);                           // [TOK][E]
+    int* sel = reinterpret_cast<int*>(lg + static_cast<size_t>(TOK) * E);     // [TOK][k]
+    float* part = reinterpret_cast<float*>(sel + TOK * k);                    // [S][EC][TOK], segment mode
+    const int lane = threadIdx.x & 63, tl = lane % TOK;
+    const bool owner = lane < TOK;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nw = blockDim.x >> 6;
-    const int64_t t_block = static_cast<int64_t>(blockIdx.x) * kRtTokens;
-    const int64_t t = t_block + lane < T ? t_block + lane : t_block;   // lanes past T repeat a valid row
+    const int64_t t_block = static_cast<int64_t>(blockIdx.x) * TOK;
+    const int64_t t = t_block + tl < T ? t_block + tl : t_block;   // lanes past T repeat a valid row
     const bf16* xr = x + t * h;
     if (expert_mode) {
         for (int e0 = wave * EC; e0 < E; e0 += nw * EC) {
@@ -300,7 +304,7 @@ __global__ __launch_bounds__(64 * kRtMaxWaves) void route_bf16_kernel(const bf16
             }
 #pragma unroll
             for (int b = 0; b < EC; ++b)
-                if (e0 + b < E) lg[lane * E + e0 + b] = total[b];
+                if (owner && e0 + b < E) lg[tl * E + e0 + b] = total[b];
         }
         __syncthreads();
     } else {
@@ -312,23 +316,24 @@ __global__ __launch_bounds__(64 * kRtMaxWaves) void route_bf16_kernel(const bf16
                 float acc[EC];
                 segment_chains<EC>(xr, wr, s * seg, seg, acc);
 #pragma unroll
-                for (int b = 0; b < EC; ++b) part[(s * EC + b) * kRtTokens + lane] = acc[b];
+                for (int b = 0; b < EC; ++b)
+                    if (owner) part[(s * EC + b) * TOK + tl] = acc[b];
             }
             __syncthreads();
-            for (int idx = threadIdx.x; idx < EC * kRtTokens; idx += blockDim.x) {
-                const int b = idx / kRtTokens, tl = idx % kRtTokens;
+            for (int idx = threadIdx.x; idx < EC * TOK; idx += blockDim.x) {
+                const int b = idx / TOK, r = idx % TOK;
                 if (e0 + b < E) {
-                    float total = part[b * kRtTokens + tl];
-                    for (int s = 1; s < S; ++s) total = total + part[(s * EC + b) * kRtTokens + tl];
-                    lg[tl * E + e0 + b] = total;
+                    float total = part[b * TOK + r];
+                    for (int s = 1; s < S; ++s) total = total + part[(s * EC + b) * TOK + r];
+                    lg[r * E + e0 + b] = total;
                 }
             }
             __syncthreads();
         }
     }
-    const int tb = static_cast<int>(min<int64_t>(kRtTokens, T - t_block));
+    const int tb = static_cast<int>(min<int64_t>(TOK, T - t_block));
     for (int idx = threadIdx.x; idx < tb * E; idx += blockDim.x) logits[t_block * E + idx] = lg[idx];
-    select_and_gate<float>(lg, sel, t_block, kRtTokens, blockDim.x, T, E, k, score, normalize, scale, bias, topi,
+    select_and_gate<float>(lg, sel, t_block, TOK, blockDim.x, T, E, k, score, normalize, scale, bias, topi,
                            gates);
 }
 
@@ -625,8 +630,13 @@ int launch_route_bf16(const void* x, const void* w, const void* bias, int64_t T,
     const int ec = E >= 64 ? 16 : 8;
     const int n_ec = (E + ec - 1) / ec;
     const int expert_mode = n_ec >= S ? 1 : 0;
-    const size_t smem = static_cast<size_t>(kRtTokens) * E * sizeof(float) + static_cast<size_t>(kRtTokens) * k * sizeof(int) +
-                        (expert_mode ? 0 : static_cast<size_t>(S) * ec * kRtTokens * sizeof(float));
+    // 32-token blocks where 64-token ones would leave CUs without a block.
+    int cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 0;
+    const int tok = (T + kRtTokens - 1) / kRtTokens < cus ? kRtTokens / 2 : kRtTokens;
+    const size_t smem = static_cast<size_t>(tok) * E * sizeof(float) + static_cast<size_t>(tok) * k * sizeof(int) +
+                        (expert_mode ? 0 : static_cast<size_t>(S) * ec * tok * sizeof(float));
     if (smem > 64 * 1024) {
         *status = 1;
         return 0;
@@ -634,18 +644,19 @@ int launch_route_bf16(const void* x, const void* w, const void* bias, int64_t T,
     *status = 0;
     if (T == 0) return 0;
     const int nw = std::min(expert_mode ? n_ec : S, kRtMaxWaves);
-    const dim3 grid(static_cast<unsigned>((T + kRtTokens - 1) / kRtTokens)), block(64 * nw);
+    const dim3 grid(static_cast<unsigned>((T + tok - 1) / tok)), block(64 * nw);
     const bf16* xb = static_cast<const bf16*>(x);
     const float* wf = static_cast<const float*>(w);
     const float* bf = static_cast<const float*>(bias);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, smem, stream, xb, wf, bf, T, h, E, k, score, normalize,
+                           static_cast<float>(scale), seg, S, expert_mode, static_cast<float*>(logits), topi,
+                           static_cast<float*>(gates));
+    };
     if (ec == 16)
-        hipLaunchKernelGGL(route_bf16_kernel<16>, grid, block, smem, stream, xb, wf, bf, T, h, E, k, score, normalize,
-                           static_cast<float>(scale), seg, S, expert_mode, static_cast<float*>(logits), topi,
-                           static_cast<float*>(gates));
+        tok == kRtTokens ? go(route_bf16_kernel<16, kRtTokens>) : go(route_bf16_kernel<16, kRtTokens / 2>);
     else
-        hipLaunchKernelGGL(route_bf16_kernel<8>, grid, block, smem, stream, xb, wf, bf, T, h, E, k, score, normalize,
-                           static_cast<float>(scale), seg, S, expert_mode, static_cast<float*>(logits), topi,
-                           static_cast<float*>(gates));
+        tok == kRtTokens ? go(route_bf16_kernel<8, kRtTokens>) : go(route_bf16_kernel<8, kRtTokens / 2>);
     return check_launch("route_bf16_kernel");
 }
 
