@@ -436,22 +436,26 @@ __global__ __launch_bounds__(kThreads) void dispatch_count_kernel(const int32_t*
 // Phase 2 (one block): totals, local offsets, per-source counts and the base
 // row of every (block, local expert).  The per-block histograms are staged in
 // LDS first (one load per entry, all in flight together) when they fit.
-constexpr int kScanStage = 16384;     // histogram entries staged in LDS (64 KB)
-constexpr int kScanStageSrc = 4096;   // block sources staged in LDS (16 KB)
-
-__global__ __launch_bounds__(1024) void dispatch_scan_kernel(const int32_t* __restrict__ block_counts,
-                                                             const int32_t* __restrict__ block_src, DispatchShape d,
-                                                             int32_t* __restrict__ counts,
-                                                             int32_t* __restrict__ offsets,
-                                                             int32_t* __restrict__ src_counts,
-                                                             int32_t* __restrict__ block_base) {
-    __shared__ int tot[kMaxE + 1];
-    __shared__ int off[kMaxE + 1];
-    __shared__ int stage[kScanStage];
-    __shared__ int stage_src[kScanStageSrc];
+// Two sizes: up to 255 experts and 8192 staged entries, a 256-thread block
+// with 38 KB of LDS; beyond that, 1024 threads and 88 KB.  The small block
+// matters where the plan runs beside a kernel that fills every CU with small
+// blocks (the fp8 weight cast): a 1024-thread block waits for 16 free wave
+// slots on one CU, which that kernel's blocks take first, and the plan's
+// next kernels wait behind it.
+template <int NT, int MAXE, int STAGE, int STAGE_SRC>
+__global__ __launch_bounds__(NT) void dispatch_scan_kernel(const int32_t* __restrict__ block_counts,
+                                                           const int32_t* __restrict__ block_src, DispatchShape d,
+                                                           int32_t* __restrict__ counts,
+                                                           int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ src_counts,
+                                                           int32_t* __restrict__ block_base) {
+    __shared__ int tot[MAXE + 1];
+    __shared__ int off[MAXE + 1];
+    __shared__ int stage[STAGE];
+    __shared__ int stage_src[STAGE_SRC];
     const int L = d.e1 - d.e0, W = d.E + 1;
     const int64_t n = static_cast<int64_t>(d.nblk) * W;
-    const bool staged = n <= kScanStage, staged_src = d.nblk <= kScanStageSrc;
+    const bool staged = n <= STAGE, staged_src = d.nblk <= STAGE_SRC;
     if (staged)
         for (int i = threadIdx.x; i < n; i += blockDim.x) stage[i] = block_counts[i];
     if (staged_src)
@@ -766,8 +770,12 @@ int dispatch_run(const char* fn, const int32_t* topi, int64_t T, int k, int E, i
                            block_src);
         if (int rc = check_launch("dispatch_count_kernel")) return rc;
     }
-    hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, stream, block_counts, block_src, d, counts,
-                       offsets, src_counts, block_base);
+    if (E + 1 <= 256 && static_cast<int64_t>(d.nblk) * (E + 1) <= 8192)
+        hipLaunchKernelGGL((dispatch_scan_kernel<256, 255, 8192, 1024>), dim3(1), dim3(256), 0, stream, block_counts,
+                           block_src, d, counts, offsets, src_counts, block_base);
+    else
+        hipLaunchKernelGGL((dispatch_scan_kernel<1024, kMaxE, 16384, 4096>), dim3(1), dim3(1024), 0, stream,
+                           block_counts, block_src, d, counts, offsets, src_counts, block_base);
     if (int rc = check_launch("dispatch_scan_kernel")) return rc;
     if (d.nblk > 0) {
         hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(d.nblk), dim3(kThreads), 0, stream, topi, d, block_base,
