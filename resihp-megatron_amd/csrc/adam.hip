@@ -23,6 +23,7 @@
 #pragma clang fp contract(off)
 
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 
 #include "rhp_common.h"
@@ -104,6 +105,45 @@ __device__ __forceinline__ void adam_one(const AdamScalars<typename AdamElem<S>:
     p = E::r(p + div_t(sc.a * m, d));
 }
 
+// Two bfloat16 elements at once, operation for operation as adam_one: each
+// operation's two results are rounded by one v_cvt_pk_bf16_f32 (the rounding
+// AdamElem<bf16>::r applies to each value alone, so the bits are the same)
+// instead of one conversion per value; the step is bound by VALU issue.
+__device__ __forceinline__ void round2(float& x, float& y) {
+    const uint32_t b = pack_bf16x2(x, y);
+    x = __uint_as_float(b << 16);
+    y = __uint_as_float(b & 0xffff0000u);
+}
+__device__ __forceinline__ void adam_two_bf16(const AdamScalars<float>& sc, float (&p)[2], float (&g)[2], float (&m)[2],
+                                              float (&v)[2]) {
+    if (sc.use_wd) {
+        g[0] = fma_t(sc.wd, p[0], g[0]);
+        g[1] = fma_t(sc.wd, p[1], g[1]);
+        round2(g[0], g[1]);
+    }
+    const bool lo = fabsf(sc.w) < 0.5f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) m[i] = lo ? fma_t(sc.w, g[i] - m[i], m[i]) : fma_t(sc.w - 1.0f, g[i] - m[i], g[i]);
+    round2(m[0], m[1]);
+    v[0] = v[0] * sc.b2;
+    v[1] = v[1] * sc.b2;
+    round2(v[0], v[1]);
+    v[0] = fma_t(sc.c * g[0], g[0], v[0]);
+    v[1] = fma_t(sc.c * g[1], g[1], v[1]);
+    round2(v[0], v[1]);
+    float d[2] = {sqrt_t(v[0]), sqrt_t(v[1])};
+    round2(d[0], d[1]);
+    d[0] = div_t(d[0], sc.bc2s);
+    d[1] = div_t(d[1], sc.bc2s);
+    round2(d[0], d[1]);
+    d[0] = d[0] + sc.eps;
+    d[1] = d[1] + sc.eps;
+    round2(d[0], d[1]);
+    p[0] = p[0] + div_t(sc.a * m[0], d[0]);
+    p[1] = p[1] + div_t(sc.a * m[1], d[1]);
+    round2(p[0], p[1]);
+}
+
 // Raw 16-byte groups of 8 elements.
 template <class S> struct Group8 {
     static constexpr int kWords = static_cast<int>(sizeof(S)) * 8 / 16;
@@ -159,14 +199,35 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(AdamTensors ts, Adam
     for (int q = 0; q < kG; ++q) {
         const int64_t e0 = base + (static_cast<int64_t>(q) * kAdamThreads + threadIdx.x) * 8;
         if (e0 < full) {
+            if constexpr (std::is_same<S, bf16>::value) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                T p = to_t<S>(gp[q].at(e)), m = to_t<S>(gm[q].at(e)), v = to_t<S>(gv[q].at(e));
-                const T g = G ? to_t<S>(gg[q].at(e)) : T(0);
-                adam_one<S>(sc, p, g, m, v);
-                gp[q].at(e) = from_t<S>(p);
-                gm[q].at(e) = from_t<S>(m);
-                gv[q].at(e) = from_t<S>(v);
+                for (int e = 0; e < 8; e += 2) {
+                    float p[2], g[2], m[2], v[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        p[i] = to_t<S>(gp[q].at(e + i));
+                        m[i] = to_t<S>(gm[q].at(e + i));
+                        v[i] = to_t<S>(gv[q].at(e + i));
+                        g[i] = G ? to_t<S>(gg[q].at(e + i)) : 0.0f;
+                    }
+                    adam_two_bf16(sc, p, g, m, v);
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        gp[q].at(e + i) = from_t<S>(p[i]);
+                        gm[q].at(e + i) = from_t<S>(m[i]);
+                        gv[q].at(e + i) = from_t<S>(v[i]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    T p = to_t<S>(gp[q].at(e)), m = to_t<S>(gm[q].at(e)), v = to_t<S>(gv[q].at(e));
+                    const T g = G ? to_t<S>(gg[q].at(e)) : T(0);
+                    adam_one<S>(sc, p, g, m, v);
+                    gp[q].at(e) = from_t<S>(p);
+                    gm[q].at(e) = from_t<S>(m);
+                    gv[q].at(e) = from_t<S>(v);
+                }
             }
             gp[q].store(P + e0);
             gm[q].store(M + e0);
