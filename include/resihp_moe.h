@@ -181,6 +181,41 @@ int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, const int32_t
                      int x_dtype, int r_dtype, int64_t T, int h, int E, int k, void* dw, void* workspace,
                      size_t workspace_bytes, hipStream_t stream);
 
+/* ----------------------------------------- sending side of expert parallelism */
+
+/*
+ * Send plan of one source: EPRuntime.forward (resihp/runtime/moe.py:189-211)
+ * up to the exchange.  The pairs of expert e, in (token, slot) order, go to
+ * e's holders in the EP group by smooth_weighted_round_robin
+ * (resihp/plan/expert_placement.py:150-164, moe.py:193-198); the send order is
+ * device-major (the group's devices in world order), then expert-major, then
+ * (token, slot) ascending (moe.py:199-207).
+ *   topi [T*k], counts [E+1], offsets [E+1], pair_row [T*k]: the plan of
+ *       rhp_dispatch with the window [0, E) (every expert), same topi
+ *   pick_off [E+1], pick_dev [pick_off[E]], pick_rank [pick_off[E]],
+ *   period_cnt [E*n_dev]: one period of every expert's holder picks (a smooth
+ *       weighted round robin repeats after the sum of its weights): position
+ *       r of expert e's period sends to device pick_dev[pick_off[e] + r]
+ *       (0 <= d < n_dev), as that device's pick_rank-th pick of the period;
+ *       period_cnt[e * n_dev + d] = picks of d in the period.  Built on the
+ *       host from the placement (placement.send_tables).
+ * Outputs (int32, device):
+ *   send_counts [n_dev * E]   counts[d, e] of moe.py:199-207 (their row sums are the
+ *                             split sizes of moe.py:210)
+ *   send_offsets [n_dev*E+1]  exclusive prefix of send_counts in send order; the rows
+ *                             for device d are [send_offsets[d*E], send_offsets[(d+1)*E])
+ *   send_perm [T*k]           send row -> flat pair t*k + j (rows < send_offsets[n_dev*E];
+ *                             idx_i = pair / k, idx_j = pair % k of moe.py:208-209)
+ *   send_row [T*k]            pair -> send row, -1 for an expert id outside [0, E)
+ * rhp_permute and rhp_combine with send_row as pair_row build the send buffer
+ * (x.index_select(0, idx_i), moe.py:212) and combine the returned rows
+ * (moe.py:225-226).  n_dev * E <= 65536.  Bit-exact with the reference order.
+ */
+int rhp_ep_send_plan(const int32_t* topi, int64_t T, int k, int E, int n_dev, const int32_t* counts,
+                     const int32_t* offsets, const int32_t* pair_row, const int32_t* pick_off, const int32_t* pick_dev,
+                     const int32_t* pick_rank, const int32_t* period_cnt, int32_t* send_counts,
+                     int32_t* send_offsets, int32_t* send_perm, int32_t* send_row, hipStream_t stream);
+
 /* ----------------------------------------- received rows (receiving side of expert parallelism) */
 
 /*
@@ -196,7 +231,10 @@ int rhp_router_wgrad(const void* dlogits_sel, const int32_t* perm, const int32_t
  *   unsort_row[rows]   received row q is expert-major row unsort_row[q]
  * recv_counts: [n_src, L] int32 on the device, the local experts' columns of the
  * exchanged counts (moe.py:209); rows must equal their sum (the reference
- * materialises the split sizes on the host, moe.py:210-211).  n_src * L <= 8192.
+ * materialises the split sizes on the host, moe.py:210-211), which the kernel
+ * writes to offsets[L].  If they differ, every map entry without a partner
+ * among the first `rows` rows is -1 (the products read such a row as zeros and
+ * drop its stores).  n_src * L <= 8192.
  */
 int rhp_recv_plan(const int32_t* recv_counts, int n_src, int L, int64_t rows, int32_t* offsets, int32_t* sort_row,
                   int32_t* unsort_row, hipStream_t stream);

@@ -250,6 +250,70 @@ def received_rows(topis, local, assign=None):
     return cat(src), cat(tok), cat(slot), counts
 
 
+def smooth_weighted_round_robin(holders, speeds, n):
+    """resihp/plan/expert_placement.py:150-164: the n pairs of an expert over its holders.  Weights
+    ``max(1, round(10 * speed))`` (speed 1.0 when absent); every step each holder gains its weight,
+    the largest running weight (ties to the larger name) is picked and pays the total."""
+    if len(holders) == 1:
+        return list(holders) * n
+    weights = {h: max(1, round(10 * speeds.get(h, 1.0))) for h in holders}
+    total = sum(weights.values())
+    current = {h: 0 for h in holders}
+    out = []
+    for _ in range(n):
+        for h in holders:
+            current[h] += weights[h]
+        pick = max(holders, key=lambda h: (current[h], h))
+        current[pick] -= total
+        out.append(pick)
+    return out
+
+
+def send_order_literal(topi, E, ep, holders_of, speeds):
+    """resihp/runtime/moe.py:189-207 as the reference writes it, for small inputs: a dict from
+    (token, slot) to its destination, filled expert by expert in ``nonzero()`` order, then for
+    every device of ``ep`` (send order) and every expert the sorted pairs sent there.
+    ``holders_of(e)`` is ``placement.group_holders(gidx, e)``.  Returns the flat pair ids
+    ``t*k + j`` in send order and ``counts [len(ep), E]``."""
+    topi = torch.as_tensor(np.asarray(topi, np.int64))
+    k = topi.shape[1]
+    dest = {}
+    for e in range(E):
+        pairs = [tuple(p) for p in (topi == e).nonzero().tolist()]
+        if pairs:
+            picks = smooth_weighted_round_robin(holders_of(e), speeds, len(pairs))
+            dest.update(zip(pairs, picks))
+    order = []
+    counts = np.zeros((len(ep), E), np.int64)
+    for di, d in enumerate(ep):
+        for e in range(E):
+            rows = sorted(p for p, h in dest.items() if h == d and int(topi[p]) == e)
+            order += rows
+            counts[di, e] = len(rows)
+    return np.asarray([i * k + j for i, j in order], np.int64), counts
+
+
+def send_order(topi, E, ep, holders_of, speeds):
+    """The same order as ``send_order_literal`` (resihp/runtime/moe.py:189-207) in array form, for
+    large inputs: each expert's pairs in ascending flat id get their round-robin destination, then a
+    stable sort by (destination, expert) keeps the pair order within every chunk.  Pairs with an id
+    outside [0, E) are not sent."""
+    flat = np.asarray(topi, np.int64).reshape(-1)
+    index = {d: i for i, d in enumerate(ep)}
+    dest = np.full(flat.size, -1, np.int64)
+    for e in range(E):
+        pairs = np.nonzero(flat == e)[0]
+        if pairs.size:
+            picks = smooth_weighted_round_robin(holders_of(e), speeds, pairs.size)
+            dest[pairs] = [index[h] for h in picks]
+    sent = np.nonzero(dest >= 0)[0]
+    key = dest[sent] * E + flat[sent]
+    order = sent[np.argsort(key, kind="stable")]
+    counts = np.zeros((len(ep), E), np.int64)
+    np.add.at(counts, (dest[sent], flat[sent]), 1)
+    return order, counts
+
+
 def recv_plan(recv_counts) -> dict[str, np.ndarray]:
     """Expert-major grouping of a received buffer (the chunk order of resihp/runtime/moe.py:213-222,
     regrouped by expert): group i holds the rows of local expert i, sources ascending, each chunk in

@@ -41,6 +41,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "rhp_token_bwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _pp, _i, _i, _i64, _i, _i, _i, _p, _p]),
     "rhp_router_wgrad_workspace_bytes": (_sz, [_i64, _i, _i, _i, _i]),
     "rhp_router_wgrad": (_i, [_p, _p, _p, _p, _i, _i, _i64, _i, _i, _i, _p, _p, _sz, _p]),
+    "rhp_ep_send_plan": (_i, [_p, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "rhp_recv_plan": (_i, [_p, _i, _i, _i64, _p, _p, _p, _p]),
     "rhp_gather_rows": (_i, [_p, _i, _i64, _i, _p, _i64, _p, _p]),
     "rhp_expert_split_workspace_bytes": (_sz, []),

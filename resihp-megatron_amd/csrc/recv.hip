@@ -74,9 +74,13 @@ __global__ __launch_bounds__(kPlanThreads) void recv_plan_kernel(const int32_t* 
         for (int e = threadIdx.x; e < L; e += kPlanThreads) offsets[e] = exp_off[e * n_src];
         if (threadIdx.x == 0) offsets[L] = src_off[n];
     }
-    const int64_t total = min(static_cast<int64_t>(src_off[n]), rows);
-    for (int64_t q = static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x; q < total;
-         q += static_cast<int64_t>(gridDim.x) * kPlanThreads) {
+    // Counts that do not add up to `rows` (a caller error) never write outside the maps, and every
+    // entry of both maps is written: rows past the counts' sum map to -1, and when the counts hold
+    // more rows than `rows`, an expert-major row whose received row lies past `rows` maps to -1.
+    // The products then read such rows as zero rows and drop their stores.
+    const int64_t sum = src_off[n];
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kPlanThreads;
+    for (int64_t q = static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x; q < sum; q += stride) {
         // last chunk c with src_off[c] <= q (empty chunks share their start with the next one)
         int lo = 0, hi = n - 1;
         while (lo < hi) {
@@ -86,9 +90,12 @@ __global__ __launch_bounds__(kPlanThreads) void recv_plan_kernel(const int32_t* 
         }
         const int s = lo / L, e = lo % L;
         const int64_t r = exp_off[e * n_src + s] + (q - src_off[lo]);
-        // Counts that do not add up to `rows` (a caller error) never write outside the maps.
-        unsort_row[q] = static_cast<int32_t>(r);
-        if (r >= 0 && r < rows) sort_row[r] = static_cast<int32_t>(q);
+        if (q < rows) unsort_row[q] = r < rows ? static_cast<int32_t>(r) : -1;
+        if (r < rows) sort_row[r] = q < rows ? static_cast<int32_t>(q) : -1;
+    }
+    for (int64_t q = sum + static_cast<int64_t>(blockIdx.x) * kPlanThreads + threadIdx.x; q < rows; q += stride) {
+        unsort_row[q] = -1;
+        sort_row[q] = -1;
     }
 }
 

@@ -9,6 +9,7 @@ device.  Nothing here computes on the CPU; every entry point goes through
 
 from __future__ import annotations
 
+import collections
 import ctypes
 
 from dataclasses import dataclass
@@ -262,6 +263,56 @@ def router_wgrad(dl: torch.Tensor, perm: torch.Tensor, offsets: torch.Tensor, x:
     return dw
 
 
+# ----------------------------------------------------------------------------- sending side
+
+
+@dataclass
+class SendTables:
+    """One period of every expert's holder picks for one EP group (int32 device tensors), as
+    ``placement.send_tables`` lays them out."""
+
+    pick_off: torch.Tensor     # [E + 1]
+    pick_dev: torch.Tensor     # [pick_off[E]]: device (index in the group's send order) of each pick
+    pick_rank: torch.Tensor    # [pick_off[E]]: picks of the same device earlier in the period
+    period_cnt: torch.Tensor   # [E * n_dev]: picks of each device in expert e's period
+    n_dev: int
+
+    @classmethod
+    def from_lists(cls, off, dev, rank, cnt, n_dev: int, device) -> "SendTables":
+        mk = lambda v: torch.tensor(v if len(v) else [0], dtype=torch.int32, device=device)  # noqa: E731
+        return cls(mk(off), mk(dev), mk(rank), mk(cnt), n_dev)
+
+
+@dataclass
+class SendPlan:
+    """A source's send order for its EP group (all int32 device tensors)."""
+
+    counts: torch.Tensor       # [n_dev, E]: pairs of expert e sent to device d (moe.py:199-207)
+    offsets: torch.Tensor      # [n_dev * E + 1]: chunk starts in send order
+    perm: torch.Tensor         # [T * k]: send row -> flat pair t*k + j (rows < offsets[-1] valid)
+    row: torch.Tensor          # [T * k]: flat pair -> send row, -1 for ids outside [0, E)
+    dispatch: DispatchPlan     # the expert-major plan it was built from (window [0, E))
+
+
+def ep_send_plan(topi: torch.Tensor, E: int, tables: SendTables) -> SendPlan:
+    """Send order of one source's routed pairs over its EP group (resihp/runtime/moe.py:193-211)."""
+    dev = _need_cuda(topi, tables.pick_off)
+    _expect(topi.dtype == torch.int32 and topi.dim() == 2, "topi must be int32 [T, k]")
+    _expect(tables.pick_off.numel() == E + 1 and tables.period_cnt.numel() == E * tables.n_dev,
+            f"send tables must cover {E} experts and {tables.n_dev} devices")
+    T, k = topi.shape
+    plan = dispatch(topi, E)
+    n = tables.n_dev
+    counts = torch.empty(n, E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n * E + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(max(1, T * k), dtype=torch.int32, device=dev)
+    row = torch.empty(max(1, T * k), dtype=torch.int32, device=dev)
+    _call("rhp_ep_send_plan", dev, _ptr(topi), T, k, E, n, _ptr(plan.counts), _ptr(plan.offsets),
+          _ptr(plan.pair_row), _ptr(tables.pick_off), _ptr(tables.pick_dev), _ptr(tables.pick_rank),
+          _ptr(tables.period_cnt), _ptr(counts), _ptr(offsets), _ptr(perm), _ptr(row))
+    return SendPlan(counts, offsets, perm[: T * k], row[: T * k], plan)
+
+
 # ----------------------------------------------------------------------------- received rows
 
 
@@ -352,24 +403,38 @@ def dtype_code_of(dtype: torch.dtype) -> int:
 
 
 # K-split workspaces, one per (device, stream): its arrival counters are shared by every launch that
-# uses it, so launches on two streams must not share one.
-_split_ws_cache: dict[tuple[int, int], torch.Tensor] = {}
+# uses it, so launches on two streams must not share one.  At most _SPLIT_WS_PER_DEVICE streams per
+# device keep one (the least recently used is dropped first), so callers that make a stream per
+# request do not grow device memory without bound.  A workspace is allocated on its own stream, so
+# the caching allocator hands a dropped one's memory only to later work on that stream.
+_SPLIT_WS_PER_DEVICE = 4
+_split_ws_cache: "collections.OrderedDict[tuple[int, int], torch.Tensor]" = collections.OrderedDict()
 
 
 def split_workspace(dev: torch.device, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
     """The K-split workspace of the expert GEMMs for ``stream`` (default: the current stream of ``dev``).
 
-    Allocated and zeroed once per (device, stream).  Its arrival counters must be zero before a call;
-    every call that completes leaves them zero, and a call that fails resets them.
+    Allocated and zeroed once per (device, stream), for the last few streams of a device.  Its arrival
+    counters must be zero before a call; every call that completes leaves them zero, and a call that
+    fails resets them.  Under HIP graph capture a workspace is never allocated: make one call outside
+    the capture on the same stream first, or the call raises.
     """
     idx = torch.device(dev).index if torch.device(dev).index is not None else torch.cuda.current_device()
     stream = stream if stream is not None else torch.cuda.current_stream(idx)
     key = (idx, stream.cuda_stream)
     ws = _split_ws_cache.get(key)
-    if ws is None:
-        with torch.cuda.stream(stream):
-            ws = torch.zeros(C.lib().rhp_expert_split_workspace_bytes(), dtype=torch.uint8, device=f"cuda:{idx}")
-        _split_ws_cache[key] = ws
+    if ws is not None:
+        _split_ws_cache.move_to_end(key)
+        return ws
+    if torch.cuda.is_current_stream_capturing():
+        raise KernelArgumentError("the expert GEMMs' K-split workspace of this stream is not allocated: "
+                                  "call them once on this stream before capturing a graph")
+    with torch.cuda.stream(stream):
+        ws = torch.zeros(C.lib().rhp_expert_split_workspace_bytes(), dtype=torch.uint8, device=f"cuda:{idx}")
+    _split_ws_cache[key] = ws
+    mine = [kk for kk in _split_ws_cache if kk[0] == idx]
+    for kk in mine[:max(0, len(mine) - _SPLIT_WS_PER_DEVICE)]:
+        del _split_ws_cache[kk]
     return ws
 
 

@@ -13,7 +13,10 @@ deliberate:
   unspecified order), and NaN router keys rank last.
 * Cross-GPU expert parallelism is out of scope: ``EPRuntime`` runs when the EP
   group is a single device (``comms.group`` returns None, the reference's
-  local-copy case, moe.py:150-151) and raises otherwise.
+  local-copy case, moe.py:150-151) and raises otherwise.  Both ends of the
+  exchange are built for one GPU: ``EPRuntime.send`` (the send order, counts
+  and rows of moe.py:189-212 for any placement, replicas included) and
+  ``EPRuntime.expert_outputs`` (the received chunks, moe.py:213-224).
 
 Errors surface as ``RuntimeError`` (as ``CommAborted`` / ``CommTimeout`` do in
 the reference), which the resilient trainer treats as recoverable; no kernel
@@ -29,7 +32,7 @@ import torch
 
 from . import kernels as K
 from .layer import LayerMeta, expert_chunks, moe_layer
-from .placement import ExpertPlacement, expert_dp_groups, smooth_weighted_round_robin
+from .placement import ExpertPlacement, expert_dp_groups, send_tables
 from .rng import generator
 from .state import FULL, GroupSpec, Holdings, TensorSpec
 
@@ -353,6 +356,36 @@ class EPRuntime:
         self.tokens_per_expert = counts[:E].to(torch.float64)
         return out
 
+    def send_tables(self) -> K.SendTables:
+        """The holder-pick periods of every expert for this device's EP group (built once)."""
+        if getattr(self, "_send_tables", None) is None:
+            off, dev, rank, cnt = send_tables(self.placement, self.gidx, self.ep, self.speeds)
+            self._send_tables = K.SendTables.from_lists(off, dev, rank, cnt, len(self.ep),
+                                                        self.params["router.weight"].device)
+        return self._send_tables
+
+    def send(self, x: torch.Tensor):
+        """The sending side of the expert-parallel exchange (moe.py:189-212) for this device's tokens.
+
+        Routes ``x``, splits each expert's pairs over its holders in the EP group
+        (smooth_weighted_round_robin with ``speeds``, :193-198) and orders them device-major, then
+        expert-major, then (token, slot) (:199-207).  Returns ``(rows, counts, in_splits, plan,
+        gates)``: ``rows`` [P, h] = ``x.index_select(0, idx_i)`` in send order (:212), ``counts``
+        the ``[|ep|, E]`` int64 matrix exchanged first (:199-209), ``in_splits`` its row sums
+        (:210), the ``K.SendPlan`` (``plan.row`` is the pair -> row map the combine of the
+        returned rows takes, :225-226) and the gates.  Sets ``tokens_per_expert`` like forward."""
+        cfg, E = self.cfg, self.cfg.num_experts
+        bias = self.buffers.get("router.expert_bias")
+        _, topi, gates = K.route(x.detach().contiguous(), self.params["router.weight"].detach().contiguous(),
+                                 None if bias is None else bias.detach().contiguous(), cfg.top_k, cfg.score,
+                                 cfg.normalize, cfg.gate_scale)
+        plan = K.ep_send_plan(topi, E, self.send_tables())
+        self.tokens_per_expert = plan.dispatch.counts[:E].to(torch.float64)
+        counts = plan.counts.to("cpu", torch.int64)
+        P = int(counts.sum())
+        rows = K.permute(x.detach().contiguous(), plan.row, cfg.top_k, P)
+        return rows, counts, counts.sum(1).tolist(), plan, gates
+
     def expert_outputs(self, recv: torch.Tensor, recv_counts: torch.Tensor) -> torch.Tensor:
         """The receiving side of the expert-parallel exchange (moe.py:213-224) for this device's experts.
 
@@ -405,4 +438,4 @@ class EPRuntime:
 
 __all__ = ["MoEConfig", "moe_specs", "expert_of", "init_param", "update_expert_bias", "batch", "route", "expert_ffn",
            "token_loss", "reference_forward", "reference_train", "moe_holdings", "edp_group_name", "moe_group_specs",
-           "EPRuntime", "local_keys", "Adam", "even_split", "smooth_weighted_round_robin"]
+           "EPRuntime", "local_keys", "Adam", "even_split"]

@@ -342,6 +342,34 @@ def test_k_split_workspace_per_stream():
     assert int(counters.abs().sum()) == 0
 
 
+def test_k_split_workspaces_stay_bounded_over_fresh_streams():
+    """A stream per call (a serving loop) does not grow device memory: only the last few streams of a
+    device keep a K-split workspace, and split products on fresh streams keep giving the same bits."""
+    dt, h, f, counts = torch.bfloat16, 256, 8192, [200, 60]
+    G = len(counts)
+    offs = torch.tensor([0, 200, 260], dtype=torch.int32, device=DEV)
+    P = 260
+    gen = torch.Generator(device=DEV).manual_seed(6)
+    a = (torch.randn(P, f, generator=gen, device=DEV)).to(dt)
+    w2 = [(torch.randn(h, f, generator=gen, device=DEV) * 0.02).to(dt) for _ in range(G)]
+    say("gemm k-split workspaces over 10 fresh streams")
+    ref = torch.empty(P, h, dtype=dt, device=DEV)
+    K.expert_fc2_fwd([a] * G, offs, True, P, w2, [ref] * G)
+    torch.cuda.synchronize()
+    dev_idx = torch.device(DEV).index or 0
+    sizes = []
+    for i in range(10):
+        s = torch.cuda.Stream(device=DEV)
+        s.wait_stream(torch.cuda.current_stream(DEV))
+        y = torch.empty(P, h, dtype=dt, device=DEV)
+        with torch.cuda.stream(s):
+            K.expert_fc2_fwd([a] * G, offs, True, P, w2, [y] * G)
+        s.synchronize()
+        assert torch.equal(y, ref), i
+        sizes.append(sum(1 for key in K._split_ws_cache if key[0] == dev_idx))
+    assert max(sizes) <= K._SPLIT_WS_PER_DEVICE and sizes[-1] == K._SPLIT_WS_PER_DEVICE
+
+
 @pytest.mark.parametrize("dtype,h,f,counts,e0", [(torch.bfloat16, 256, 128, [300, 0, 517], 2),
                                                  (torch.bfloat16, 512, 256, [40, 700, 129, 1], 0),
                                                  (torch.bfloat16, 1024, 8192, [200, 330], 1),

@@ -43,6 +43,35 @@ def test_recv_plan_bit_exact(shape, hi):
     assert np.array_equal(plan.unsort_row.cpu().numpy(), ref["unsort_row"])
 
 
+@pytest.mark.parametrize("delta", [-37, 0, 53])
+def test_recv_plan_with_a_wrong_row_count(delta):
+    """A caller's row count that differs from the counts' sum never leaves a map entry unwritten: rows
+    without a partner among the first `rows` map to -1 (read as zero rows, their stores dropped), the
+    rest as with the true count, and offsets[L] holds the true sum."""
+    rng = np.random.default_rng(77)
+    counts = rng.integers(0, 40, size=(4, 6))
+    total = int(counts.sum())
+    rows = total + delta
+    ref = M.recv_plan(counts)
+    say(f"recv plan with rows = sum {delta:+d}")
+    plan = K.recv_plan(torch.from_numpy(counts).to(torch.int32).to(DEV), rows=rows)
+    torch.cuda.synchronize()
+    sort_row = plan.sort_row.cpu().numpy()
+    unsort_row = plan.unsort_row.cpu().numpy()
+    assert sort_row.size == rows and unsort_row.size == rows
+    exp_sort = np.full(rows, -1)
+    exp_unsort = np.full(rows, -1)
+    n = min(rows, total)
+    for r in range(n):
+        q = ref["sort_row"][r]
+        exp_sort[r] = q if q < rows else -1
+    for q in range(n):
+        r = ref["unsort_row"][q]
+        exp_unsort[q] = r if r < rows else -1
+    assert np.array_equal(sort_row, exp_sort) and np.array_equal(unsort_row, exp_unsort)
+    assert int(plan.offsets[-1].item()) == total
+
+
 @pytest.mark.parametrize("dtype,h", [(torch.bfloat16, 2048), (torch.bfloat16, 8), (torch.float32, 100),
                                      (torch.float64, 6), (torch.bfloat16, 4096)])
 def test_gather_rows_bit_exact(dtype, h):
