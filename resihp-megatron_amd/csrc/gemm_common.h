@@ -320,15 +320,15 @@ template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI =
 // A 256 x 256 output tile per workgroup of 8 waves (two per SIMD).  Wave w
 // owns X rows [128 (w % 2), +128) and Y rows [64 (w / 2), +64).  The bf16
 // products hold them in 8 x 4 accumulators of v_mfma_f32_16x16x32_bf16 (128
-// registers), the fp8 products in 4 x 2 of the 32x32x64 fp8 MFMA.  Under load
+// registers), the fp8 products in 4 x 2 of the 32x32x64 fp8 MFMA.  (The bf16
+// forward products run the same tile on 4 waves of 128 x 128 outputs, with
+// their accumulators in AGPRs; grouped_gemm.hip says why.)  Under load
 // the GPU runs at its power limit, so energy per step sets the clock: the
 // 16x16x32 shape reads and writes half the accumulator bytes per FLOP of
 // 32x32x16, and with operands in registers sustains 1.9 PFLOP/s against 1.75.
 // In these kernels it raises the clock by 8-15 % and lowers MFMA busy by
 // about as much for the input gradients (whose step time stays with the
-// operand loads), 3-4 % net for the weight gradients and the forward.  A
-// 4-wave tile of 128 x 128 per wave (one wave per SIMD) hides too little of
-// the 16-cycle MFMA issue stream and runs slower.
+// operand loads), 3-4 % net for the weight gradients and the forward.
 //
 // Operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds:
 // no staging registers and no LDS stores.  One such load moves 64 lanes x 16

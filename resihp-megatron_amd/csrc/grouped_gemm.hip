@@ -42,9 +42,21 @@ namespace {
 
 constexpr int kK64 = 64;
 constexpr int kT64Bytes = kTile * kK64 * 2;                // 32 KB per operand tile
-static_assert((kT64Bytes / 1024) % kWaves == 0, "whole loads per wave");
 
-template <int NW = kWaves>
+// Waves per bf16 tile.  The forward products run on four waves, one per
+// SIMD, each owning 128 x 128 outputs (accumulators in AGPRs): per MFMA they
+// read a third fewer fragment bytes from LDS than eight waves of 128 x 64,
+// and measured on the Mixtral shape fc1 and fc2 forward take 1.7 % and 5.6 %
+// less time (MFMA busy 64-67 % at 1.70-1.85 GHz).  The input- and
+// weight-gradient products keep eight waves, two per SIMD: their transposing
+// LDS reads are twice as many instructions per MFMA, and one wave per SIMD
+// left the MFMAs idle behind them (weight gradients 8.5 % slower, MFMA busy
+// 56 % against 66 %).
+template <int MODE>
+constexpr int bf16_waves() { return MODE == kFwd ? 4 : 8; }
+static_assert((kT64Bytes / 1024) % 8 == 0, "whole loads per wave");
+
+template <int NW>
 struct Dma64Map {
     uint32_t vo[kT64Bytes / 1024 / NW];
     uint32_t fr[8];   // K-major: block-0 offset (block b: XOR 64 b); MN-major: block-0 offset (block b: + 16384 b)
@@ -88,6 +100,47 @@ __device__ __forceinline__ bf16x8_t frag_mn32(const uint8_t* tile, uint32_t fr, 
     const s16x4_t hi =
         __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(q + 4 * 512)));
     return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// One v_mfma_f32_16x16x32_bf16, c += a b.  With four waves a wave's 128 x 128
+// outputs are 256 accumulator registers, which live in AGPRs: written as
+// inline assembly with the accumulator tied to an AGPR operand, every MFMA
+// reads and writes its accumulator in place.  (Through the builtin the
+// register allocator moved accumulators between AGPRs, and through VGPRs,
+// about 100 times per K step, each move waiting for the MFMA that wrote its
+// source.)  The compiler does not know the instruction behind the assembly,
+// so the tile adds the wait states around them itself (mfma_drain,
+// mfma_srcc_ready).  Eight waves keep their 128
+// accumulators in VGPRs through the builtin.
+template <int NW>
+__device__ __forceinline__ void mfma16(f32x4_t& c, const bf16x8_t& a, const bf16x8_t& b) {
+    if constexpr (NW == 4) asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    else c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Wait states the assembly MFMAs need, which the compiler cannot add for
+// instructions it does not know.  mfma_drain: after the last MFMA, before its
+// accumulators are read (an 8-pass XDL result needs 11 wait states on
+// gfx940-class hardware; 24 are given).  mfma_srcc_ready: at the top of every
+// K step, two wait states between a v_accvgpr_write of an accumulator (its
+// zero initialisation, placed wherever the compiler likes before the loop)
+// and an MFMA reading it; a K step is thousands of cycles.  The scheduling
+// barriers keep the instructions on either side where they are.
+template <int NW>
+__device__ __forceinline__ void mfma_drain() {
+    if constexpr (NW == 4) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+template <int NW>
+__device__ __forceinline__ void mfma_srcc_ready() {
+    if constexpr (NW == 4) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 1" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
 // ------------------------------------------------------------------ the MFMA kernel: a ring of five operand slots
@@ -256,18 +309,22 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
         for (int j = 0; j < FY; ++j) acc[i][j] = f32x4_t{};
 
     // Fragments of one k32 block: X fragments 0..7 (16 X rows each) and Y
-    // fragments 0 .. FY - 1.  Y fragments are double-buffered; X fragment q
-    // of the next block is read right after the MFMAs of part q (its last use
-    // in this block), so X takes one set of registers.
+    // fragments 0 .. FY - 1.  Y fragments are double-buffered.  With eight
+    // waves X fragment q of the next block is read right after the MFMAs of
+    // part q (its last use in this block), so X takes one set of registers;
+    // four waves have the registers to double-buffer X too (set xn of the
+    // next block, xc of this one), so no fragment is overwritten right after
+    // an MFMA that reads it.
     typedef bf16x8_t YSet[FY];
-    bf16x8_t xf[8];
+    constexpr int kXSets = NW == 4 ? 2 : 1;
+    bf16x8_t xf[kXSets][8];
     auto kfrag = [](const uint8_t* tile, uint32_t fr, int b) {
         return *reinterpret_cast<const bf16x8_t*>(tile + (fr ^ static_cast<uint32_t>(b << 6)));
     };
     // sx, sy: byte offsets of the slots, wave-uniform values the compiler
     // cannot fold into per-slot address registers.
-    auto read_x = [&](uint32_t sx, int b, int i) {
-        xf[i] = kXK ? kfrag(lds + sx, mx.fr[i], b) : frag_mn32(lds + sx, mx.fr[i], b);
+    auto read_x = [&](int set, uint32_t sx, int b, int i) {
+        xf[set][i] = kXK ? kfrag(lds + sx, mx.fr[i], b) : frag_mn32(lds + sx, mx.fr[i], b);
     };
     auto read_y = [&](YSet& y, uint32_t sy, int b, int j) {
         y[j] = kYK ? kfrag(lds + sy, my.fr[j], b) : frag_mn32(lds + sy, my.fr[j], b);
@@ -279,18 +336,24 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
     // q; and the n loads `load` issues: the loads then reach the address unit
     // at the rate it drains them, instead of every wave queueing a whole tile
     // at once and stalling.
-    auto block = [&](const YSet& yc, YSet& yn, uint32_t sx, uint32_t sy, int b, auto load, auto n_c) {
+    auto block = [&](const YSet& yc, YSet& yn, int xc, int xn, uint32_t sx, uint32_t sy, int b, auto load, auto n_c) {
         constexpr int n = decltype(n_c)::value;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             if (q < 4) {
 #pragma unroll
                 for (int j = FY * q / 4; j < FY * (q + 1) / 4; ++j) read_y(yn, sy, b, j);
+                // Double-buffered X: the next block's X fragments go in over the first half
+                // too, so none of the block's reads is still in flight at its end.
+                if constexpr (kXSets == 2) {
+                    read_x(xn, sx, b, 2 * q);
+                    read_x(xn, sx, b, 2 * q + 1);
+                }
             }
 #pragma unroll
             for (int j = 0; j < FY; ++j)
-                acc[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[q], yc[j], acc[q][j], 0, 0, 0);
-            read_x(sx, b, q);
+                mfma16<NW>(acc[q][j], xf[xc][q], yc[j]);
+            if constexpr (kXSets == 1) read_x(xn, sx, b, q);
 #pragma unroll
             for (int l = n * q / 8; l < n * (q + 1) / 8; ++l) load(l);
             __builtin_amdgcn_sched_barrier(0);
@@ -322,7 +385,7 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
 #pragma unroll
             for (int j = 0; j < FY; ++j) read_y(ya, kT64Bytes, 0, j);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) read_x(0, 0, i);
+            for (int i = 0; i < 8; ++i) read_x(0, 0, 0, i);
             // lgkmcnt(0): the loop's first block then waits only for the
             // fragments it uses.  With these reads still counted on entry, the
             // compiler's wait analysis, which merges the entry and the loop's own
@@ -336,13 +399,14 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
             // X of step kt leaves, with block 1.
             int sx = 0, sy = 1, nx = 2, ny = 3, fx = 4;
             for (int kt = 0; kt < nk; ++kt) {
-                block(ya, yb, sx * kT64Bytes, sy * kT64Bytes, 1, [&](int l) { issue_x(kt + 2, fx, l, l + 1); },
+                mfma_srcc_ready<NW>();
+                block(ya, yb, 0, kXSets - 1, sx * kT64Bytes, sy * kT64Bytes, 1, [&](int l) { issue_x(kt + 2, fx, l, l + 1); },
                       Pending{});
                 // Steps up to kt + 1 complete (X of step kt + 2 in flight),
                 // every read of slots sx and sy done.
                 wait_lds(Pending{});
                 barrier();
-                block(yb, ya, nx * kT64Bytes, ny * kT64Bytes, 0, [&](int l) { issue_y(kt + 2, sx, l, l + 1); },
+                block(yb, ya, kXSets - 1, 0, nx * kT64Bytes, ny * kT64Bytes, 0, [&](int l) { issue_y(kt + 2, sx, l, l + 1); },
                       Pending{});
                 const int x2 = fx, y2 = sx;
                 fx = sy;
@@ -354,6 +418,7 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
         }
         wait_loads_all();   // the tiles past the last step
     }
+    mfma_drain<NW>();
     Acc16<WY> out;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -505,7 +570,7 @@ void launch_one(const Job& j, const Params& p, hipStream_t s) {
         if (!nb) return;
         // A K split adds at most one round of pieces to each XCD's items.
         if (MODE != kWgrad && p.split_cap > 1) nb = kXcds * ((nb + kXcds - 1) / kXcds + p.cu_per_xcd);
-        constexpr int nw = kWaves;
+        constexpr int nw = bf16_waves<MODE>();
         if constexpr (MODE != kWgrad) {
             if (j.a_idx || j.c_idx) {
                 hipLaunchKernelGGL((gg_bf16_kernel<MODE, EPI, nw, false, true>), dim3(static_cast<unsigned>(nb)),
