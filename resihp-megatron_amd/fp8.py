@@ -86,17 +86,28 @@ class Fp8State:
 
     def load_state_tensors(self, tensors: dict[str, torch.Tensor], experts: list[int]) -> None:
         """Copies a keyed state (``state_tensors`` of any holder) into this one, whose local slots hold
-        ``experts``; a missing key or a wrong shape raises and leaves this state unchanged."""
+        ``experts``; a missing key, a wrong shape or a wrong dtype raises and leaves this state unchanged.
+
+        Nothing is converted by value: a pending amax (``.amax``, a float held as its bits in int32) also
+        accepts a float32 tensor of the amax itself, as the reference keeps its pending amax
+        (resihp/runtime/reference_model.py:207, 263), and takes its bits."""
         mine = self.state_tensors(experts)
         missing = [k for k in mine if k not in tensors]
         if missing:
             raise KeyError(f"fp8 state misses {missing[0]}")
+        src = {}
         for k, dst in mine.items():
-            if tuple(tensors[k].shape) != tuple(dst.shape):
-                raise ValueError(f"{k} has shape {tuple(tensors[k].shape)}, expected {tuple(dst.shape)}")
+            t = tensors[k]
+            if tuple(t.shape) != tuple(dst.shape):
+                raise ValueError(f"{k} has shape {tuple(t.shape)}, expected {tuple(dst.shape)}")
+            if k.endswith(".amax") and t.dtype == torch.float32:
+                t = t.contiguous().view(torch.int32)
+            if t.dtype != dst.dtype:
+                raise TypeError(f"{k} has dtype {t.dtype}, expected {dst.dtype}")
+            src[k] = t
         with torch.no_grad():
             for k, dst in mine.items():
-                dst.copy_(tensors[k].to(dst.device, dst.dtype))
+                dst.copy_(src[k].to(dst.device))
 
     def finish_iteration(self) -> None:
         """Prepend every pending amax to its history and reset it (reference_model.py:212-216)."""

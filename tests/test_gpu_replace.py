@@ -171,3 +171,15 @@ def test_fp8_state_by_key_follows_the_expert_not_the_slot():
     with pytest.raises(KeyError):
         dst.load_state_tensors(partial, [2, 5, 9])
     assert torch.equal(dst.history, before)
+    # nothing is converted by value: a pending amax given as float32 (the reference's pending_amax)
+    # arrives as its bits, any other dtype mismatch raises and changes nothing
+    as_float = dict(src)
+    as_float["experts.5.fc1.amax"] = torch.tensor([3.7], dtype=torch.float32, device=DEV)
+    dst.load_state_tensors(as_float, [2, 5, 9])
+    assert dst.amax[dst.w1(1)].view(torch.float32).item() == pytest.approx(3.7, rel=1e-7)
+    bad = dict(src)
+    bad["fp8.expert_input.amax_history"] = src["fp8.expert_input.amax_history"].double()
+    before_amax = dst.amax.clone()
+    with pytest.raises(TypeError):
+        dst.load_state_tensors(bad, [2, 5, 9])
+    assert torch.equal(dst.amax, before_amax)
