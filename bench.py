@@ -353,6 +353,57 @@ def copy_probe(nbytes: int) -> int:
     return 0
 
 
+def dense_probe(reps: int) -> int:
+    """The vendor library (hipBLASLt through torch.mm) on the dense products of the Mixtral-shape layer:
+    each of the six expert products once with all 16384 routed rows in one matrix (the weight gradients
+    then reduce over all rows) and once per expert on 2048 rows, bf16, 2-D products only.  Prints one
+    JSON line per product with its TFLOP/s; run under rocprofv3 it names the library's kernels and
+    gives their counters beside those of the grouped kernels."""
+    dev = torch.device("cuda:0")
+    P, h, f, E = 16384, 4096, 14336, 8
+    g = torch.Generator(device=dev).manual_seed(3)
+
+    def rnd(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * std).to(torch.bfloat16)
+
+    x, w1, w2 = rnd(P, h), rnd(2 * f, h, std=0.02), rnd(h, f, std=0.02)
+    act, dy, dh = rnd(P, f), rnd(P, h), rnd(P, 2 * f)
+    products = {   # name: (left, right, FLOP); right operands of the forms the layer's products read
+        "fc1_fwd": (lambda a, r: torch.mm(a, w1.t()), x, 2 * P * h * 2 * f),
+        "fc2_fwd": (lambda a, r: torch.mm(a, w2.t()), act, 2 * P * f * h),
+        "fc2_dgrad": (lambda a, r: torch.mm(a, w2), dy, 2 * P * h * f),
+        "fc2_wgrad": (lambda a, r: torch.mm(a.t(), r), dy, 2 * P * h * f),
+        "fc1_dgrad": (lambda a, r: torch.mm(a, w1), dh, 2 * P * 2 * f * h),
+        "fc1_wgrad": (lambda a, r: torch.mm(a.t(), r), dh, 2 * P * 2 * f * h),
+    }
+    right = {"fc2_wgrad": act, "fc1_wgrad": x}
+    stream = torch.cuda.current_stream(dev)
+    for name, (fn, a, flop) in products.items():
+        r = right.get(name)
+        for split in (1, E):
+            rows = P // split
+
+            def run():
+                for e in range(split):
+                    sl = slice(e * rows, (e + 1) * rows)
+                    fn(a[sl], r[sl] if r is not None else None)
+
+            for _ in range(3):
+                run()
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record(stream)
+            for _ in range(reps):
+                run()
+            t1.record(stream)
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / reps
+            print(json.dumps({"dense_probe": name, "rows_per_product": rows, "products": split, "ms": round(ms, 4),
+                              "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+                              "frac_of_2500": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}), flush=True)
+    return 0
+
+
 def gemm_traffic(workload: str) -> float | None:
     """HBM bytes per step of the grouped GEMM launches, from profiles/gemm_traffic_<workload>.json
     (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), when it was measured."""
@@ -372,9 +423,13 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only copy BYTES bytes on the device three times (calibrates HBM byte counters)")
+    ap.add_argument("--dense-probe", type=int, default=0, metavar="REPS",
+                    help="only time the vendor library's dense products of the Mixtral-shape layer (REPS each)")
     args = ap.parse_args()
     if args.copy_probe:
         return copy_probe(args.copy_probe)
+    if args.dense_probe:
+        return dense_probe(args.dense_probe)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs the MoE layer on one GPU; multi-GPU expert parallelism "
                                    "(the all-to-all dispatch) is not part of it", "n_gpus": args.gpus}))
