@@ -329,34 +329,77 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
     auto read_y = [&](YSet& y, uint32_t sy, int b, int j) {
         y[j] = kYK ? kfrag(lds + sy, my.fr[j], b) : frag_mn32(lds + sy, my.fr[j], b);
     };
-    // The MFMAs of one k32 block (X fragments xf, Y fragments yc) in eight
-    // parts, part q being X fragment q with every Y fragment.  Spread over the
-    // parts go the reads of the next block (block b of slots sx, sy): its Y
-    // fragments (into yn) over the first four parts, X fragment q after part
-    // q; and the n loads `load` issues: the loads then reach the address unit
-    // at the rate it drains them, instead of every wave queueing a whole tile
-    // at once and stalling.
+    // The MFMAs of one k32 block (X fragments xf[xc], Y fragments yc), with
+    // the reads of the next block (block b of slots sx, sy: its Y fragments
+    // into yn, its X fragments into xf[xn]) and the n loads `load` issues
+    // spread between them: the loads then reach the address unit at the rate
+    // it drains them, instead of every wave queueing a whole tile at once and
+    // stalling, and each memory instruction issues while an MFMA runs.  Which
+    // MFMA each read or load follows differs by wave count and mode (below);
+    // a per-tile timing copy of the kernel (cycle stamps around each K step)
+    // measured each order.
     auto block = [&](const YSet& yc, YSet& yn, int xc, int xn, uint32_t sx, uint32_t sy, int b, auto load, auto n_c) {
         constexpr int n = decltype(n_c)::value;
+        if constexpr (kXSets == 2) {
+            // Four waves: one memory instruction after every other MFMA, over the first
+            // 3 n MFMAs of the block: the 16 fragment reads of the next block (its Y
+            // fragments first) and the n loads, one load after every two reads.  Each
+            // then issues in the shadow of the MFMA before it; clustered between groups of
+            // MFMAs they left the MFMA pipe idle while they issued.
+            constexpr int kReads = FY + 8, kOps = kReads + n;
+            static_assert(2 * kOps <= 8 * FY, "memory instructions fit between the MFMAs");
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            if (q < 4) {
+            for (int m = 0; m < 8 * FY; ++m) {
+                mfma16<NW>(acc[m / FY][m % FY], xf[xc][m / FY], yc[m % FY]);
+                if (m % 2 == 1 && m / 2 < kOps) {
+                    const int i = m / 2;
+                    if (i % 3 == 2) {
+                        load(i / 3);
+                    } else {
+                        const int r = i - i / 3;
+                        if (r < FY) read_y(yn, sy, b, r);
+                        else read_x(xn, sx, b, r - FY);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else if constexpr (MODE == kWgrad) {
+            // Eight waves (X single-buffered), weight gradients: in part q, X fragment q of
+            // the next block is read after the part's last MFMA (its last use), the next
+            // block's Y fragments go in over the first parts and the loads over all parts,
+            // each placed after one MFMA (K step 2700 -> 2520 cycles against the grouping by
+            // part below, whose LDS reads the compiler clusters between MFMA groups).
+            static_assert(FY == 4 && n <= 8, "eight waves: four Y fragments, at most a load a part");
 #pragma unroll
-                for (int j = FY * q / 4; j < FY * (q + 1) / 4; ++j) read_y(yn, sy, b, j);
-                // Double-buffered X: the next block's X fragments go in over the first half
-                // too, so none of the block's reads is still in flight at its end.
-                if constexpr (kXSets == 2) {
-                    read_x(xn, sx, b, 2 * q);
-                    read_x(xn, sx, b, 2 * q + 1);
+            for (int q = 0; q < 8; ++q) {
+#pragma unroll
+                for (int j = 0; j < FY; ++j) {
+                    mfma16<NW>(acc[q][j], xf[xc][q], yc[j]);
+                    if (j == 0 && q < 4) read_y(yn, sy, b, q);
+                    if (j == 1 && n * q / 8 < n * (q + 1) / 8) load(n * q / 8);
+                    if (j == FY - 1) read_x(xn, sx, b, q);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
+        } else {
+            // Eight waves, input gradients: the eight parts of a block, part q being X
+            // fragment q with every Y fragment; the next block's Y fragments are read over
+            // the first four parts, its X fragment q after part q, and the loads spread one or
+            // none a part (placing each read and load after its own MFMA, as the weight
+            // gradients do, measured 0.6-1.2 % slower here).
 #pragma unroll
-            for (int j = 0; j < FY; ++j)
-                mfma16<NW>(acc[q][j], xf[xc][q], yc[j]);
-            if constexpr (kXSets == 1) read_x(xn, sx, b, q);
+            for (int q = 0; q < 8; ++q) {
+                if (q < 4) {
 #pragma unroll
-            for (int l = n * q / 8; l < n * (q + 1) / 8; ++l) load(l);
-            __builtin_amdgcn_sched_barrier(0);
+                    for (int j = FY * q / 4; j < FY * (q + 1) / 4; ++j) read_y(yn, sy, b, j);
+                }
+#pragma unroll
+                for (int j = 0; j < FY; ++j) mfma16<NW>(acc[q][j], xf[xc][q], yc[j]);
+                read_x(xn, sx, b, q);
+#pragma unroll
+                for (int l = n * q / 8; l < n * (q + 1) / 8; ++l) load(l);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
     using Pending = std::integral_constant<int, kPerWave>;        // one operand tile stays in flight
