@@ -285,20 +285,24 @@ def test_expert_outputs_reject_unhosted_expert():
         rt.expert_outputs(recv, torch.from_numpy(full))
 
 
-def test_config4_from_received_buffer_full_size():
-    """Config 4 at its full size: 32768 source tokens (8 x 4096) and the hot share's ~226 K received
-    rows.  Plan bit-exact; 256 sampled rows' outputs and input gradients, and 16 x 16 sampled elements
-    of each expert's two weight gradients (each a sum over all of the expert's rows), against float64."""
-    window = (0, 16)
+@pytest.mark.parametrize("window", [(0, 16), (112, 128)], ids=["hot-share", "tail-share"])
+def test_config4_from_received_buffer_full_size(window):
+    """Config 4 at its full size: 32768 source tokens (8 x 4096) and the received rows of the hot share
+    (~226 K) or of the tail share, where the empty experts are.  Plan bit-exact; 256 sampled rows'
+    outputs and input gradients, and 16 x 16 sampled elements of each expert's two weight gradients
+    (each a sum over all of the expert's rows; zero for an empty expert), against float64."""
+    e0, e1 = window
     cfg, recv, counts, src, w1, w2 = _ep_share(32768, window)
     P = recv.shape[0]
     rt, params = _runtime(cfg, window, w1, w2)
     full = np.zeros((8, 128), np.int64)
-    full[:, :16] = counts
+    full[:, e0:e1] = counts
+    if e0 == 112:
+        assert (counts.sum(0) == 0).any(), "the Zipf tail share holds empty experts"
     recv = recv.requires_grad_(True)
     g = torch.Generator(device=DEV).manual_seed(17)
     dy = torch.randn(P, 2048, generator=g, device=DEV).to(torch.bfloat16)
-    say(f"config 4 full size: {P} received rows")
+    say(f"config 4 full size {window}: {P} received rows, counts per expert {counts.sum(0).tolist()}")
     y = rt.expert_outputs(recv, torch.from_numpy(full))
     y.backward(dy)
     torch.cuda.synchronize()
@@ -308,12 +312,12 @@ def test_config4_from_received_buffer_full_size():
     # expert of every received row
     chunk_exp = np.repeat(np.tile(np.arange(16), 8), counts.reshape(-1))
     rng = np.random.default_rng(5)
-    rows = torch.from_numpy(rng.choice(P, 256, replace=False))
+    rows = torch.from_numpy(rng.choice(P, min(256, P), replace=False))
     c64 = lambda t: t.detach().cpu().double()  # noqa: E731
     xs, dys = c64(recv[rows.to(DEV)]), c64(dy[rows.to(DEV)])
-    yr, dxr = torch.zeros(256, 2048, dtype=torch.float64), torch.zeros(256, 2048, dtype=torch.float64)
-    for e in range(16):
-        sel = torch.from_numpy(np.nonzero(chunk_exp[rows.numpy()] == e)[0])
+    yr, dxr = torch.zeros(rows.numel(), 2048, dtype=torch.float64), torch.zeros(rows.numel(), 2048, dtype=torch.float64)
+    for i, e in enumerate(range(e0, e1)):
+        sel = torch.from_numpy(np.nonzero(chunk_exp[rows.numpy()] == i)[0])
         if sel.numel():
             xe = xs[sel].clone().requires_grad_(True)
             out = _swiglu64(xe, c64(w1[e]), c64(w2[e]))
@@ -324,8 +328,8 @@ def test_config4_from_received_buffer_full_size():
     f = 768
     cols = torch.from_numpy(rng.choice(f, 16, replace=False))
     outs = torch.from_numpy(rng.choice(2048, 16, replace=False))
-    for e in range(16):
-        q = torch.from_numpy(np.nonzero(chunk_exp == e)[0]).to(DEV)
+    for i, e in enumerate(range(e0, e1)):
+        q = torch.from_numpy(np.nonzero(chunk_exp == i)[0]).to(DEV)
         xe, dye = c64(recv[q]), c64(dy[q])
         W1, W2 = c64(w1[e]), c64(w2[e])
         gt, up = xe @ W1[cols].t(), xe @ W1[f + cols].t()
