@@ -496,12 +496,73 @@ __device__ __forceinline__ int64_t tile_first_row(const Tile& t) {
 // The pre-activation values a backward epilogue needs (GELU: hpre, SwiGLU:
 // gate and up), loaded for one half before its accumulators are staged.
 // Thread t covers rows r0 + t / 64 + (NT / 64) n and columns 4 (t % 64) .. + 3.
+__device__ __forceinline__ void unpack_bf16x4(uint2 v, float* o) {
+    o[0] = __uint_as_float(v.x << 16);
+    o[1] = __uint_as_float(v.x & 0xffff0000u);
+    o[2] = __uint_as_float(v.y << 16);
+    o[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+
 template <int EPI, int NT>
 struct AuxHalf {
     static constexpr int kPieces = kEpRows * 64 / NT;     // 4-column pieces per thread
     static constexpr int kParts = EPI == kEpiSwigluBwd ? 2 : EPI == kEpiGeluBwd ? 1 : 0;
     uint2 v[kParts ? kPieces : 1][kParts ? kParts : 1];
 };
+
+// The SwiGLU backward's two saved factors for one half in 8-column pieces
+// (16-byte loads): thread t covers columns 8 (t % 32) .. + 7 of rows
+// r0 + t / 32 + (NT / 32) n.  Half the load and store instructions of 4-column
+// pieces: with 256 load instructions a CU, the 8-byte form spent 6 µs issuing
+// them before the half could be staged.
+typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
+template <int NT>
+struct AuxHalfWide {
+    static constexpr int kPieces = kEpRows * 32 / NT;
+    u32x4v_t v[kPieces][2];
+};
+
+template <int MODE, int NT>
+__device__ __forceinline__ void load_aux_half_wide(const Params& p, const Tile& t, int r0, AuxHalfWide<NT>& aux) {
+    const __amdgpu_buffer_rsrc_t view = tile_view(p.aux[t.g], tile_first_row<MODE>(t), p.ldaux, t.x0, t.y_lim);
+    const int x = (threadIdx.x & 31) * 8;
+    uint32_t off = x < t.x_lim ? static_cast<uint32_t>(((r0 + (threadIdx.x >> 5)) * p.ldaux + x) * 2) : kOutOfRange;
+    const uint32_t step = static_cast<uint32_t>((NT / 32) * p.ldaux * 2);
+#pragma unroll
+    for (int n = 0; n < AuxHalfWide<NT>::kPieces; ++n, off += step) {
+        aux.v[n][0] = __builtin_bit_cast(u32x4v_t, __builtin_amdgcn_raw_buffer_load_b128(view, static_cast<int>(off), 0, 0));
+        aux.v[n][1] = __builtin_bit_cast(u32x4v_t, __builtin_amdgcn_raw_buffer_load_b128(view, static_cast<int>(off),
+                                                                                         p.f * 2, 0));
+    }
+}
+
+// The SwiGLU backward's store of one staged half in 8-column pieces: the
+// activation gradient times each saved factor, [dact u silu'(g) | dact silu(g)].
+template <int MODE, int NT>
+__device__ __forceinline__ void epilogue_half_swiglu_bwd_wide(const Params& p, const Tile& t, const float* ep, int r0,
+                                                              const AuxHalfWide<NT>& aux) {
+    const __amdgpu_buffer_rsrc_t ov = tile_view(p.c[t.g], tile_first_row<MODE>(t), p.ldc, t.x0, t.y_lim);
+    const int rr = threadIdx.x >> 5, x = (threadIdx.x & 31) * 8;
+    uint32_t off = x < t.x_lim ? static_cast<uint32_t>(((r0 + rr) * p.ldc + x) * 2) : kOutOfRange;
+    const uint32_t step = static_cast<uint32_t>((NT / 32) * p.ldc * 2);
+#pragma unroll
+    for (int n = 0; n < AuxHalfWide<NT>::kPieces; ++n, off += step) {
+        const int r = rr + n * (NT / 32);
+        const float4 a = lds_f4(ep, r, x), b = lds_f4(ep, r, x + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        u32x4v_t o[2];
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+            float f[8];
+            unpack_bf16x4(make_uint2(aux.v[n][part][0], aux.v[n][part][1]), f);
+            unpack_bf16x4(make_uint2(aux.v[n][part][2], aux.v[n][part][3]), f + 4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[part][q] = pack_bf16x2(v[2 * q] * f[2 * q], v[2 * q + 1] * f[2 * q + 1]);
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(o[0], ov, static_cast<int>(off), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(o[1], ov, static_cast<int>(off), p.f * 2, 0);
+    }
+}
 
 template <int MODE, int EPI, int NT>
 __device__ __forceinline__ void load_aux_half(const Params& p, const Tile& t, int r0, AuxHalf<EPI, NT>& aux) {
@@ -516,13 +577,6 @@ __device__ __forceinline__ void load_aux_half(const Params& p, const Tile& t, in
             if constexpr (EPI == kEpiSwigluBwd) aux.v[n][1] = view_load_b64(view, off, static_cast<uint32_t>(p.f * 2));
         }
     }
-}
-
-__device__ __forceinline__ void unpack_bf16x4(uint2 v, float* o) {
-    o[0] = __uint_as_float(v.x << 16);
-    o[1] = __uint_as_float(v.x & 0xffff0000u);
-    o[2] = __uint_as_float(v.y << 16);
-    o[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
 // Rows [r0, r0 + 128) of the tile, staged in ep.  Thread t of NT handles
@@ -840,8 +894,12 @@ struct SplitSum {
 template <int HALF, int MODE, int EPI, int NT, int QF, bool MAP, class Acc>
 __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, float* ep, const Acc& acc, int wx, int wy,
                                               int wy_rows, int lane, float mul, const SplitSum& split, QuantAcc& qa) {
-    AuxHalf<EPI, NT> aux;
-    load_aux_half<MODE, EPI, NT>(p, t, HALF * kEpRows, aux);
+    // The bf16 SwiGLU backward loads and stores 8-column pieces; every other epilogue 4-column ones.
+    constexpr bool kWide = EPI == kEpiSwigluBwd && QF < 0;
+    AuxHalf<kWide ? kEpiStore : EPI, NT> aux;
+    AuxHalfWide<NT> aux_w;
+    if constexpr (kWide) load_aux_half_wide<MODE, NT>(p, t, HALF * kEpRows, aux_w);
+    else load_aux_half<MODE, EPI, NT>(p, t, HALF * kEpRows, aux);
     int32_t dst_rows = -1;
     if constexpr (MAP && EPI == kEpiStore && QF < 0)
         if (p.c_idx != nullptr) dst_rows = scatter_rows_half<NT>(p, t, HALF * kEpRows);
@@ -883,6 +941,8 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
     lds_barrier();
     if constexpr (QF >= 0)
         epilogue_half_q<MODE, EPI, NT, QF>(p, t, ep, HALF * kEpRows, aux, qa);
+    else if constexpr (kWide)
+        epilogue_half_swiglu_bwd_wide<MODE, NT>(p, t, ep, HALF * kEpRows, aux_w);
     else
         epilogue_half<MODE, EPI, NT, MAP>(p, t, ep, HALF * kEpRows, aux, dst_rows);
 }
