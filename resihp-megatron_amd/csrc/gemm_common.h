@@ -221,11 +221,25 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
         t->k_end = max(0, min(t->k_end, p.rows_cap - (p.rows_from_offsets ? r0 : 0)));
         return kTileOk;
     }
-    uint32_t total = 0;
-    for (int g = 0; g < p.G; ++g) {
-        const int M = p.offsets[g + 1] - p.offsets[g];
-        total += static_cast<uint32_t>((M + yt_rows - 1) / yt_rows) * xt_n;
+    // Lane g of the wave holds group g (at most 64 groups a launch): its rows,
+    // first row and tile count; an inclusive scan over the lanes gives where
+    // each group's tiles end.  (A loop over the groups costs a dependent
+    // scalar load per group: with 64 groups, microseconds a block.)
+    static_assert(kMaxG <= 64, "one group per lane");
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    int g_first = 0, g_rows = 0;
+    if (lane < p.G) {
+        g_first = p.offsets[lane];
+        g_rows = p.offsets[lane + 1] - g_first;
     }
+    const uint32_t g_tiles = static_cast<uint32_t>((g_rows + yt_rows - 1) / yt_rows) * xt_n;
+    uint32_t g_end = g_tiles;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t v = __shfl_up(g_end, d);
+        if (lane >= d) g_end += v;
+    }
+    const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(g_end), 63));
     t->piece = 0;
     t->pieces = 1;
     t->slot = 0;
@@ -262,11 +276,15 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
         if (bid >= total) return kTileDone;
         L = xcd_remap(bid, total);
     }
-    for (int g = 0; g < p.G; ++g) {
-        const int M = p.offsets[g + 1] - p.offsets[g];
+    {
+        // The group of item L: the first whose tiles end past it.
+        const uint64_t past = __ballot(g_end > L);
+        if (past == 0) return kTileDone;
+        const int g = __ffsll(static_cast<unsigned long long>(past)) - 1;
+        L -= static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(g_end - g_tiles), g));
+        const int M = __builtin_amdgcn_readlane(g_rows, g);
         const int mt = (M + yt_rows - 1) / yt_rows;
-        const uint32_t n_tiles = static_cast<uint32_t>(mt) * xt_n;
-        if (L < n_tiles) {
+        {
             // Panels of at most kRowPanel row tiles (of balanced height), column
             // tiles outer within a panel: the 32 consecutive tiles an XCD runs at
             // a time then span 5-8 row tiles by 4-6 column tiles instead of a
@@ -292,7 +310,7 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
             t->x_lim = p.N - t->x0;
             t->y0 = yt * yt_rows;
             t->y_lim = M - t->y0;
-            t->row0 = p.rows_from_offsets ? p.offsets[g] : 0;
+            t->row0 = p.rows_from_offsets ? __builtin_amdgcn_readlane(g_first, g) : 0;
             t->k_begin = 0;
             t->k_end = p.K;
             if (t->pieces > 1) {
@@ -306,9 +324,7 @@ __device__ __forceinline__ int find_tile(const Params& p, int xt_cols, int yt_ro
             t->y_lim = min(t->y_lim, p.rows_cap - static_cast<int>(t->row0) - t->y0);
             return t->y_lim > 0 ? kTileOk : kTileSkip;
         }
-        L -= n_tiles;
     }
-    return kTileDone;
 }
 
 // X columns covered by one MFMA tile: SwiGLU FWD tiles cover 128 activation
