@@ -896,6 +896,47 @@ __device__ __forceinline__ void epilogue_half_q(const Params& p, const Tile& t, 
     }
 }
 
+// The quantising SwiGLU backward in 8-column pieces (thread t: columns
+// 8 (t % 32) .. + 7 of rows r0 + t / 32 + (NT / 32) n): the factors come in
+// 16-byte loads and each part's eight codes leave in one 8-byte store, a
+// quarter of the 4-byte code stores of 4-column pieces (which cost the
+// launch 15 %).  A row is still read and overwritten by one wave only (its
+// 32 lanes), so the codes go to the row's own staging space as before.
+template <int MODE, int NT, int QF>
+__device__ __forceinline__ void epilogue_half_q_swiglu_bwd_wide(const Params& p, const Tile& t, float* ep, int r0,
+                                                                const AuxHalfWide<NT>& aux, QuantAcc& qa) {
+    const __amdgpu_buffer_rsrc_t qv = code_view(p.q, tile_first_row<MODE>(t), p.q_ld, t.x0, t.y_lim);
+    const int rr = threadIdx.x >> 5, x = (threadIdx.x & 31) * 8;
+    const bool ok = x < t.x_lim;
+    uint32_t oq = ok ? static_cast<uint32_t>((r0 + rr) * p.q_ld + x) : kOutOfRange;
+    const uint32_t sq = static_cast<uint32_t>((NT / 32) * p.q_ld);
+#pragma unroll
+    for (int n = 0; n < AuxHalfWide<NT>::kPieces; ++n, oq += sq) {
+        const int r = rr + n * (NT / 32);
+        const bool valid = ok && r0 + r < t.y_lim;
+        const float4 a = lds_f4(ep, r, x), b = lds_f4(ep, r, x + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {   // the saved factors [u silu'(g) | silu(g)]
+            float f[8];
+            unpack_bf16x4(make_uint2(aux.v[n][part][0], aux.v[n][part][1]), f);
+            unpack_bf16x4(make_uint2(aux.v[n][part][2], aux.v[n][part][3]), f + 4);
+            const uint32_t c0 = quant4<QF>(v[0] * f[0], v[1] * f[1], v[2] * f[2], v[3] * f[3], valid, qa);
+            const uint32_t c1 = quant4<QF>(v[4] * f[4], v[5] * f[5], v[6] * f[6], v[7] * f[7], valid, qa);
+            u32x2_t w;
+            w[0] = c0;
+            w[1] = c1;
+            __builtin_amdgcn_raw_buffer_store_b64(w, qv, static_cast<int>(oq), part * p.f, 0);
+            if (p.qt)
+                *reinterpret_cast<uint2*>(&ep[code_word(r, part * 64 + 2 * (threadIdx.x & 31))]) = make_uint2(c0, c1);
+        }
+    }
+    if (p.qt) {   // the transposed copy (uniform: every wave takes the same branch)
+        lds_barrier();
+        store_transposed_half<128, 64, NT>(p, t, ep, r0);
+    }
+}
+
 // The partial tiles of a K-split tile's pieces: piece q at first + q * stride
 // (float4 units), each thread's accumulator piece n at float4 n NT + thread
 // (thread-major).  pieces = 0: no split, the accumulators are the tile.
@@ -910,8 +951,8 @@ struct SplitSum {
 template <int HALF, int MODE, int EPI, int NT, int QF, bool MAP, class Acc>
 __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, float* ep, const Acc& acc, int wx, int wy,
                                               int wy_rows, int lane, float mul, const SplitSum& split, QuantAcc& qa) {
-    // The bf16 SwiGLU backward loads and stores 8-column pieces; every other epilogue 4-column ones.
-    constexpr bool kWide = EPI == kEpiSwigluBwd && QF < 0;
+    // The SwiGLU backward loads and stores 8-column pieces; every other epilogue 4-column ones.
+    constexpr bool kWide = EPI == kEpiSwigluBwd;
     AuxHalf<kWide ? kEpiStore : EPI, NT> aux;
     AuxHalfWide<NT> aux_w;
     if constexpr (kWide) load_aux_half_wide<MODE, NT>(p, t, HALF * kEpRows, aux_w);
@@ -956,7 +997,10 @@ __device__ __forceinline__ void epilogue_pass(const Params& p, const Tile& t, fl
     }
     lds_barrier();
     if constexpr (QF >= 0)
-        epilogue_half_q<MODE, EPI, NT, QF>(p, t, ep, HALF * kEpRows, aux, qa);
+        if constexpr (kWide)
+            epilogue_half_q_swiglu_bwd_wide<MODE, NT, QF>(p, t, ep, HALF * kEpRows, aux_w, qa);
+        else
+            epilogue_half_q<MODE, EPI, NT, QF>(p, t, ep, HALF * kEpRows, aux, qa);
     else if constexpr (kWide)
         epilogue_half_swiglu_bwd_wide<MODE, NT>(p, t, ep, HALF * kEpRows, aux_w);
     else
