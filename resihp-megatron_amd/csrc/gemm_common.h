@@ -337,8 +337,9 @@ template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI =
 // owns X rows [128 (w % 2), +128) and Y rows [64 (w / 2), +64).  The bf16
 // products hold them in 8 x 4 accumulators of v_mfma_f32_16x16x32_bf16 (128
 // registers), the fp8 products in 4 x 2 of the 32x32x64 fp8 MFMA.  (The bf16
-// forward products run the same tile on 4 waves of 128 x 128 outputs, with
-// their accumulators in AGPRs; grouped_gemm.hip says why.)  Under load
+// forward and input-gradient products run the same tile on 4 waves of
+// 128 x 128 outputs, with their accumulators in AGPRs; grouped_gemm.hip says
+// why.)  Under load
 // the GPU runs at its power limit, so energy per step sets the clock: the
 // 16x16x32 shape reads and writes half the accumulator bytes per FLOP of
 // 32x32x16, and with operands in registers sustains 1.9 PFLOP/s against 1.75.
@@ -366,6 +367,7 @@ template <int EPI> __host__ __device__ constexpr int x_per_tile() { return EPI =
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 

@@ -43,17 +43,18 @@ namespace {
 constexpr int kK64 = 64;
 constexpr int kT64Bytes = kTile * kK64 * 2;                // 32 KB per operand tile
 
-// Waves per bf16 tile.  The forward products run on four waves, one per
-// SIMD, each owning 128 x 128 outputs (accumulators in AGPRs): per MFMA they
-// read a third fewer fragment bytes from LDS than eight waves of 128 x 64,
-// and measured on the Mixtral shape fc1 and fc2 forward take 1.7 % and 5.6 %
-// less time (MFMA busy 64-67 % at 1.70-1.85 GHz).  The input- and
-// weight-gradient products keep eight waves, two per SIMD: their transposing
-// LDS reads are twice as many instructions per MFMA, and one wave per SIMD
-// left the MFMAs idle behind them (weight gradients 8.5 % slower, MFMA busy
-// 56 % against 66 %).
+// Waves per bf16 tile.  The forward and input-gradient products run on four
+// waves, one per SIMD, each owning 128 x 128 outputs (accumulators in AGPRs):
+// per MFMA they read a third fewer fragment bytes from LDS than eight waves
+// of 128 x 64.  Measured on the Mixtral shape: fc1 and fc2 forward 1.7 % and
+// 5.6 % less time, fc1 and fc2 input gradients 3.3 % and 1.8 % (K step 2760
+// -> 2650 cycles, with each transposing read in its own MFMA shadow).  The
+// weight-gradient products keep eight waves, two per SIMD: both their
+// operands come through transposing reads, twice the LDS instructions per
+// MFMA, and one wave per SIMD left the MFMAs idle behind them (8.5 % slower,
+// MFMA busy 56 % against 66 %).
 template <int MODE>
-constexpr int bf16_waves() { return MODE == kFwd ? 4 : 8; }
+constexpr int bf16_waves() { return MODE != kWgrad ? 4 : 8; }
 static_assert((kT64Bytes / 1024) % 8 == 0, "whole loads per wave");
 
 template <int NW>
@@ -326,6 +327,19 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
     auto read_x = [&](int set, uint32_t sx, int b, int i) {
         xf[set][i] = kXK ? kfrag(lds + sx, mx.fr[i], b) : frag_mn32(lds + sx, mx.fr[i], b);
     };
+    // Half h of an MN-major X fragment (one transposing read, k rows 8 g + 4 h
+    // .. + 3), for schedules that give each LDS instruction its own MFMA.
+    auto read_x_half = [&](int set, uint32_t sx, int b, int i, int h) {
+        typedef s16x4_t __attribute__((address_space(3))) * lds_v4;
+        const uint8_t* q = lds + sx + mx.fr[i] + b * 32 * 512 + h * 4 * 512;
+        const s16x4_t v =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4>(reinterpret_cast<uintptr_t>(q)));
+        s16x4_t lo = __builtin_shufflevector(__builtin_bit_cast(s16x8_t, xf[set][i]), __builtin_bit_cast(s16x8_t, xf[set][i]), 0, 1, 2, 3);
+        s16x4_t hi = __builtin_shufflevector(__builtin_bit_cast(s16x8_t, xf[set][i]), __builtin_bit_cast(s16x8_t, xf[set][i]), 4, 5, 6, 7);
+        if (h == 0) lo = v;
+        else hi = v;
+        xf[set][i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
     auto read_y = [&](YSet& y, uint32_t sy, int b, int j) {
         y[j] = kYK ? kfrag(lds + sy, my.fr[j], b) : frag_mn32(lds + sy, my.fr[j], b);
     };
@@ -340,7 +354,28 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
     // measured each order.
     auto block = [&](const YSet& yc, YSet& yn, int xc, int xn, uint32_t sx, uint32_t sy, int b, auto load, auto n_c) {
         constexpr int n = decltype(n_c)::value;
-        if constexpr (kXSets == 2) {
+        if constexpr (kXSets == 2 && !kXK) {
+            // Four waves, MN-major X (input gradients): 8 Y reads, 16 transposing
+            // X half-reads and n loads, one memory instruction after every other
+            // MFMA, a load in every fourth place.
+            constexpr int kOps = FY + 16 + n;
+            static_assert(2 * kOps <= 8 * FY && n * 4 <= kOps, "memory instructions fit between the MFMAs");
+#pragma unroll
+            for (int m = 0; m < 8 * FY; ++m) {
+                mfma16<NW>(acc[m / FY][m % FY], xf[xc][m / FY], yc[m % FY]);
+                if (m % 2 == 1 && m / 2 < kOps) {
+                    const int i = m / 2;
+                    if (i % 4 == 3 && i / 4 < n) {
+                        load(i / 4);
+                    } else {
+                        const int r = i - (i / 4 < n ? (i + 1) / 4 : n);
+                        if (r < FY) read_y(yn, sy, b, r);
+                        else read_x_half(xn, sx, b, (r - FY) / 2, (r - FY) % 2);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else if constexpr (kXSets == 2) {
             // Four waves: one memory instruction after every other MFMA, over the first
             // 3 n MFMAs of the block: the 16 fragment reads of the next block (its Y
             // fragments first) and the n loads, one load after every two reads.  Each
@@ -363,13 +398,13 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-        } else if constexpr (MODE == kWgrad) {
+        } else {
             // Eight waves (X single-buffered), weight gradients: in part q, X fragment q of
             // the next block is read after the part's last MFMA (its last use), the next
             // block's Y fragments go in over the first parts and the loads over all parts,
             // each placed after one MFMA (K step 2700 -> 2520 cycles against the grouping by
             // part below, whose LDS reads the compiler clusters between MFMA groups).
-            static_assert(FY == 4 && n <= 8, "eight waves: four Y fragments, at most a load a part");
+            static_assert(MODE == kWgrad && FY == 4 && n <= 8, "eight waves: weight gradients, four Y fragments, at most a load a part");
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
 #pragma unroll
@@ -380,25 +415,6 @@ __device__ __forceinline__ void gg_bf16_tile(const Params& p, Tile t, uint8_t* l
                     if (j == FY - 1) read_x(xn, sx, b, q);
                     __builtin_amdgcn_sched_barrier(0);
                 }
-            }
-        } else {
-            // Eight waves, input gradients: the eight parts of a block, part q being X
-            // fragment q with every Y fragment; the next block's Y fragments are read over
-            // the first four parts, its X fragment q after part q, and the loads spread one or
-            // none a part (placing each read and load after its own MFMA, as the weight
-            // gradients do, measured 0.6-1.2 % slower here).
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                if (q < 4) {
-#pragma unroll
-                    for (int j = FY * q / 4; j < FY * (q + 1) / 4; ++j) read_y(yn, sy, b, j);
-                }
-#pragma unroll
-                for (int j = 0; j < FY; ++j) mfma16<NW>(acc[q][j], xf[xc][q], yc[j]);
-                read_x(xn, sx, b, q);
-#pragma unroll
-                for (int l = n * q / 8; l < n * (q + 1) / 8; ++l) load(l);
-                __builtin_amdgcn_sched_barrier(0);
             }
         }
     };
