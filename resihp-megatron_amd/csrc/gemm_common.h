@@ -494,12 +494,28 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_view(const void* base, in
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p), 0, min(rows, kTile) * ld * 2, 0x00020000);
 }
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void view_store_bf16x4(__amdgpu_buffer_rsrc_t v, uint32_t off, uint32_t soff, float a, float b,
                                                   float c, float d) {
     u32x2_t w;
     w[0] = pack_bf16x2(a, b);
     w[1] = pack_bf16x2(c, d);
     __builtin_amdgcn_raw_buffer_store_b64(w, v, static_cast<int>(off), static_cast<int>(soff), 0);
+}
+// 16-byte buffer stores take their whole offset in the VGPR offset, soffset 0:
+// the compiler keeps a VALU write off a >8-byte store's data registers for the
+// next wait states only when soffset is not a register, and with a register
+// soffset a conversion writing the first data register right after the store
+// changed the stored bytes (seen in the quantising SwiGLU forward).  off may be
+// kOutOfRange; adding an offset below 2^31 keeps it past every view.
+__device__ __forceinline__ void view_store_b128(u32x4v_t w, __amdgpu_buffer_rsrc_t v, uint32_t off, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(w, v, static_cast<int>(off + soff), 0, 0);
+}
+__device__ __forceinline__ void view_store_bf16x8(__amdgpu_buffer_rsrc_t v, uint32_t off, uint32_t soff, const float* x) {
+    u32x4v_t w;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w[q] = pack_bf16x2(x[2 * q], x[2 * q + 1]);
+    view_store_b128(w, v, off, soff);
 }
 __device__ __forceinline__ uint2 view_load_b64(__amdgpu_buffer_rsrc_t v, uint32_t off, uint32_t soff) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(v, static_cast<int>(off), static_cast<int>(soff), 0));
@@ -533,7 +549,6 @@ struct AuxHalf {
 // r0 + t / 32 + (NT / 32) n.  Half the load and store instructions of 4-column
 // pieces: with 256 load instructions a CU, the 8-byte form spent 6 µs issuing
 // them before the half could be staged.
-typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
 template <int NT>
 struct AuxHalfWide {
     static constexpr int kPieces = kEpRows * 32 / NT;
@@ -577,8 +592,8 @@ __device__ __forceinline__ void epilogue_half_swiglu_bwd_wide(const Params& p, c
 #pragma unroll
             for (int q = 0; q < 4; ++q) o[part][q] = pack_bf16x2(v[2 * q] * f[2 * q], v[2 * q + 1] * f[2 * q + 1]);
         }
-        __builtin_amdgcn_raw_buffer_store_b128(o[0], ov, static_cast<int>(off), 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(o[1], ov, static_cast<int>(off), p.f * 2, 0);
+        view_store_b128(o[0], ov, off, 0);
+        view_store_b128(o[1], ov, off, static_cast<uint32_t>(p.f * 2));
     }
 }
 
@@ -667,26 +682,50 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
     }
     if (EPI == kEpiSwigluFwd) {
         // X columns of the tile are [gate 64 | up 64] for each half of 128
-        // activation columns; thread t covers activation columns 4 (t % 32) ..
-        // + 3 of rows r0 + t / 32 + (NT / 32) n.
+        // activation columns; thread t covers activation columns 8 (t % 16) ..
+        // + 7 of rows r0 + t / 16 + (NT / 16) n, in 16-byte stores.
         const __amdgpu_buffer_rsrc_t hv = tile_view(p.c[g], first, p.ldc, t.x0, t.y_lim);
         const __amdgpu_buffer_rsrc_t av = tile_view(p.c2[g], first, p.ldc2, t.x0, t.y_lim);
-        const int rr = threadIdx.x >> 5, a = (threadIdx.x & 31) * 4;
+        const int rr = threadIdx.x >> 4, a = (threadIdx.x & 15) * 8;
         const int xg = (a >> 6) * 128 + (a & 63);
         const bool ok = a < t.x_lim;
         uint32_t oh = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc + a) * 2) : kOutOfRange;
         uint32_t oa = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc2 + a) * 2) : kOutOfRange;
-        const uint32_t sh = static_cast<uint32_t>((NT / 32) * p.ldc * 2), sa = static_cast<uint32_t>((NT / 32) * p.ldc2 * 2);
+        const uint32_t sh = static_cast<uint32_t>((NT / 16) * p.ldc * 2), sa = static_cast<uint32_t>((NT / 16) * p.ldc2 * 2);
         const uint32_t up = static_cast<uint32_t>(p.f * 2);
 #pragma unroll
-        for (int n = 0; n < kEpRows * 32 / NT; ++n, oh += sh, oa += sa) {
+        for (int n = 0; n < kEpRows * 16 / NT; ++n, oh += sh, oa += sa) {
+            const int r = rr + n * (NT / 16);
+            const float4 g0 = lds_f4(ep, r, xg), g1 = lds_f4(ep, r, xg + 4);
+            const float4 u0 = lds_f4(ep, r, xg + 64), u1 = lds_f4(ep, r, xg + 68);
+            const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            float fg[8], fu[8], act[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const SwigluOut o = swiglu_fwd(gv[e], uv[e]);
+                fg[e] = o.fg;
+                fu[e] = o.fu;
+                act[e] = o.act;
+            }
+            view_store_bf16x8(hv, oh, 0, fg);
+            view_store_bf16x8(hv, oh, up, fu);
+            view_store_bf16x8(av, oa, 0, act);
+        }
+        return;
+    }
+    if constexpr (EPI == kEpiStore) {
+        // Thread t covers columns 8 (t % 32) .. + 7 of rows r0 + t / 32 + (NT / 32) n, in 16-byte stores.
+        const __amdgpu_buffer_rsrc_t ov = tile_view(p.c[g], first, p.ldc, t.x0, t.y_lim);
+        const int rr = threadIdx.x >> 5, x = (threadIdx.x & 31) * 8;
+        uint32_t off = x < t.x_lim ? static_cast<uint32_t>(((r0 + rr) * p.ldc + x) * 2) : kOutOfRange;
+        const uint32_t step = static_cast<uint32_t>((NT / 32) * p.ldc * 2);
+#pragma unroll
+        for (int n = 0; n < kEpRows * 32 / NT; ++n, off += step) {
             const int r = rr + n * (NT / 32);
-            const float4 gv = lds_f4(ep, r, xg), uv = lds_f4(ep, r, xg + 64);
-            const SwigluOut o0 = swiglu_fwd(gv.x, uv.x), o1 = swiglu_fwd(gv.y, uv.y), o2 = swiglu_fwd(gv.z, uv.z),
-                            o3 = swiglu_fwd(gv.w, uv.w);
-            view_store_bf16x4(hv, oh, 0, o0.fg, o1.fg, o2.fg, o3.fg);
-            view_store_bf16x4(hv, oh, up, o0.fu, o1.fu, o2.fu, o3.fu);
-            view_store_bf16x4(av, oa, 0, o0.act, o1.act, o2.act, o3.act);
+            const float4 a = lds_f4(ep, r, x), b = lds_f4(ep, r, x + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            view_store_bf16x8(ov, off, 0, v);
         }
         return;
     }
@@ -823,27 +862,41 @@ __device__ __forceinline__ void epilogue_half_q(const Params& p, const Tile& t, 
     const int64_t first = tile_first_row<MODE>(t);
     const __amdgpu_buffer_rsrc_t qv = code_view(p.q, first, p.q_ld, t.x0, t.y_lim);
     if constexpr (EPI == kEpiSwigluFwd) {
-        // Thread t covers activation columns 4 (t % 32) .. + 3 of rows r0 + t / 32 + (NT / 32) n.
-        constexpr int kW = 32, kN = kEpRows * 32 / NT;
+        // Thread t covers activation columns 8 (t % 16) .. + 7 of rows r0 + t / 16 + (NT / 16) n:
+        // 16-byte factor stores and one 8-byte code store a row.
+        constexpr int kW = 32, kN = kEpRows * 16 / NT;
         const __amdgpu_buffer_rsrc_t hv = tile_view(p.c[g], first, p.ldc, t.x0, t.y_lim);
-        const int rr = threadIdx.x >> 5, a = (threadIdx.x & 31) * 4;
+        const int rr = threadIdx.x >> 4, a = (threadIdx.x & 15) * 8;
         const int xg = (a >> 6) * 128 + (a & 63);
         const bool ok = a < t.x_lim;
         uint32_t oh = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc + a) * 2) : kOutOfRange;
         uint32_t oq = ok ? static_cast<uint32_t>((r0 + rr) * p.q_ld + a) : kOutOfRange;
-        const uint32_t sh = static_cast<uint32_t>((NT / 32) * p.ldc * 2), sq = static_cast<uint32_t>((NT / 32) * p.q_ld);
+        const uint32_t sh = static_cast<uint32_t>((NT / 16) * p.ldc * 2), sq = static_cast<uint32_t>((NT / 16) * p.q_ld);
         const uint32_t up = static_cast<uint32_t>(p.f * 2);
 #pragma unroll
         for (int n = 0; n < kN; ++n, oh += sh, oq += sq) {
-            const int r = rr + n * (NT / 32);
-            const float4 gv = lds_f4(ep, r, xg), uv = lds_f4(ep, r, xg + 64);
-            const SwigluOut o0 = swiglu_fwd(gv.x, uv.x), o1 = swiglu_fwd(gv.y, uv.y), o2 = swiglu_fwd(gv.z, uv.z),
-                            o3 = swiglu_fwd(gv.w, uv.w);
-            view_store_bf16x4(hv, oh, 0, o0.fg, o1.fg, o2.fg, o3.fg);
-            view_store_bf16x4(hv, oh, up, o0.fu, o1.fu, o2.fu, o3.fu);
-            const uint32_t code = quant4<QF>(o0.act, o1.act, o2.act, o3.act, ok && r0 + r < t.y_lim, qa);
-            __builtin_amdgcn_raw_buffer_store_b32(code, qv, static_cast<int>(oq), 0, 0);
-            if (p.qt) ep[code_word(r, threadIdx.x & 31)] = __uint_as_float(code);
+            const int r = rr + n * (NT / 16);
+            const float4 g0 = lds_f4(ep, r, xg), g1 = lds_f4(ep, r, xg + 4);
+            const float4 u0 = lds_f4(ep, r, xg + 64), u1 = lds_f4(ep, r, xg + 68);
+            const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            float fg[8], fu[8], act[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const SwigluOut o = swiglu_fwd(gv[e], uv[e]);
+                fg[e] = o.fg;
+                fu[e] = o.fu;
+                act[e] = o.act;
+            }
+            view_store_bf16x8(hv, oh, 0, fg);
+            view_store_bf16x8(hv, oh, up, fu);
+            const bool valid = ok && r0 + r < t.y_lim;
+            u32x2_t w;
+            w[0] = quant4<QF>(act[0], act[1], act[2], act[3], valid, qa);
+            w[1] = quant4<QF>(act[4], act[5], act[6], act[7], valid, qa);
+            __builtin_amdgcn_raw_buffer_store_b64(w, qv, static_cast<int>(oq), 0, 0);
+            if (p.qt)
+                *reinterpret_cast<uint2*>(&ep[code_word(r, 2 * (threadIdx.x & 15))]) = make_uint2(w[0], w[1]);
         }
         if (p.qt) {   // the transposed copy (uniform: every wave takes the same branch)
             lds_barrier();
