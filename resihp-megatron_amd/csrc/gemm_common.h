@@ -613,30 +613,44 @@ __device__ __forceinline__ void load_aux_half(const Params& p, const Tile& t, in
 }
 
 // Rows [r0, r0 + 128) of the tile, staged in ep.  Thread t of NT handles
-// 4-column pieces t, t + NT, ...; a wave covers one row (or two rows of 128
-// columns).  Stores go through views of the tile's valid rows, so that a
-// piece's address is one add from the previous one's and pieces of rows past
-// the tile drop out in the memory unit.
-// Destination rows of a half under a scatter map: lane n of a wave holds the
-// c_idx row of the wave's n-th row of the half (rows r0 + wave + (NT / 64) n),
-// or -1 past the tile's valid rows.
+// 4-column pieces t, t + NT, ... (8-column pieces where the epilogue says so);
+// a wave covers whole row segments.  Stores go through views of the tile's
+// valid rows, so that a piece's address is one add from the previous one's
+// and pieces of rows past the tile drop out in the memory unit.
+//
+// Per-row values of the 8-column row-map epilogues: thread t covers rows
+// t / 32 + (NT / 32) n of the half, so wave w covers rows 2 w + h + (NT / 32) n
+// (h = lane / 32); lane j of the wave holds the value of row
+// 2 w + (j & 1) + (NT / 32) (j / 2), and piece n of lane l reads lane
+// 2 n + l / 32.
+template <int NT>
+__device__ __forceinline__ int wide_row_of_lane(int r0) {
+    const int lane = threadIdx.x & 63;
+    return r0 + 2 * static_cast<int>(threadIdx.x >> 6) + (lane & 1) + (NT / 32) * (lane >> 1);
+}
+template <class T>
+__device__ __forceinline__ T wide_row_value(T v, int n) {
+    return __shfl(v, 2 * n + static_cast<int>((threadIdx.x & 63) >> 5));
+}
+
+// Destination rows of a half under a scatter map (c_idx), -1 past the tile's
+// valid rows, in the lanes as above.
 template <int NT>
 __device__ __forceinline__ int32_t scatter_rows_half(const Params& p, const Tile& t, int r0) {
-    constexpr int kN = kEpRows * 64 / NT;
-    const int lane = threadIdx.x & 63, r = r0 + (threadIdx.x >> 6) + (NT / 64) * lane;
-    if (lane >= kN || r >= t.y_lim) return -1;
+    constexpr int kN = kEpRows * 32 / NT;
+    const int lane = threadIdx.x & 63, r = wide_row_of_lane<NT>(r0);
+    if (lane >= 2 * kN || r >= t.y_lim) return -1;
     const int32_t d = p.c_idx[t.row0 + t.y0 + r];
     return d >= 0 && d < p.c_rows ? d : -1;
 }
 
-// The router term's row factors of a half: lane n of a wave holds
-// rdl[rperm[row]] of the wave's n-th row (rows r0 + wave + (NT / 64) n), 0 past
-// the tile's valid rows.
+// The router term's row factors of a half, rdl[rperm[row]], 0 past the tile's
+// valid rows, in the lanes as above.
 template <int NT>
 __device__ __forceinline__ float router_scale_half(const Params& p, const Tile& t, int r0) {
-    constexpr int kN = kEpRows * 64 / NT;
-    const int lane = threadIdx.x & 63, r = r0 + (threadIdx.x >> 6) + (NT / 64) * lane;
-    if (lane >= kN || r >= t.y_lim) return 0.0f;
+    constexpr int kN = kEpRows * 32 / NT;
+    const int lane = threadIdx.x & 63, r = wide_row_of_lane<NT>(r0);
+    if (lane >= 2 * kN || r >= t.y_lim) return 0.0f;
     return p.rdl[p.rperm[t.row0 + t.y0 + r]];
 }
 
@@ -646,36 +660,46 @@ __device__ __forceinline__ void epilogue_half(const Params& p, const Tile& t, co
     const int g = t.g;
     const int64_t first = tile_first_row<MODE>(t);
     if constexpr (EPI == kEpiStoreRouter) {
-        // Plain store plus the router term: dst_rows carries the rows' logit gradients (lane n: the
-        // wave's n-th row), the router row's four columns of this thread are loaded once.
+        // Plain store plus the router term, in 8-column pieces: dst_rows carries the rows' logit
+        // gradients (wide_row_value), the router row's eight columns of this thread are loaded once.
         const __amdgpu_buffer_rsrc_t ov = tile_view(p.c[g], first, p.ldc, t.x0, t.y_lim);
-        const int rr = threadIdx.x >> 6, x = (threadIdx.x & 63) * 4;
+        const int rr = threadIdx.x >> 5, x = (threadIdx.x & 31) * 8;
         const bool ok = x < t.x_lim;
-        const float4 w = ok ? *reinterpret_cast<const float4*>(p.rw + static_cast<int64_t>(p.rw_e0 + g) * p.N + t.x0 + x)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float* wr = p.rw + static_cast<int64_t>(p.rw_e0 + g) * p.N + t.x0 + x;
+        const float4 w0 = ok ? *reinterpret_cast<const float4*>(wr) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 w1 = ok ? *reinterpret_cast<const float4*>(wr + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
         uint32_t off = ok ? static_cast<uint32_t>(((r0 + rr) * p.ldc + x) * 2) : kOutOfRange;
-        const uint32_t step = static_cast<uint32_t>((NT / 64) * p.ldc * 2);
+        const uint32_t step = static_cast<uint32_t>((NT / 32) * p.ldc * 2);
 #pragma unroll
-        for (int n = 0; n < kEpRows * 64 / NT; ++n, off += step) {
-            const float d = __int_as_float(__builtin_amdgcn_readlane(dst_rows, n));
-            const float4 v = lds_f4(ep, rr + n * (NT / 64), x);
-            view_store_bf16x4(ov, off, 0, v.x + d * w.x, v.y + d * w.y, v.z + d * w.z, v.w + d * w.w);
+        for (int n = 0; n < kEpRows * 32 / NT; ++n, off += step) {
+            const float d = __int_as_float(wide_row_value(dst_rows, n));
+            const int r = rr + n * (NT / 32);
+            const float4 a = lds_f4(ep, r, x), b = lds_f4(ep, r, x + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = v[e] + d * w[e];
+            view_store_bf16x8(ov, off, 0, o);
         }
         return;
     }
     if constexpr (MAP && EPI == kEpiStore) {
         if (p.c_idx != nullptr) {
-            // Scattered rows: the view spans the whole output; each row's offset comes from the map.
+            // Scattered rows, in 8-column pieces: the view spans the whole output; each row's offset
+            // comes from the map (wide_row_value).
             const __amdgpu_buffer_rsrc_t ov = __builtin_amdgcn_make_buffer_rsrc(
                 p.c[g], 0, static_cast<int>(p.c_rows * p.ldc * 2), 0x00020000);
-            const int x = (threadIdx.x & 63) * 4;
+            const int rr = threadIdx.x >> 5, x = (threadIdx.x & 31) * 8;
             const bool ok = x < t.x_lim;
 #pragma unroll
-            for (int n = 0; n < kEpRows * 64 / NT; ++n) {
-                const int32_t d = __builtin_amdgcn_readlane(dst_rows, n);
+            for (int n = 0; n < kEpRows * 32 / NT; ++n) {
+                const int32_t d = wide_row_value(dst_rows, n);
                 const uint32_t off = ok && d >= 0 ? static_cast<uint32_t>((d * p.ldc + t.x0 + x) * 2) : kOutOfRange;
-                const float4 v = lds_f4(ep, (threadIdx.x >> 6) + n * (NT / 64), x);
-                view_store_bf16x4(ov, off, 0, v.x, v.y, v.z, v.w);
+                const int r = rr + n * (NT / 32);
+                const float4 a = lds_f4(ep, r, x), b = lds_f4(ep, r, x + 4);
+                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                view_store_bf16x8(ov, off, 0, v);
             }
             return;
         }
