@@ -28,6 +28,7 @@ CPU baseline: the float64/float32 torch restatement of the reference layer
 from __future__ import annotations
 
 import argparse
+import ctypes
 import importlib.util
 import json
 import os
@@ -71,20 +72,55 @@ def _package():
     return mod
 
 
+class _HipEvent:
+    """A HIP timing event created with hipEventDisableSystemFence: recording it takes a timestamp without
+    the system-scope release (L2 write-back) a default event performs, which left about 10 us between
+    the launches around it.  Only timestamps are read from these events."""
+
+    _lib = None
+    DISABLE_SYSTEM_FENCE = 0x20000000   # hipEventDisableSystemFence
+
+    def __init__(self):
+        if _HipEvent._lib is None:
+            lib = ctypes.CDLL("libamdhip64.so")
+            lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+            lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            _HipEvent._lib = lib
+        self.ev = ctypes.c_void_p()
+        if _HipEvent._lib.hipEventCreateWithFlags(ctypes.byref(self.ev), self.DISABLE_SYSTEM_FENCE) != 0:
+            raise RuntimeError("hipEventCreateWithFlags failed")
+
+    def record(self, stream):
+        if _HipEvent._lib.hipEventRecord(self.ev, ctypes.c_void_p(stream.cuda_stream)) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_time(self, end) -> float:
+        ms = ctypes.c_float()
+        if _HipEvent._lib.hipEventElapsedTime(ctypes.byref(ms), self.ev, end.ev) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def __del__(self):
+        if _HipEvent._lib is not None and self.ev:
+            _HipEvent._lib.hipEventDestroy(self.ev)
+
+
 class EventTimer:
     """HIP events around every C-ABI call, on the stream the call enqueues on."""
 
     def __init__(self):
         self.pending: dict[str, list] = {}
-        self.pairs: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
+        self.pairs: list[tuple[str, _HipEvent, _HipEvent]] = []
 
     def start(self, name, stream):
-        ev = torch.cuda.Event(enable_timing=True)
+        ev = _HipEvent()
         ev.record(stream)
         self.pending.setdefault(name, []).append(ev)
 
     def stop(self, name, stream):
-        ev = torch.cuda.Event(enable_timing=True)
+        ev = _HipEvent()
         ev.record(stream)
         self.pairs.append((name, self.pending[name].pop(), ev))
 
