@@ -291,6 +291,19 @@ class _MoELayerFn(torch.autograd.Function):
         else:   # the fp8 products read only the codes of the rows' gradient
             dy, dgates = fp8.combine_bwd(DY, dout, y, gates, pair_row, P)
         dl = K.route_bwd(dgates, gates, logits, topi, meta.score, meta.normalize, meta.gate_scale)
+        dwr = None
+        if ctx.needs_input_grad[3]:
+            # The router's weight gradient needs only dl and x: on the side stream, beside the expert
+            # products, instead of an HBM-bound pass that ends the backward on its own.
+            side = _side_stream(x.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                if meta.full:
+                    rperm, roff = perm, offsets
+                else:
+                    full_plan = K.dispatch(topi, meta.num_experts)
+                    rperm, roff = full_plan.perm, full_plan.offsets
+                dwr = K.router_wgrad(dl, rperm, roff, x, meta.num_experts, router_w.dtype)
         # With every expert local each routed slot has a row, so fc1's input-gradient product can add the
         # router term to its rows (the token backward then sums it with the rows).
         fold = (need_x and meta.full and ctx.fp8[0] is None and P > 0 and x.dtype != torch.float64
@@ -314,14 +327,9 @@ class _MoELayerFn(torch.autograd.Function):
         if shared_side:
             main.wait_stream(_side_stream(x.device))
         dx = K.token_bwd(dout, dxp, pair_row, None if fold else dl, topi, router_w, shared_dx) if need_x else None
-        dwr = None
-        if ctx.needs_input_grad[3]:
-            if meta.full:
-                rperm, roff = perm, offsets
-            else:
-                full_plan = K.dispatch(topi, meta.num_experts)
-                rperm, roff = full_plan.perm, full_plan.offsets
-            dwr = K.router_wgrad(dl, rperm, roff, x, meta.num_experts, router_w.dtype)
+        if dwr is not None:
+            main.wait_stream(_side_stream(x.device))
+            dwr.record_stream(main)   # made on the side stream, used on the caller's
         return (None, None, dx, dwr, None, *dw1, *dw2, *sdw1, *sdw2)
 
 
