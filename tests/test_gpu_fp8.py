@@ -253,6 +253,14 @@ def test_fused_cast_edge_rows(act):
     _fused_case(act, 3.0, 0, 384, 640, [1, 255, 0, 256, 257, 513])
 
 
+def test_fused_cast_many_tiles():
+    """About 2300 tiles a product (7300 rows, h = 1024, f = 2048): every epilogue store of the fused
+    products, factors and codes alike, bit for bit against the unfused pair.  A 16-byte store whose data
+    registers were overwritten right after it (register soffset, no wait states) changed 64 of 483,072
+    stored values in a 12-tile product; this one has 40 times the tiles."""
+    _fused_case("swiglu", 3.0, 0, 1024, 2048, [2048, 1537, 0, 3000, 700])
+
+
 def _fused_case(act, hist_scale, margin, h, f, counts):
     G, P = len(counts), sum(counts)
     F1 = 2 * f if act == "swiglu" else f
